@@ -1,0 +1,159 @@
+/*
+ * mw8.h -- C ABI of the MI355X-native W8A8 int8 linear + fused-MoE library
+ * (libmw8.so, built for gfx950 with hipcc).
+ *
+ * Every entry point is asynchronous on the given HIP stream (pass
+ * torch.cuda.current_stream().cuda_stream, or 0 for the null stream),
+ * never synchronizes, never allocates device memory and is safe to capture
+ * in a HIP graph.  The caller owns every buffer; pointers are device
+ * pointers, tensors are row-major with the last dimension contiguous.
+ *
+ * Return value: 0 on success, a nonzero MW8_ERR_* code otherwise; the
+ * message of the last failure on the calling thread is returned by
+ * mw8_last_error().  No C++ exception crosses this boundary.
+ *
+ * Numerics (checked bit-exactly against the CPU oracle):
+ *   quantizer   s[m] = amax_k|x[m,k]| / 127 (fp32 IEEE division),
+ *               q[m,k] = clamp(rint(x[m,k] / s[m]), -127, 127), zero row -> s = 0, q = 0
+ *   GEMM        acc[m,n] = sum_k A[m,k] * W[n,k]   (exact int32)
+ *   epilogue    y[m,n] = bf16_rne(((float)acc * sa[m]) * sw[n] [+ bias[n]] [* routed])
+ *               each operation rounded separately (no FMA contraction)
+ */
+#ifndef MW8_H_
+#define MW8_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mw8_stream_t; /* hipStream_t */
+
+enum {
+  MW8_OK = 0,
+  MW8_ERR_ARG = 1,       /* null pointer or bad enum */
+  MW8_ERR_SHAPE = 2,     /* unsupported or inconsistent sizes */
+  MW8_ERR_ALIGN = 3,     /* pointer / leading dimension misaligned */
+  MW8_ERR_WORKSPACE = 4, /* workspace missing or too small */
+  MW8_ERR_LAUNCH = 5     /* HIP launch failure */
+};
+
+/* Message of the last failure on this thread ("" if none). */
+const char* mw8_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int mw8_version(void);
+
+/*
+ * Per-token dynamic int8 quantizer: x bf16 [M, K] (row stride ldx elements)
+ * -> q int8 [M, K] (row stride ldq) and s fp32 [M].
+ * No reference counterpart: it is inserted before the reference's
+ * F.linear (python/minisgl/layers/linear.py:32) and before both grouped
+ * GEMMs of fused_experts_impl (python/minisgl/moe/fused.py:192,208).
+ */
+int mw8_quant_per_token_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q,
+                             int64_t ldq, float* s, mw8_stream_t stream);
+
+/*
+ * Fused activation + requant: x bf16 [R, 2d] (gate | up) ->
+ * a = bf16(act(gate) * up), then quantized like mw8_quant_per_token_bf16 into
+ * q int8 [R, d], s fp32 [R].  act: 0 = silu, 1 = gelu (erf).  act_out
+ * (bf16 [R, d]) is optional and receives a.  2d % 16 == 0.
+ * Replaces silu_and_mul / gelu_and_mul (python/minisgl/layers/activation.py:9-18)
+ * as called at python/minisgl/moe/fused.py:206-207 and
+ * python/minisgl/models/utils.py:48, fused with the requant of the next GEMM.
+ */
+int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t act, int8_t* q,
+                               float* s, void* act_out, mw8_stream_t stream);
+
+/*
+ * Bytes of workspace mw8_gemm_w8a8_* needs for (M, N, K); 0 if none.
+ * The workspace must be zero-filled once when allocated; every call leaves
+ * its arrival counters at zero again.  Calls that share one workspace must
+ * be ordered (same stream).
+ */
+size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * W8A8 linear: y bf16 [M, N] = epilogue(A int8 [M, K] . W int8 [N, K]^T,
+ * sa fp32 [M], sw fp32 [N], bias bf16 [N] or NULL).  K % 16 == 0,
+ * A and W 16-byte aligned.
+ * Replaces _LinearTPImpl.forward -> F.linear(x, weight, bias)
+ * (python/minisgl/layers/linear.py:31-32, also :103 and :124).
+ */
+int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                       const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* workspace,
+                       size_t workspace_bytes, mw8_stream_t stream);
+
+/*
+ * Same GEMM, raw int32 accumulators acc [M, N] (parity hook; no scales).
+ * Test hook for the A4 int32 contract; no reference counterpart.
+ */
+int mw8_gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int64_t N,
+                      int64_t K, void* workspace, size_t workspace_bytes, mw8_stream_t stream);
+
+/*
+ * Router: logits [M, E] (bf16 if logits_is_bf16 else fp32) -> fp32 softmax,
+ * top-k, optional renormalisation (w / sum w, then w / (sum w + 1e-8)).
+ * topk_w fp32 [M, topk], topk_ids int32 [M, topk].  E <= 1024, topk <= 64.
+ * Replaces fused_topk -> sgl_kernel.topk_softmax (python/minisgl/moe/fused.py:9-28).
+ */
+int mw8_topk_softmax(const void* logits, int32_t logits_is_bf16, int64_t M, int32_t E,
+                     int32_t topk, int32_t renormalize, float* topk_w, int32_t* topk_ids,
+                     mw8_stream_t stream);
+
+/* numel + slots * (block - 1): length of sorted_ids (python/minisgl/moe/fused.py:73). */
+int64_t mw8_moe_align_max_padded(int64_t numel, int32_t slots, int32_t block_size);
+
+/*
+ * Expert alignment: topk_ids int32 [numel] -> sorted_ids int32
+ * [mw8_moe_align_max_padded(...)] (pairs grouped by expert in ascending flat
+ * order, each group padded to a multiple of block_size with the sentinel
+ * numel), expert_ids int32 [ceil(max_padded / block_size)] (-1 past the
+ * used blocks), num_post_pad int32 [1].  Ids outside [0, slots) are skipped.
+ * slots <= 512.  The count stays on the device.
+ * Replaces moe_align_block_size -> sgl_kernel.moe_align_block_size
+ * (python/minisgl/moe/fused.py:31-89; the reference passes slots = E + 1, :81).
+ */
+int mw8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int32_t slots,
+                             int32_t block_size, int32_t* sorted_ids, int32_t* expert_ids,
+                             int32_t* num_post_pad, mw8_stream_t stream);
+
+/*
+ * Grouped W8A8 GEMM over expert segments.  For every sorted position r
+ * below *num_post_pad with p = sorted_ids[r] < num_valid:
+ *   out[p, :] = epilogue(A[p / top_k] . W[e]^T, sa[p / top_k], sw[e], routed = topk_w[p])
+ * where e = expert_ids[r / block_size]; topk_w may be NULL (no routed
+ * multiply).  A int8 [*, K], W int8 [E, N, K], sw fp32 [E, N], out bf16
+ * [num_valid, N].  block_size in {16, 64, 128}.
+ * Replaces fused_moe_kernel_triton / fused_moe_kernel
+ * (python/minisgl/kernel/moe_impl.py:6-62, python/minisgl/kernel/triton/fused_moe.py:50-193).
+ */
+int mw8_moe_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                           const int32_t* sorted_ids, const int32_t* expert_ids,
+                           const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
+                           int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
+                           int32_t block_size, void* out, mw8_stream_t stream);
+
+/* Same, raw int32 accumulators out [num_valid, N] (parity hook; no reference counterpart). */
+int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorted_ids,
+                          const int32_t* expert_ids, const int32_t* num_post_pad,
+                          int64_t max_sorted, int32_t top_k, int64_t num_valid, int64_t N,
+                          int64_t K, int32_t E, int32_t block_size, int32_t* out,
+                          mw8_stream_t stream);
+
+/*
+ * Slot sum: in bf16 [M, k, H] -> out bf16 [M, H], fp32 sum in slot order.
+ * H % 8 == 0.  Replaces moe_sum_reduce_triton
+ * (python/minisgl/kernel/moe_impl.py:65-98, python/minisgl/kernel/triton/fused_moe.py:5-47).
+ */
+int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, void* out,
+                            mw8_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MW8_H_ */

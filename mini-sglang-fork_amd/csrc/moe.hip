@@ -1,0 +1,303 @@
+// Fused-MoE building blocks (gfx950): router top-k softmax, expert
+// alignment (stable counting sort with block padding), grouped W8A8 GEMM
+// over expert segments, and the top-k slot sum.
+#include "gemm_kernels.h"
+
+namespace mw8 {
+
+void launch_grouped_tile_bf16(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
+void launch_grouped_tile_i32(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
+
+namespace {
+
+// ------------------------------------------------------------------ top-k
+// One wave per token.  Softmax in fp32 over E logits (bf16 or fp32 input),
+// then k rounds of a wave arg-max (larger value wins, lower expert index
+// wins ties), then the two renormalisations of the reference
+// (python/minisgl/moe/fused.py:22-24).
+template <int VPL>
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, int is_bf16,
+                                                           int64_t M, int E, int topk,
+                                                           int renorm, float* __restrict__ tw,
+                                                           int32_t* __restrict__ tid_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;
+  float v[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      v[j] = is_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(logits)[t * E + e])
+                     : static_cast<const float*>(logits)[t * E + e];
+    } else {
+      v[j] = -__builtin_huge_valf();
+    }
+  }
+  float mx = v[0];
+#pragma unroll
+  for (int j = 1; j < VPL; ++j) mx = fmaxf(mx, v[j]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    v[j] = (lane + 64 * j < E) ? expf(v[j] - mx) : 0.0f;
+    sum += v[j];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) v[j] = (lane + 64 * j < E) ? v[j] / sum : -1.0f;
+
+  float w_sel = 0.0f;  // lane i keeps the i-th selected weight / id
+  int id_sel = 0;
+  for (int i = 0; i < topk; ++i) {
+    float bv = v[0];
+    int bi = lane;
+#pragma unroll
+    for (int j = 1; j < VPL; ++j)
+      if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == i) { w_sel = bv; id_sel = bi; }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (lane + 64 * j == bi) v[j] = -1.0f;
+  }
+  if (renorm) {
+    float s1 = 0.0f;
+    for (int i = 0; i < topk; ++i) s1 += __shfl(w_sel, i, 64);
+    w_sel = w_sel / s1;
+    float s2 = 0.0f;
+    for (int i = 0; i < topk; ++i) s2 += __shfl(w_sel, i, 64);
+    w_sel = w_sel / (s2 + 1e-8f);
+  }
+  if (lane < topk) {
+    tw[t * topk + lane] = w_sel;
+    tid_out[t * topk + lane] = id_sel;
+  }
+}
+
+// ------------------------------------------------------------ alignment
+// Single 1024-thread block.  Counts per expert slot, exclusive scan of the
+// block-padded counts, sentinel fill, then a stable scatter: pairs are
+// visited in chunks of 1024 flat indices; within a wave, lanes holding the
+// same expert are found with a bitwise ballot match, their rank is the
+// popcount of lower matching lanes; across waves and chunks prefix counts
+// come from LDS.  Segment order is therefore ascending flat index.
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / 64;
+constexpr int kAlignMaxSlots = 512;
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int slots, int bsz,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks, int nbits) {
+  __shared__ int cnt[kAlignMaxSlots];
+  __shared__ int off[kAlignMaxSlots];
+  __shared__ int run[kAlignMaxSlots];
+  __shared__ int wcnt[kAlignWaves][kAlignMaxSlots];
+  __shared__ int wave_tot[kAlignWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int e = tid; e < slots; e += kAlignThreads) { cnt[e] = 0; run[e] = 0; }
+  __syncthreads();
+  for (int64_t i = tid; i < numel; i += kAlignThreads) {
+    const int e = ids[i];
+    if (e >= 0 && e < slots) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+
+  // exclusive scan of padded counts (slots <= 1024: one per thread)
+  int padded = 0;
+  if (tid < slots) padded = ((cnt[tid] + bsz - 1) / bsz) * bsz;
+  int x = padded;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+  if (tid < slots) off[tid] = base + x - padded;
+  int total = 0;
+  for (int w = 0; w < kAlignWaves; ++w) total += wave_tot[w];
+  __syncthreads();
+  if (tid == 0) *npp = total;
+
+  for (int64_t i = tid; i < max_padded; i += kAlignThreads) sorted_ids[i] = static_cast<int32_t>(numel);
+  for (int64_t b = static_cast<int64_t>(total) / bsz + tid; b < max_blocks; b += kAlignThreads) expert_ids[b] = -1;
+  if (tid < slots && padded > 0)
+    for (int b = off[tid] / bsz; b < (off[tid] + padded) / bsz; ++b) expert_ids[b] = tid;
+  __syncthreads();
+
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base_i = 0; base_i < numel; base_i += kAlignThreads) {
+    for (int j = tid; j < kAlignWaves * slots; j += kAlignThreads) (&wcnt[0][0])[(j / slots) * kAlignMaxSlots + j % slots] = 0;
+    __syncthreads();
+    const int64_t i = base_i + tid;
+    const int e = i < numel ? ids[i] : -1;
+    const bool valid = e >= 0 && e < slots;
+    uint64_t m = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t bb = __ballot((e >> b) & 1);
+      m &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    const int rank = __popcll(m & below);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(m);
+    __syncthreads();
+    if (valid) {
+      int pre = 0;
+      for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
+      sorted_ids[off[e] + run[e] + pre + rank] = static_cast<int32_t>(i);
+    }
+    __syncthreads();
+    for (int s = tid; s < slots; s += kAlignThreads) {
+      int add = 0;
+      for (int w = 0; w < kAlignWaves; ++w) add += wcnt[w][s];
+      run[s] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------ slot sum
+// out[t, h] = bf16(sum_i in[t, i, h]) in fp32, slot order i = 0..k-1
+// (python/minisgl/kernel/triton/fused_moe.py:36-47); 8 columns per thread.
+__global__ __launch_bounds__(256) void moe_sum_reduce_kernel(const uint16_t* __restrict__ in,
+                                                             int64_t M, int k, int64_t H,
+                                                             uint16_t* __restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t hv = H >> 3;
+  if (idx >= M * hv) return;
+  const int64_t t = idx / hv, h = (idx % hv) * 8;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  for (int i = 0; i < k; ++i) {
+    const v4i raw = *reinterpret_cast<const v4i*>(in + (t * k + i) * H + h);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = static_cast<uint32_t>(raw[j]);
+      acc[2 * j] = acc[2 * j] + bf16_to_f32(static_cast<uint16_t>(u & 0xFFFFu));
+      acc[2 * j + 1] = acc[2 * j + 1] + bf16_to_f32(static_cast<uint16_t>(u >> 16));
+    }
+  }
+  v4i o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[2 * j])) |
+                            (static_cast<uint32_t>(f32_to_bf16(acc[2 * j + 1])) << 16));
+  *reinterpret_cast<v4i*>(out + t * H + h) = o;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int VPL>
+void launch_topk(const void* lg, int is_bf16, int64_t M, int E, int k, int renorm, float* tw,
+                 int32_t* ti, hipStream_t st) {
+  hipLaunchKernelGGL((topk_softmax_kernel<VPL>), dim3(static_cast<unsigned>((M + 3) / 4)),
+                     dim3(256), 0, st, lg, is_bf16, M, E, k, renorm, tw, ti);
+}
+
+}  // namespace
+
+int topk_softmax(const void* logits, int is_bf16, int64_t M, int E, int topk, int renorm,
+                 float* topk_w, int32_t* topk_ids, hipStream_t st) {
+  MW8_REQUIRE(logits && topk_w && topk_ids, kErrArg, "topk_softmax: null pointer");
+  MW8_REQUIRE(E > 0 && E <= 1024 && topk > 0 && topk <= E && topk <= 64, kErrShape,
+              "topk_softmax: need 0 < topk <= min(E, 64), E <= 1024 (E=%d topk=%d)", E, topk);
+  if (M <= 0) return kOk;
+  MW8_REQUIRE(M < (1ll << 32), kErrShape, "topk_softmax: too many tokens");
+  const int vpl = (E + 63) / 64;
+  if (vpl <= 1) launch_topk<1>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
+  else if (vpl <= 2) launch_topk<2>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
+  else if (vpl <= 4) launch_topk<4>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
+  else if (vpl <= 8) launch_topk<8>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
+  else launch_topk<16>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
+  return check_launch("topk_softmax");
+}
+
+int64_t moe_align_max_padded(int64_t numel, int slots, int bsz) {
+  return numel + static_cast<int64_t>(slots) * (bsz - 1);
+}
+
+int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int slots, int bsz,
+                         int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp,
+                         hipStream_t st) {
+  MW8_REQUIRE(topk_ids && sorted_ids && expert_ids && npp, kErrArg, "moe_align: null pointer");
+  MW8_REQUIRE(slots > 0 && slots <= kAlignMaxSlots && bsz > 0 && bsz <= 4096, kErrShape,
+              "moe_align: need 0 < slots <= 512 and 0 < block <= 4096 (slots=%d block=%d)", slots,
+              bsz);
+  MW8_REQUIRE(numel >= 0 && numel < (1ll << 31) - static_cast<int64_t>(slots) * bsz, kErrShape,
+              "moe_align: too many pairs");
+  const int64_t max_padded = moe_align_max_padded(numel, slots, bsz);
+  const int64_t max_blocks = (max_padded + bsz - 1) / bsz;
+  int nbits = 1;
+  while ((1 << nbits) < slots) ++nbits;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, numel, slots,
+                     bsz, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits);
+  return check_launch("moe_align");
+}
+
+int moe_sum_reduce_bf16(const void* in, int64_t M, int k, int64_t H, void* out, hipStream_t st) {
+  MW8_REQUIRE(in && out, kErrArg, "moe_sum_reduce: null pointer");
+  MW8_REQUIRE(M >= 0 && k > 0 && H > 0 && H % 8 == 0, kErrShape,
+              "moe_sum_reduce: need H %% 8 == 0 (H=%lld)", (long long)H);
+  MW8_REQUIRE(aligned16(in) && aligned16(out), kErrAlign, "moe_sum_reduce: 16-byte alignment");
+  if (M == 0) return kOk;
+  const int64_t n = M * (H / 8);
+  hipLaunchKernelGGL(moe_sum_reduce_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, st, static_cast<const uint16_t*>(in), M, k, H, static_cast<uint16_t*>(out));
+  return check_launch("moe_sum_reduce");
+}
+
+int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                  const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* npp,
+                  int64_t max_sorted, const float* topk_w, int top_k, int64_t num_valid,
+                  int64_t N, int64_t K, int E, int bsz, void* out, int epi, hipStream_t st) {
+  MW8_REQUIRE(A && W && sorted_ids && expert_ids && npp && out, kErrArg, "moe_gemm: null pointer");
+  MW8_REQUIRE(epi == kEpiI32 || (sa && sw), kErrArg, "moe_gemm: null scales");
+  MW8_REQUIRE(N > 0 && K > 0 && K % 16 == 0 && K <= (1ll << 17), kErrShape,
+              "moe_gemm: need K %% 16 == 0 and K <= 131072 (N=%lld K=%lld)", (long long)N,
+              (long long)K);
+  MW8_REQUIRE(bsz == 16 || bsz == 64 || bsz == 128, kErrShape,
+              "moe_gemm: block size must be 16, 64 or 128 (got %d)", bsz);
+  MW8_REQUIRE(top_k >= 1 && E >= 1 && num_valid >= 0 && max_sorted >= 0, kErrShape,
+              "moe_gemm: bad routing sizes");
+  MW8_REQUIRE(aligned16(A) && aligned16(W), kErrAlign, "moe_gemm: A and W need 16-byte alignment");
+  const int64_t blocks = max_sorted / bsz;  // blocks past num_post_pad exit on device
+  if (blocks == 0) return kOk;
+  MW8_REQUIRE(blocks < 65536, kErrShape, "moe_gemm: too many expert blocks");
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
+  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
+  g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
+  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.splits = 1; g.kc = static_cast<int>(K);
+  if (bsz == 16) {
+    const int ldl = static_cast<int>(((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16);
+    const size_t lds = static_cast<size_t>(16) * ldl;
+    MW8_REQUIRE(lds <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",
+                (long long)K);
+    const dim3 grid(static_cast<unsigned>((N + kStreamRows - 1) / kStreamRows),
+                    static_cast<unsigned>(blocks));
+    if (epi == kEpiBf16)
+      hipLaunchKernelGGL((stream_gemm_kernel<1, kEpiBf16, SortedRows>), grid, dim3(256), lds, st, g);
+    else
+      hipLaunchKernelGGL((stream_gemm_kernel<1, kEpiI32, SortedRows>), grid, dim3(256), lds, st, g);
+  } else {
+    if (epi == kEpiBf16) launch_grouped_tile_bf16(g, static_cast<unsigned>(blocks), bsz, st);
+    else launch_grouped_tile_i32(g, static_cast<unsigned>(blocks), bsz, st);
+  }
+  return check_launch("moe_gemm");
+}
+
+}  // namespace mw8

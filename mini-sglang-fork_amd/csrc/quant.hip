@@ -1,0 +1,275 @@
+// Per-token dynamic int8 quantizer and fused activation + requant (gfx950).
+//
+// quant_rows:   x bf16 [M, K] -> q int8 [M, K], s fp32 [M]
+//               s = amax/127, q = clamp(rint(x/s), -127, 127)   (bit-exact)
+// act_rows:     x bf16 [R, 2d] (gate | up) -> a = bf16(act(g) * u) ->
+//               quantized exactly as above; optionally also writes a.
+//
+// One row is owned by TPR threads (64 = one wave, or 256 = four waves).
+// Each thread keeps VPT 16-byte vectors (8 bf16) of the row in registers,
+// so the row is read from HBM once: 16-byte coalesced loads, an integer
+// max over the sign-cleared bf16 bit patterns (monotone for finite
+// values), a wave/LDS max-reduction, then quantize-from-registers and
+// 8-byte stores.  Rows whose length exceeds TPR*VPT*8 take the generic
+// kernel, which re-reads the row (second read hits L2).
+#include "mw8_common.h"
+
+namespace mw8 {
+namespace {
+
+constexpr int kBlock = 256;
+
+// 8 bf16 values packed two per 32-bit register (element j in bits
+// 16*(j&1) .. of word j/2), so a register-resident row costs 4 VGPRs per
+// 16-byte vector.
+struct alignas(16) U16x8 {
+  uint32_t w[4];
+  __device__ __forceinline__ uint32_t get(int j) const {
+    return (j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xFFFFu);
+  }
+};
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    uint32_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Max over the TPR threads owning one row.  TPR == 64: pure wave
+// reduction.  TPR == 256: one row per block, cross-wave through LDS.
+template <int TPR>
+__device__ __forceinline__ uint32_t row_max(uint32_t v, uint32_t* red) {
+  v = wave_max_u32(v);
+  if constexpr (TPR == 64) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    uint32_t m = red[0];
+#pragma unroll
+    for (int w = 1; w < TPR / 64; ++w) m = red[w] > m ? red[w] : m;
+    return m;
+  }
+}
+
+__device__ __forceinline__ uint32_t absmax8(const U16x8& v, uint32_t m) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = v.w[j] & 0x7FFFu, hi = (v.w[j] >> 16) & 0x7FFFu;
+    m = lo > m ? lo : m;
+    m = hi > m ? hi : m;
+  }
+  return m;
+}
+
+__device__ __forceinline__ uint2 quant8(const U16x8& v, const RowScale& rs) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int q = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(v.get(j))), rs));
+    lo |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int q = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(v.get(4 + j))), rs));
+    hi |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * j);
+  }
+  return make_uint2(lo, hi);
+}
+
+// ------------------------------------------------------------ quantizer
+template <int TPR, int VPT>
+__global__ __launch_bounds__(kBlock) void quant_rows_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s) {
+  __shared__ uint32_t red[kBlock / 64];
+  constexpr int kRowsPerBlock = kBlock / TPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  const bool live = row < M;  // uniform per wave (TPR >= 64)
+  const int64_t nvec = K >> 3;
+  const U16x8* xr = reinterpret_cast<const U16x8*>(x + (live ? row : 0) * ldx);
+
+  U16x8 v[VPT];
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (live && idx < nvec) {
+      v[i] = xr[idx];
+      m = absmax8(v[i], m);
+    }
+  }
+  m = row_max<TPR>(m, red);
+  if (!live) return;
+  const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
+  uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (idx < nvec) qr[idx] = quant8(v[i], rs);
+  }
+  if (t == 0) s[row] = rs.s;
+}
+
+// Any K (no alignment beyond 2 bytes): one row per block, two passes.
+__global__ __launch_bounds__(kBlock) void quant_rows_generic_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s) {
+  __shared__ uint32_t red[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * ldx;
+  uint32_t m = 0;
+  for (int64_t k = threadIdx.x; k < K; k += kBlock) {
+    uint32_t a = xr[k] & 0x7FFFu;
+    m = a > m ? a : m;
+  }
+  m = row_max<kBlock>(m, red);
+  const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
+  for (int64_t k = threadIdx.x; k < K; k += kBlock)
+    q[row * ldq + k] = static_cast<int8_t>(static_cast<int>(quant_div_rne(bf16_to_f32(xr[k]), rs)));
+  if (threadIdx.x == 0) s[row] = rs.s;
+}
+
+// --------------------------------------------------- activation + requant
+__device__ __forceinline__ float act_fn(float g, int act) {
+  if (act == 0) return g / (1.0f + __expf(-g));  // silu
+  return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f));  // gelu (erf)
+}
+
+template <int TPR, int VPT>
+__global__ __launch_bounds__(kBlock) void act_rows_kernel(
+    const uint16_t* __restrict__ x, int64_t R, int64_t d, int act,
+    int8_t* __restrict__ q, float* __restrict__ s, uint16_t* __restrict__ a_out) {
+  __shared__ uint32_t red[kBlock / 64];
+  constexpr int kRowsPerBlock = kBlock / TPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  const bool live = row < R;
+  const int64_t nvec = d >> 3;
+  const U16x8* gr = reinterpret_cast<const U16x8*>(x + (live ? row : 0) * 2 * d);
+  const U16x8* ur = gr + nvec;
+
+  U16x8 v[VPT];
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (live && idx < nvec) {
+      const U16x8 g = gr[idx];
+      const U16x8 u = ur[idx];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a0 = act_fn(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j))), act) *
+                         bf16_to_f32(static_cast<uint16_t>(u.get(2 * j)));
+        const float a1 = act_fn(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j + 1))), act) *
+                         bf16_to_f32(static_cast<uint16_t>(u.get(2 * j + 1)));
+        v[i].w[j] = static_cast<uint32_t>(f32_to_bf16(a0)) |
+                    (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
+      }
+      m = absmax8(v[i], m);
+    }
+  }
+  m = row_max<TPR>(m, red);
+  if (!live) return;
+  const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
+  uint2* qr = reinterpret_cast<uint2*>(q + row * d);
+  U16x8* ar = a_out ? reinterpret_cast<U16x8*>(a_out + row * d) : nullptr;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (idx < nvec) {
+      qr[idx] = quant8(v[i], rs);
+      if (ar) ar[idx] = v[i];
+    }
+  }
+  if (t == 0) s[row] = rs.s;
+}
+
+// Pick (TPR, VPT) for a row of nvec 16-byte vectors; false if none fits.
+template <template <int, int> class Launch, typename... Args>
+bool dispatch_rows(int64_t nvec, int64_t rows, hipStream_t st, Args... args) {
+  auto go = [&](auto tpr_c, auto vpt_c) {
+    constexpr int TPR = decltype(tpr_c)::value;
+    constexpr int VPT = decltype(vpt_c)::value;
+    const int64_t blocks = (rows + (kBlock / TPR) - 1) / (kBlock / TPR);
+    Launch<TPR, VPT>::run(dim3(static_cast<unsigned>(blocks)), st, args...);
+    return true;
+  };
+  using I64 = std::integral_constant<int, 64>;
+  using I256 = std::integral_constant<int, 256>;
+  if (nvec <= 64 * 1) return go(I64{}, std::integral_constant<int, 1>{});
+  if (nvec <= 64 * 2) return go(I64{}, std::integral_constant<int, 2>{});
+  if (nvec <= 64 * 4) return go(I64{}, std::integral_constant<int, 4>{});
+  if (nvec <= 64 * 8) return go(I64{}, std::integral_constant<int, 8>{});
+  if (nvec <= 256 * 4) return go(I256{}, std::integral_constant<int, 4>{});
+  if (nvec <= 256 * 8) return go(I256{}, std::integral_constant<int, 8>{});
+  if (nvec <= 256 * 12) return go(I256{}, std::integral_constant<int, 12>{});
+  if (nvec <= 256 * 16) return go(I256{}, std::integral_constant<int, 16>{});
+  return false;
+}
+
+template <int TPR, int VPT>
+struct QuantLaunch {
+  static void run(dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, int64_t M,
+                  int64_t K, int8_t* q, int64_t ldq, float* s) {
+    hipLaunchKernelGGL((quant_rows_kernel<TPR, VPT>), grid, dim3(kBlock), 0, st, x, ldx, M, K,
+                       q, ldq, s);
+  }
+};
+
+template <int TPR, int VPT>
+struct ActLaunch {
+  static void run(dim3 grid, hipStream_t st, const uint16_t* x, int64_t R, int64_t d, int act,
+                  int8_t* q, float* s, uint16_t* a_out) {
+    hipLaunchKernelGGL((act_rows_kernel<TPR, VPT>), grid, dim3(kBlock), 0, st, x, R, d, act, q,
+                       s, a_out);
+  }
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+}  // namespace
+
+int quant_per_token_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                         float* s, hipStream_t st) {
+  MW8_REQUIRE(x && q && s, kErrArg, "quant_per_token: null pointer");
+  MW8_REQUIRE(M >= 0 && K > 0 && ldx >= K && ldq >= K, kErrShape,
+              "quant_per_token: bad sizes M=%lld K=%lld ldx=%lld ldq=%lld", (long long)M,
+              (long long)K, (long long)ldx, (long long)ldq);
+  if (M == 0) return kOk;
+  MW8_REQUIRE(M < (1ll << 31), kErrShape, "quant_per_token: M too large");
+  const auto* xb = static_cast<const uint16_t*>(x);
+  const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned16(x) &&
+                      aligned8(q);
+  if (!(vec_ok && dispatch_rows<QuantLaunch>(K / 8, M, st, xb, ldx, M, K, q, ldq, s))) {
+    hipLaunchKernelGGL(quant_rows_generic_kernel, dim3(static_cast<unsigned>(M)), dim3(kBlock), 0,
+                       st, xb, ldx, M, K, q, ldq, s);
+  }
+  return check_launch("quant_per_token");
+}
+
+int act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int act, int8_t* q, float* s,
+                           void* a_out, hipStream_t st) {
+  MW8_REQUIRE(x && q && s, kErrArg, "act_and_mul_quant: null pointer");
+  MW8_REQUIRE(act == 0 || act == 1, kErrArg, "act_and_mul_quant: act must be 0 (silu) or 1 (gelu)");
+  MW8_REQUIRE(R >= 0 && two_d > 0 && two_d % 16 == 0, kErrShape,
+              "act_and_mul_quant: need 2d %% 16 == 0, got %lld", (long long)two_d);
+  if (R == 0) return kOk;
+  MW8_REQUIRE(R < (1ll << 31), kErrShape, "act_and_mul_quant: too many rows");
+  MW8_REQUIRE(aligned16(x) && aligned8(q) && (!a_out || aligned16(a_out)), kErrAlign,
+              "act_and_mul_quant: x/act_out need 16-byte and q 8-byte alignment");
+  const int64_t d = two_d / 2;
+  const bool ok = dispatch_rows<ActLaunch>(d / 8, R, st, static_cast<const uint16_t*>(x), R, d, act,
+                                           q, s, static_cast<uint16_t*>(a_out));
+  MW8_REQUIRE(ok, kErrShape, "act_and_mul_quant: d=%lld exceeds the register-resident limit 32768",
+              (long long)d);
+  return check_launch("act_and_mul_quant");
+}
+
+}  // namespace mw8

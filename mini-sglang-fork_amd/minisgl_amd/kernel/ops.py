@@ -1,0 +1,299 @@
+"""torch-facing wrappers over the HIP C ABI.
+
+Every function validates shapes/dtypes on the host, allocates outputs with
+torch (the caching allocator, so the calls stay capturable in a HIP graph),
+and launches on the current torch stream.  Nothing here computes on the
+CPU: a missing library or a non-GPU tensor raises.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from .lib import check, load
+
+_ACT = {"silu": 0, "gelu": 1}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(*ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("the W8A8 HIP path needs GPU tensors (no CPU fallback)")
+
+
+# ----------------------------------------------------------------- workspace
+_WORKSPACE: Dict[torch.device, torch.Tensor] = {}
+
+
+def gemm_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
+    """Zero-initialised split-K workspace for (M, N, K), cached per device.
+
+    The kernels leave the workspace's arrival counters at zero after every
+    call, so the buffer is reusable as long as calls sharing it are ordered
+    on one stream.  Reserve the largest size before capturing a graph.
+    """
+    need = int(load().mw8_gemm_workspace_bytes(M, N, K))
+    if need == 0:
+        return None
+    dev = torch.device(device)
+    ws = _WORKSPACE.get(dev)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACE[dev] = ws
+    return ws
+
+
+# ----------------------------------------------------------------- quantizer
+def quant_per_token(
+    x: torch.Tensor, out: Optional[torch.Tensor] = None, scale: Optional[torch.Tensor] = None
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 [M, K] -> (int8 [M, K], fp32 [M]); s = amax/127, q = rint(x/s)."""
+    _on_gpu(x)
+    _need(x.dtype == torch.bfloat16 and x.dim() == 2, "quant_per_token: x must be bf16 [M, K]")
+    _need(x.stride(1) == 1, "quant_per_token: last dim must be contiguous")
+    M, K = x.shape
+    q = out if out is not None else torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = scale if scale is not None else torch.empty((M,), dtype=torch.float32, device=x.device)
+    _need(q.dtype == torch.int8 and q.shape == (M, K) and q.stride(1) == 1, "bad q buffer")
+    _need(s.dtype == torch.float32 and s.shape == (M,) and s.is_contiguous(), "bad s buffer")
+    if M == 0:
+        return q, s
+    check(
+        load().mw8_quant_per_token_bf16(
+            _ptr(x), M, K, x.stride(0), _ptr(q), q.stride(0), _ptr(s), _stream(x)
+        )
+    )
+    return q, s
+
+
+def act_and_mul_quant(
+    x: torch.Tensor, activation: str = "silu", return_act: bool = False
+):
+    """bf16 [R, 2d] -> (int8 [R, d], fp32 [R][, bf16 act [R, d]])."""
+    _on_gpu(x)
+    _need(activation in _ACT, f"unsupported activation {activation}")
+    _need(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x: bf16 [R, 2d]")
+    R, two_d = x.shape
+    d = two_d // 2
+    q = torch.empty((R, d), dtype=torch.int8, device=x.device)
+    s = torch.empty((R,), dtype=torch.float32, device=x.device)
+    a = torch.empty((R, d), dtype=torch.bfloat16, device=x.device) if return_act else None
+    if R > 0:
+        check(
+            load().mw8_act_and_mul_quant_bf16(
+                _ptr(x), R, two_d, _ACT[activation], _ptr(q), _ptr(s), _ptr(a), _stream(x)
+            )
+        )
+    return (q, s, a) if return_act else (q, s)
+
+
+# ----------------------------------------------------------------- dense GEMM
+def _check_gemm(q: torch.Tensor, w: torch.Tensor) -> Tuple[int, int, int]:
+    _on_gpu(q, w)
+    _need(q.dtype == torch.int8 and q.dim() == 2 and q.is_contiguous(), "A: int8 [M, K] contiguous")
+    _need(w.dtype == torch.int8 and w.dim() == 2 and w.is_contiguous(), "W: int8 [N, K] contiguous")
+    _need(q.shape[1] == w.shape[1], "A/W K mismatch")
+    return q.shape[0], w.shape[0], q.shape[1]
+
+
+def gemm_w8a8(
+    q: torch.Tensor,
+    s_a: torch.Tensor,
+    w: torch.Tensor,
+    s_w: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """y bf16 [M, N] = bf16(((acc * s_a[m]) * s_w[n]) + bias[n])."""
+    M, N, K = _check_gemm(q, w)
+    _need(s_a.dtype == torch.float32 and s_a.shape == (M,) and s_a.is_contiguous(), "s_a: fp32 [M]")
+    _need(s_w.dtype == torch.float32 and s_w.shape == (N,) and s_w.is_contiguous(), "s_w: fp32 [N]")
+    if bias is not None:
+        _need(bias.dtype == torch.bfloat16 and bias.shape == (N,) and bias.is_contiguous(), "bias: bf16 [N]")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=q.device)
+    _need(y.dtype == torch.bfloat16 and y.shape == (M, N) and y.is_contiguous(), "bad out buffer")
+    if M == 0:
+        return y
+    ws = gemm_workspace(M, N, K, q.device)
+    check(
+        load().mw8_gemm_w8a8_bf16(
+            _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K,
+            _ptr(ws), 0 if ws is None else ws.numel(), _stream(q),
+        )
+    )
+    return y
+
+
+def gemm_w8a8_i32(q: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Raw int32 accumulators acc [M, N] = A . W^T (parity hook)."""
+    M, N, K = _check_gemm(q, w)
+    acc = torch.empty((M, N), dtype=torch.int32, device=q.device)
+    if M == 0:
+        return acc
+    ws = gemm_workspace(M, N, K, q.device)
+    check(
+        load().mw8_gemm_w8a8_i32(
+            _ptr(q), _ptr(w), _ptr(acc), M, N, K, _ptr(ws), 0 if ws is None else ws.numel(),
+            _stream(q),
+        )
+    )
+    return acc
+
+
+# ----------------------------------------------------------------- MoE pieces
+def topk_softmax(
+    gating_output: torch.Tensor, topk: int, renormalize: bool
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Router: fp32 softmax, top-k, optional double renormalisation.
+
+    Mirrors fused_topk (python/minisgl/moe/fused.py:9-28), including the
+    extra ``w / (sum(w) + 1e-8)`` of :23-24, in one kernel.
+    """
+    _on_gpu(gating_output)
+    g = gating_output
+    _need(g.dim() == 2 and g.is_contiguous(), "gating_output: [M, E] contiguous")
+    _need(g.dtype in (torch.bfloat16, torch.float32), "gating_output: bf16 or fp32")
+    M, E = g.shape
+    w = torch.empty((M, topk), dtype=torch.float32, device=g.device)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=g.device)
+    if M > 0:
+        check(
+            load().mw8_topk_softmax(
+                _ptr(g), int(g.dtype == torch.bfloat16), M, E, topk, int(renormalize),
+                _ptr(w), _ptr(ids), _stream(g),
+            )
+        )
+    return w, ids
+
+
+def moe_align_block_size(
+    topk_ids: torch.Tensor, block_size: int, num_experts: int
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Same contract and buffer sizes as python/minisgl/moe/fused.py:31-89
+    (``num_experts + 1`` expert slots, sentinel ``numel`` padding).  Pairs
+    inside one expert segment are in ascending flat order."""
+    _on_gpu(topk_ids)
+    _need(topk_ids.dtype == torch.int32 and topk_ids.is_contiguous(), "topk_ids: int32 contiguous")
+    lib = load()
+    numel = topk_ids.numel()
+    slots = num_experts + 1
+    max_padded = int(lib.mw8_moe_align_max_padded(numel, slots, block_size))
+    max_blocks = -(-max_padded // block_size)
+    dev = topk_ids.device
+    sorted_ids = torch.empty((max_padded,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((max_blocks,), dtype=torch.int32, device=dev)
+    num_tokens_post_pad = torch.empty((1,), dtype=torch.int32, device=dev)
+    check(
+        lib.mw8_moe_align_block_size(
+            _ptr(topk_ids), numel, slots, block_size, _ptr(sorted_ids), _ptr(expert_ids),
+            _ptr(num_tokens_post_pad), _stream(topk_ids),
+        )
+    )
+    return sorted_ids, expert_ids, num_tokens_post_pad
+
+
+def fused_moe_kernel_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    C: torch.Tensor,
+    topk_weights: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    mul_routed_weight: bool,
+    top_k: int,
+    block_size: int,
+    num_valid_tokens: int,
+) -> None:
+    """Grouped W8A8 GEMM, the counterpart of fused_moe_kernel_triton
+    (python/minisgl/kernel/moe_impl.py:6-62): row p of C (a flat
+    (token, slot) pair, C viewed as [M*k, N]) receives
+    ``epilogue(A[p // top_k] . B[e]^T)``, times ``topk_weights[p]`` if
+    ``mul_routed_weight``."""
+    _on_gpu(A, A_scale, B, B_scale, C)
+    _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [T, K]")
+    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
+    E, N, K = B.shape
+    _need(A.shape[1] == K, "A/B K mismatch")
+    _need(A_scale.dtype == torch.float32 and A_scale.shape == (A.shape[0],), "A_scale: fp32 [T]")
+    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
+    _need(C.dtype == torch.bfloat16 and C.is_contiguous() and C.numel() == num_valid_tokens * N, "C: bf16 [M*k, N]")
+    assert topk_weights.stride(1) == 1  # python/minisgl/kernel/moe_impl.py:25
+    assert sorted_token_ids.stride(0) == 1  # :26
+    check(
+        load().mw8_moe_gemm_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids),
+            _ptr(expert_ids), _ptr(num_tokens_post_padded), sorted_token_ids.shape[0],
+            _ptr(topk_weights) if mul_routed_weight else None, top_k, num_valid_tokens, N, K, E,
+            block_size, _ptr(C), _stream(A),
+        )
+    )
+
+
+def fused_moe_kernel_w8a8_i32(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    top_k: int,
+    block_size: int,
+    num_valid_tokens: int,
+) -> torch.Tensor:
+    """Raw int32 accumulators of the grouped GEMM, [num_valid, N] (parity hook)."""
+    _on_gpu(A, B)
+    E, N, K = B.shape
+    out = torch.zeros((num_valid_tokens, N), dtype=torch.int32, device=A.device)
+    check(
+        load().mw8_moe_gemm_w8a8_i32(
+            _ptr(A), _ptr(B), _ptr(sorted_token_ids), _ptr(expert_ids),
+            _ptr(num_tokens_post_padded), sorted_token_ids.shape[0], top_k, num_valid_tokens,
+            N, K, E, block_size, _ptr(out), _stream(A),
+        )
+    )
+    return out
+
+
+def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
+    """out[t] = bf16(sum_i in[t, i]) (python/minisgl/kernel/moe_impl.py:65-98)."""
+    _on_gpu(input, output)
+    assert input.is_contiguous() and output.is_contiguous()
+    token_num, topk_num, hidden_dim = input.shape
+    assert output.shape[0] == token_num and output.shape[1] == hidden_dim
+    _need(input.dtype == torch.bfloat16 and output.dtype == torch.bfloat16, "bf16 only")
+    check(
+        load().mw8_moe_sum_reduce_bf16(
+            _ptr(input), token_num, topk_num, hidden_dim, _ptr(output), _stream(input)
+        )
+    )
+
+
+__all__ = [
+    "gemm_workspace",
+    "quant_per_token",
+    "act_and_mul_quant",
+    "gemm_w8a8",
+    "gemm_w8a8_i32",
+    "topk_softmax",
+    "moe_align_block_size",
+    "fused_moe_kernel_w8a8",
+    "fused_moe_kernel_w8a8_i32",
+    "moe_sum_reduce",
+]

@@ -1,0 +1,116 @@
+"""W8A8 drop-ins for the reference's linear layers
+(python/minisgl/layers/linear.py:13-127).
+
+Same constructors and the same ``forward(x: bf16 [..., K]) -> bf16 [..., N]``;
+the parameters become ``weight`` int8 [N, K] (the reference's [out, in]
+layout, :28), ``weight_scale`` fp32 [N] (per output channel) and ``bias``
+bf16 [N] or None.  ``forward`` = per-token int8 quantization of ``x`` +
+int8 MFMA GEMM with the scale/bias epilogue, both HIP kernels.
+
+This build runs on one GPU, so every layer is built at tensor-parallel
+size 1: local sizes equal full sizes and the row-parallel all-reduce
+(:104-105, :125-126) is absent.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from ..kernel import gemm_w8a8, quant_per_token
+from .base import BaseOP
+
+
+def quantize_weight(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel symmetric int8 quantization of a bf16 weight
+    [N, K]: ``weight_scale[n] = amax_k |w[n, k]| / 127`` and
+    ``weight[n, k] = rint(w[n, k] / weight_scale[n])`` (the same per-row
+    kernel as the activation quantizer)."""
+    return quant_per_token(w.contiguous())
+
+
+class _LinearW8A8Impl(BaseOP):
+    """Common body of the W8A8 linear layers (mirrors _LinearTPImpl, :13-32)."""
+
+    def __init__(
+        self,
+        full_isize: int,
+        full_osize: int,
+        local_isize: int,
+        local_osize: int,
+        has_bias: bool,
+    ):
+        self.full_input_size = full_isize
+        self.full_output_size = full_osize
+        self.local_input_size = local_isize
+        self.local_output_size = local_osize
+        self.weight = torch.empty(local_osize, local_isize, dtype=torch.int8)
+        self.weight_scale = torch.empty(local_osize, dtype=torch.float32)
+        self.bias = torch.empty(local_osize, dtype=torch.bfloat16) if has_bias else None
+
+    def forward_quantized(self, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+        """GEMM + epilogue on an already-quantized input (q int8 [M, K], s fp32 [M])."""
+        return gemm_w8a8(q, s, self.weight, self.weight_scale, self.bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, x.shape[-1])
+        q, s = quant_per_token(x2)
+        y = self.forward_quantized(q, s)
+        return y.view(*lead, y.shape[-1])
+
+    def load_float_weight(self, w: torch.Tensor, bias: Optional[torch.Tensor] = None) -> None:
+        """Quantize a bf16 [N, K] weight on the device into this layer."""
+        q, s = quantize_weight(w.to(torch.bfloat16))
+        self.weight, self.weight_scale = q, s
+        if bias is not None:
+            self.bias = bias.to(torch.bfloat16).contiguous()
+
+
+class LinearReplicated(_LinearW8A8Impl):
+    def __init__(self, input_size: int, output_size: int, has_bias: bool):
+        super().__init__(input_size, output_size, input_size, output_size, has_bias)
+
+
+class LinearColParallelMerged(_LinearW8A8Impl):
+    """Merged column-parallel layer (gate|up): N = sum(output_sizes) (:56-68)."""
+
+    def __init__(self, input_size: int, output_sizes: List[int], has_bias: bool):
+        n = sum(output_sizes)
+        super().__init__(input_size, n, input_size, n, has_bias)
+
+
+class LinearQKVMerged(_LinearW8A8Impl):
+    """q|k|v merged: N = (num_qo_heads + 2 * num_kv_heads) * head_dim (:71-88)."""
+
+    def __init__(
+        self,
+        hidden_size: int,
+        head_dim: int,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        has_bias: bool,
+    ):
+        n = (num_qo_heads + 2 * num_kv_heads) * head_dim
+        super().__init__(hidden_size, n, hidden_size, n, has_bias)
+
+
+class LinearOProj(_LinearW8A8Impl):
+    def __init__(self, input_size: int, output_size: int, has_bias: bool):
+        super().__init__(input_size, output_size, input_size, output_size, has_bias)
+
+
+class LinearRowParallel(_LinearW8A8Impl):
+    def __init__(self, input_size: int, output_size: int, has_bias: bool):
+        super().__init__(input_size, output_size, input_size, output_size, has_bias)
+
+
+__all__ = [
+    "quantize_weight",
+    "LinearReplicated",
+    "LinearColParallelMerged",
+    "LinearQKVMerged",
+    "LinearOProj",
+    "LinearRowParallel",
+]

@@ -1,0 +1,138 @@
+"""W8A8 fused-MoE backend: the orchestration of fused_experts_impl
+(python/minisgl/moe/fused.py:127-227) over HIP kernels.
+
+Flow for M tokens, top-k slots, E experts, w1 int8 [E, N=2I, H],
+w2 int8 [E, H, I]:
+
+1. route: ``topk_softmax`` (fp32 softmax, top-k, double renormalisation)
+2. ``moe_align_block_size`` with BLOCK_SIZE_M from ``get_default_config``
+3. quantize ``hidden_states`` once per token (GEMM1 addresses A rows as
+   ``pair // top_k``)
+4. GEMM1 -> bf16 cache [M*k, N]; routed weight only if
+   ``apply_router_weight_on_input`` (reference :201)
+5. activation + requant -> int8 [M*k, I] + fp32 scales
+6. GEMM2 (top_k = 1) -> bf16 cache [M*k, H], routed weight otherwise (:217)
+7. slot sum, written into ``hidden_states`` in place (:175, :223-226)
+
+All counts stay on the device (no host sync), so the call can be captured
+in a HIP graph.
+"""
+
+from __future__ import annotations
+
+import functools
+from typing import Dict, Tuple
+
+import torch
+
+from ..kernel import (
+    act_and_mul_quant,
+    fused_moe_kernel_w8a8,
+    moe_align_block_size,
+    moe_sum_reduce,
+    quant_per_token,
+    topk_softmax,
+)
+from .base import BaseMoeBackend
+
+
+def fused_topk(
+    hidden_states: torch.Tensor,
+    gating_output: torch.Tensor,
+    topk: int,
+    renormalize: bool,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(topk_weights fp32 [M, k], topk_ids int32 [M, k]); one HIP kernel
+    (python/minisgl/moe/fused.py:9-28)."""
+    assert hidden_states.shape[0] == gating_output.shape[0], "Number of tokens mismatch"
+    return topk_softmax(gating_output.contiguous(), topk, renormalize)
+
+
+def get_default_config(M: int, E: int, N: int, K: int, topk: int) -> Dict[str, int]:
+    """Two tile regimes keyed on tokens vs experts, as the reference
+    (python/minisgl/moe/fused.py:92-113): a 16-row block when M <= E
+    (decode: weight streaming), otherwise a 64-row block (MFMA tiles)."""
+    if M <= E:
+        return {"BLOCK_SIZE_M": 16}
+    return {"BLOCK_SIZE_M": 64}
+
+
+def try_get_optimal_moe_config(w1_shape, w2_shape, top_k: int, M: int) -> Dict[str, int]:
+    E, _, N = w2_shape
+    return get_default_config(M, E, N, w1_shape[2], top_k)
+
+
+def fused_experts_impl_w8a8(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    w1_scale: torch.Tensor,
+    w2: torch.Tensor,
+    w2_scale: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    activation: str = "silu",
+    apply_router_weight_on_input: bool = False,
+) -> torch.Tensor:
+    assert hidden_states.shape[1] == w1.shape[2], "Hidden size mismatch"
+    assert topk_weights.shape == topk_ids.shape, "topk shape mismatch"
+    assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+    assert w1.is_contiguous(), "Expert weights1 must be contiguous"
+    assert w2.is_contiguous(), "Expert weights2 must be contiguous"
+    assert hidden_states.dtype == torch.bfloat16, "W8A8 MoE takes bf16 activations"
+    assert w1.dtype == torch.int8 and w2.dtype == torch.int8, "W8A8 MoE takes int8 weights"
+    M, H = hidden_states.shape
+    E, N, _ = w1.shape
+    k = topk_ids.shape[1]
+    config = functools.partial(try_get_optimal_moe_config, w1.shape, w2.shape, k)(M)
+    bsz = config["BLOCK_SIZE_M"]
+
+    sorted_ids, expert_ids, num_post_pad = moe_align_block_size(topk_ids, bsz, E)
+    q_h, s_h = quant_per_token(hidden_states)
+    # one buffer backs both bf16 caches, as in the reference (:157-172)
+    cache = torch.empty(M * k * max(N, H), dtype=torch.bfloat16, device=hidden_states.device)
+    cache1 = cache[: M * k * N].view(M * k, N)
+    fused_moe_kernel_w8a8(
+        q_h, s_h, w1, w1_scale, cache1, topk_weights, sorted_ids, expert_ids, num_post_pad,
+        apply_router_weight_on_input, k, bsz, M * k,
+    )
+    q_a, s_a = act_and_mul_quant(cache1, activation)
+    cache3 = cache[: M * k * H].view(M * k, H)
+    fused_moe_kernel_w8a8(
+        q_a, s_a, w2, w2_scale, cache3, topk_weights, sorted_ids, expert_ids, num_post_pad,
+        not apply_router_weight_on_input, 1, bsz, M * k,
+    )
+    moe_sum_reduce(cache3.view(M, k, H), hidden_states)
+    return hidden_states
+
+
+class FusedMoeW8A8(BaseMoeBackend):
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        w1: torch.Tensor,
+        w2: torch.Tensor,
+        gating_output: torch.Tensor,
+        topk: int,
+        renormalize: bool,
+        activation: str = "silu",
+        apply_router_weight_on_input: bool = False,
+        w1_scale: torch.Tensor | None = None,
+        w2_scale: torch.Tensor | None = None,
+        **kwargs,
+    ) -> torch.Tensor:
+        if w1_scale is None or w2_scale is None:
+            raise ValueError("the W8A8 MoE backend needs w1_scale and w2_scale")
+        topk_weights, topk_ids = fused_topk(hidden_states, gating_output, topk, renormalize)
+        return fused_experts_impl_w8a8(
+            hidden_states, w1, w1_scale, w2, w2_scale, topk_weights, topk_ids, activation,
+            apply_router_weight_on_input=apply_router_weight_on_input,
+        )
+
+
+__all__ = [
+    "fused_topk",
+    "get_default_config",
+    "try_get_optimal_moe_config",
+    "fused_experts_impl_w8a8",
+    "FusedMoeW8A8",
+]

@@ -1,0 +1,156 @@
+"""GPU parity of the dense W8A8 GEMM (stream core for M <= 64, MFMA tile core
+above) against the CPU oracle: int32 accumulators and bf16 outputs
+bit-exact (the epilogue is the oracle's closed form, one rounding per op);
+rel-L2 <= 1e-3 is checked as the contract bound as well."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, bf16_bits_equal, f32, rel_l2
+from minisgl_amd.benchmark import linear_case
+from minisgl_amd.kernel import MW8Error, gemm_w8a8, gemm_w8a8_i32, quant_per_token
+from minisgl_amd.layers import (
+    LinearColParallelMerged,
+    LinearOProj,
+    LinearQKVMerged,
+    LinearReplicated,
+    LinearRowParallel,
+)
+from oracle import w8a8 as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _run_case(M, K, N, seed=0, bias=False, rows=None):
+    c = linear_case(M, K, N, seed=seed, bias=bias)
+    x = c["x"].to(DEV)
+    w = c["w"].to(DEV)
+    s_w = c["s_w"].to(DEV)
+    b = c["bias"].to(DEV) if bias else None
+    q, s_a = quant_per_token(x)
+    acc = gemm_w8a8_i32(q, w)
+    y = gemm_w8a8(q, s_a, w, s_w, b)
+    torch.cuda.synchronize()
+    # oracle on the same bytes (optionally on a row sample for large M)
+    xs = f32(c["x"]) if rows is None else f32(c["x"][rows])
+    q_ref, s_ref = orc.quant_per_token(xs)
+    sel = slice(None) if rows is None else rows
+    np.testing.assert_array_equal(q.cpu().numpy()[sel], q_ref)
+    acc_ref = orc.gemm_i32(q_ref, c["w"].numpy())
+    np.testing.assert_array_equal(acc.cpu().numpy()[sel], acc_ref)
+    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy(), None if not bias else f32(c["bias"]))
+    y_sel = y[sel] if rows is None else y[torch.as_tensor(rows, device=DEV)]
+    assert rel_l2(f32(y_sel), y_ref) <= 1e-3
+    eq = bf16_bits_equal(y_sel, y_ref)
+    assert eq.all(), f"{(~eq).sum()} of {eq.size} bf16 outputs differ"
+
+
+@pytest.mark.parametrize(
+    "M,K,N",
+    [
+        (1, 128, 64), (3, 144, 100), (16, 1024, 6144), (17, 256, 192), (5, 2048, 80),
+        (33, 1024, 128), (64, 1024, 320), (64, 4096, 512),
+        (65, 512, 256), (100, 144, 100), (128, 1024, 1024), (200, 1040, 300), (512, 2048, 640),
+    ],
+)
+def test_gemm_small_shapes(M, K, N):
+    announce(f"gemm M={M} K={K} N={N}")
+    _run_case(M, K, N, seed=M + K + N)
+
+
+def test_gemm_cfg0():
+    """Config 0: Qwen3-0.6B gate_up, M=16 K=1024 N=6144, seed 0."""
+    announce("gemm cfg0")
+    _run_case(16, 1024, 6144, seed=0)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 512])
+@pytest.mark.parametrize("K,N", [(5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120)])
+def test_gemm_qwen3_14b(M, K, N):
+    announce(f"gemm 14B M={M} K={K} N={N}")
+    _run_case(M, K, N, seed=0)
+
+
+@pytest.mark.parametrize("M", [4096, 8192])
+@pytest.mark.parametrize("K,N", [(5120, 7168), (17408, 5120)])
+def test_gemm_qwen3_14b_large_m_sampled(M, K, N):
+    """Large M: every output is computed on the GPU; a fixed sample of rows
+    (first, last, and random rows of each 128-row tile band) is checked."""
+    announce(f"gemm 14B large M={M} K={K} N={N}")
+    rng = np.random.default_rng(M + K)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 62, replace=False)]))
+    _run_case(M, K, N, seed=0, rows=rows)
+
+
+def test_gemm_bias():
+    announce("gemm bias")
+    _run_case(16, 512, 384, seed=3, bias=True)
+    _run_case(300, 512, 384, seed=4, bias=True)
+
+
+def test_gemm_extremes():
+    """All +127 x all -127 hits the closed form -K*127*127 in int32."""
+    announce("gemm extremes")
+    for M in (2, 130):
+        K, N = 17408, 256
+        a = torch.full((M, K), 127, dtype=torch.int8, device=DEV)
+        w = torch.full((N, K), -127, dtype=torch.int8, device=DEV)
+        acc = gemm_w8a8_i32(a, w)
+        assert int(acc.min()) == int(acc.max()) == -K * 127 * 127
+
+
+def test_gemm_workspace_reuse_and_zero_rows():
+    """Two split-K calls in a row through one workspace (counters re-armed)."""
+    announce("gemm workspace reuse")
+    c1 = linear_case(8, 5120, 5120, seed=11)
+    c2 = linear_case(3, 5120, 5120, seed=12)
+    outs = []
+    for c in (c1, c2, c1):
+        q, s = quant_per_token(c["x"].to(DEV))
+        outs.append(gemm_w8a8_i32(q, c["w"].to(DEV)).cpu())
+    assert torch.equal(outs[0], outs[2])
+    q_ref, _ = orc.quant_per_token(f32(c2["x"]))
+    np.testing.assert_array_equal(outs[1].numpy(), orc.gemm_i32(q_ref, c2["w"].numpy()))
+    empty = gemm_w8a8(torch.empty(0, 64, dtype=torch.int8, device=DEV), torch.empty(0, device=DEV),
+                      torch.zeros(32, 64, dtype=torch.int8, device=DEV), torch.ones(32, device=DEV))
+    assert empty.shape == (0, 32)
+
+
+def test_gemm_rejects_bad_k():
+    a = torch.zeros(4, 40, dtype=torch.int8, device=DEV)
+    w = torch.zeros(8, 40, dtype=torch.int8, device=DEV)
+    with pytest.raises(MW8Error):
+        gemm_w8a8_i32(a, w)
+
+
+def test_linear_layers_drop_in():
+    """The Linear* drop-ins: constructor shapes as the reference, forward =
+    quant + GEMM + epilogue, parity with the oracle."""
+    announce("linear layers")
+    gen = torch.Generator().manual_seed(5)
+    layers = [
+        LinearReplicated(256, 128, has_bias=False),
+        LinearColParallelMerged(256, [192, 192], has_bias=False),
+        LinearQKVMerged(256, head_dim=32, num_qo_heads=4, num_kv_heads=2, has_bias=True),
+        LinearOProj(256, 256, has_bias=False),
+        LinearRowParallel(256, 512, has_bias=False),
+    ]
+    for layer in layers:
+        N, K = layer.weight.shape
+        sd = {
+            "weight": torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8).to(DEV),
+            "weight_scale": (torch.rand(N, generator=gen) * 1e-2).to(DEV),
+        }
+        if layer.bias is not None:
+            sd["bias"] = torch.randn(N, generator=gen).to(torch.bfloat16).to(DEV)
+        layer.load_state_dict(dict(sd))
+        for M in (1, 70):
+            x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+            y = layer.forward(x.to(DEV))
+            y_ref, *_ = orc.linear_w8a8(
+                f32(x), sd["weight"].cpu().numpy(), sd["weight_scale"].cpu().numpy(),
+                None if layer.bias is None else f32(sd["bias"]),
+            )
+            assert bf16_bits_equal(y, y_ref).all()
