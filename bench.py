@@ -1,0 +1,366 @@
+#!/usr/bin/env python
+"""W8A8 int8 linear benchmark on one MI355X (configs[1] of BASELINE.json).
+
+One step = the W8A8 GEMM (int8 MFMA + per-token x per-channel scale
+epilogue -> bf16) over the whole Qwen3-14B sweep: {qkv K5120 N7168,
+o_proj K5120 N5120, gate_up K5120 N34816, down K17408 N5120} x
+M in {1, 8, 64, 512, 4096, 8192} -- 24 launches, activations already
+quantized and resident in HBM.  Weights are kept in ``--copies`` distinct
+copies and rotated so that no launch finds its weights in the 256 MB MALL.
+
+Printed (one JSON line): whole-step throughput in TOPS (value), per-shape
+time / TOPS / GB/s / roofline fraction from HIP events recorded around
+every launch inside the timed region, the dominant kernel's roofline, the
+CPU baseline (the CPU oracle, timed on the host on a bounded sample, plus
+the reference's bf16 ``F.linear`` CPU op on the same sample), and secondary
+measurements (quantizer at config 2, MoE layer tokens/s at config 3, the
+Qwen3-32B GEMM chain at config 4) timed outside the main region.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mini-sglang-fork_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W8A8 GEMM TOPS + HBM GB/s (roofline %) at M=1..8192; MoE layer tokens/s"
+HBM_PEAK_GBPS = 8000.0
+INT8_OPS_PER_CLK_CU = 8192  # dense int8 MFMA ops per clock per CU (CDNA4)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemm_bytes(M: int, N: int, K: int, bias: bool = False) -> int:
+    return M * K + N * K + 4 * M + 4 * N + 2 * M * N + (2 * N if bias else 0)
+
+
+def device_peaks(lib):
+    cu, clk, l2 = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    rc = lib.mw8_device_info(0, ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(l2))
+    if rc != 0:
+        raise RuntimeError(lib.mw8_last_error().decode())
+    tops = cu.value * clk.value * 1e3 * INT8_OPS_PER_CLK_CU / 1e12
+    return {"cus": cu.value, "clock_mhz": clk.value / 1e3, "int8_peak_tops": tops,
+            "hbm_peak_gbps": HBM_PEAK_GBPS}
+
+
+def roofline_frac(ops: float, nbytes: float, t_s: float, peak_tops: float) -> float:
+    attainable = min(peak_tops * 1e12, HBM_PEAK_GBPS * 1e9 * ops / nbytes)
+    return (ops / t_s) / attainable
+
+
+# --------------------------------------------------------------------------
+# CPU baseline: the CPU oracle (numpy, the "port") and the reference's CPU
+# torch op F.linear(x_bf16, W.bfloat16()) on a bounded sample of the sweep.
+# --------------------------------------------------------------------------
+def cpu_baseline(shapes, m_sample: int, budget_s: float):
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from minisgl_amd.benchmark import linear_case
+    from oracle import w8a8 as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        blas_threads = os.cpu_count() or 1
+    torch.set_num_threads(os.cpu_count() or 1)
+    cases = [linear_case(m_sample, K, N, seed=0) for _, K, N in shapes]
+    ops = sum(2.0 * m_sample * K * N for _, K, N in shapes)
+    t0 = time.perf_counter()
+    runs = 0
+    while True:
+        for c in cases:
+            orc.linear_w8a8(c["x"].float().numpy(), c["w"].numpy(), c["s_w"].numpy())
+        runs += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    t_oracle = (time.perf_counter() - t0) / runs
+    # the reference's CPU op, one pass (bf16 weights)
+    t1 = time.perf_counter()
+    for c in cases:
+        F.linear(c["x"], c["w"].to(torch.bfloat16))
+    t_ref = time.perf_counter() - t1
+    return {
+        "value": ops / t_oracle / 1e12,
+        "unit": "TOPS",
+        "cores": int(blas_threads),
+        "kind": "port",
+        "sample": (f"cfg1 shapes qkv/o_proj/gate_up/down at M={m_sample} (one pass = "
+                   f"{ops / 1e9:.0f} GOP), CPU oracle quant + exact int GEMM (fp64 BLAS) + "
+                   f"fp32 epilogue, {runs} pass(es) in {t_oracle * runs:.1f} s"),
+        "ms_per_pass": t_oracle * 1e3,
+        "reference_torch_bf16_linear_tops": ops / t_ref / 1e12,
+        "reference_torch_bf16_linear_ms": t_ref * 1e3,
+        "torch_threads": torch.get_num_threads(),
+        "host_cpus": os.cpu_count(),
+    }
+
+
+# --------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=2, help="weight copies rotated to defeat the MALL")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build targets a single MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES, SWEEP_M
+    from minisgl_amd.kernel import gemm_w8a8, load, quant_per_token
+
+    lib = load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    peaks = device_peaks(lib)
+    peak_tops = peaks["int8_peak_tops"]
+    log(f"device: {peaks}")
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    # weights: R distinct copies per shape (values: uniform int8 in [-127, 127])
+    W = {}
+    SW = {}
+    for name, K, N in QWEN3_14B_SHAPES:
+        W[name] = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev)
+                   for _ in range(args.copies)]
+        SW[name] = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
+    # activations: the outlier recipe, quantized once (resident int8 + fp32 scales)
+    A = {}
+    for M in SWEEP_M:
+        for name, K, N in QWEN3_14B_SHAPES:
+            if (M, K) not in A:
+                x = torch.randn(M, K, generator=gen, device=dev)
+                mask = torch.rand(M, K, generator=gen, device=dev) < 1e-3
+                x[mask] *= 20
+                A[(M, K)] = quant_per_token(x.to(torch.bfloat16))
+                del x, mask
+    Y = {(M, name): torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+         for M in SWEEP_M for name, K, N in QWEN3_14B_SHAPES}
+    plan = [(M, name, K, N) for M in SWEEP_M for name, K, N in QWEN3_14B_SHAPES]
+    # reserve the split-K workspace for the largest small-M shape before timing
+    from minisgl_amd.kernel.ops import gemm_workspace
+
+    for M, name, K, N in plan:
+        gemm_workspace(M, N, K, dev)
+    torch.cuda.synchronize()
+    log(f"workload ready: {len(plan)} GEMMs per step, {args.copies} weight copies, "
+        f"{torch.cuda.memory_allocated() / 2**30:.2f} GiB allocated")
+
+    launch_no = [0]
+
+    def step(events=None):
+        for i, (M, name, K, N) in enumerate(plan):
+            q, s = A[(M, K)]
+            w = W[name][launch_no[0] % args.copies]
+            launch_no[0] += 1
+            if events is not None:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                gemm_w8a8(q, s, w, SW[name], out=Y[(M, name)])
+                e1.record()
+                events[i].append((e0, e1))
+            else:
+                gemm_w8a8(q, s, w, SW[name], out=Y[(M, name)])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[] for _ in plan]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(events)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ops_step = sum(2.0 * M * N * K for M, _, K, N in plan)
+    value = ops_step * args.steps / wall / 1e12
+
+    shapes = []
+    for i, (M, name, K, N) in enumerate(plan):
+        ts = [a.elapsed_time(b) * 1e-3 for a, b in events[i]]
+        t = sum(ts) / len(ts)
+        ops = 2.0 * M * N * K
+        nb = gemm_bytes(M, N, K)
+        ai = ops / nb
+        bound = "mfma" if ai >= peak_tops * 1e12 / (HBM_PEAK_GBPS * 1e9) else "hbm"
+        shapes.append({
+            "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2),
+            "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
+            "bound": bound, "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
+            "kernel": "stream_gemm_kernel" if M <= 64 else "tile_gemm_kernel",
+        })
+    dom = max(shapes, key=lambda r: r["us"])
+    dom_ops = 2.0 * dom["M"] * dom["N"] * dom["K"]
+    dom_t = dom["us"] * 1e-6
+    roofline = {
+        "bound": dom["bound"],
+        "achieved": round(dom_ops / dom_t / 1e12, 2) if dom["bound"] == "mfma"
+        else round(gemm_bytes(dom["M"], dom["N"], dom["K"]) / dom_t / 1e9, 1),
+        "peak": round(peak_tops, 1) if dom["bound"] == "mfma" else HBM_PEAK_GBPS,
+        "unit": "TOPS" if dom["bound"] == "mfma" else "GB/s",
+        "frac": dom["roofline_frac"],
+        "traffic": None,
+        "kernel": f"{dom['kernel']} ({dom['shape']} M={dom['M']} K={dom['K']} N={dom['N']})",
+        "per_launch": (f"{dom_ops / 1e9:.1f} GOP = 2*M*N*K and "
+                       f"{gemm_bytes(dom['M'], dom['N'], dom['K']) / 1e6:.1f} MB algorithmic "
+                       f"per launch, avg of {args.steps} launches timed with HIP events"),
+    }
+    log(f"step: {wall / args.steps * 1e3:.3f} ms, {value:.1f} TOPS; dominant {roofline['kernel']} "
+        f"{dom['us']} us frac {dom['roofline_frac']}")
+    for r in shapes:
+        log(f"  {r['shape']:8s} M={r['M']:5d} {r['us']:9.2f} us {r['tops']:8.1f} TOPS "
+            f"{r['gbps']:8.1f} GB/s  {r['bound']} frac={r['roofline_frac']:.3f}")
+
+    # release the sweep buffers before the secondary measurements
+    del W, A, Y
+    torch.cuda.empty_cache()
+    secondary = None if args.no_secondary else run_secondary(dev, peak_tops)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(QWEN3_14B_SHAPES, 512, args.cpu_budget)
+    if cpu:
+        log(f"cpu baseline: {cpu['value']:.3f} TOPS ({cpu['cores']} threads); torch bf16 "
+            f"F.linear {cpu['reference_torch_bf16_linear_tops']:.3f} TOPS")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": ("synthetic: randn bf16 activations with 0.1% x20 outliers (quantized per token "
+                 "before the timed region), int8 weights uniform in [-127,127], fp32 scales in "
+                 "[1e-3,1e-2]"),
+        "config": {
+            "workload": ("cfg1 W8A8 linear sweep, Qwen3-14B shapes qkv(5120->7168) "
+                         "o_proj(5120->5120) gate_up(5120->34816) down(17408->5120) x "
+                         "M in {1,8,64,512,4096,8192}; one step = 24 GEMM launches"),
+            "weight_copies_rotated": args.copies,
+            "ops_per_step": ops_step,
+        },
+        "device": peaks,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "shapes": shapes,
+        "secondary": secondary,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_secondary(dev, peak_tops):
+    """Config 2 (quantizer), config 3 (MoE layer) and config 4 (32B chain),
+    each timed with a graph of 10 calls replayed 10 times."""
+    import torch
+
+    from minisgl_amd.benchmark import moe_case, perf_hip
+    from minisgl_amd.benchmark.inputs import QWEN3_32B_CHAIN
+    from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
+    from minisgl_amd.kernel import act_and_mul_quant, gemm_w8a8, quant_per_token
+    from minisgl_amd.layers import MoELayer
+    from minisgl_amd.moe import create_moe_backend
+
+    res = {}
+    gen = torch.Generator(device=dev).manual_seed(1)
+    # config 2: quantizer [8192, 17408]
+    M, K = 8192, 17408
+    x = torch.randn(M, K, generator=gen, device=dev)
+    x[torch.rand(M, K, generator=gen, device=dev) < 1e-3] *= 20
+    x = x.to(torch.bfloat16)
+    q = torch.empty(M, K, dtype=torch.int8, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    t = perf_hip(lambda: quant_per_token(x, q, s)) * 1e-3
+    nb = 3 * M * K + 4 * M
+    res["quant_cfg2"] = {"us": round(t * 1e6, 2), "gbps": round(nb / t / 1e9, 1),
+                         "roofline_frac": round(nb / t / 1e9 / HBM_PEAK_GBPS, 4)}
+    log(f"quant cfg2: {res['quant_cfg2']}")
+    del x, q, s
+
+    # config 3: MoE layer tokens/s
+    res["moe_cfg3"] = {}
+    for Mt in (16, 256, 4096):
+        c = moe_case(Mt, seed=0)
+        layer = MoELayer(128, 8, 2048, 768)
+        layer.load_state_dict({"gate_up_proj": c["w1"].to(dev), "down_proj": c["w2"].to(dev),
+                               "gate_up_scale": c["s_w1"].to(dev), "down_scale": c["s_w2"].to(dev)})
+        set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+        h0 = c["hidden"].to(dev)
+        lg = c["logits"].to(dev)
+        h = h0.clone()
+
+        def f():
+            h.copy_(h0)
+            layer.forward(h, lg)
+
+        t = perf_hip(f) * 1e-3
+        reset_global_ctx()
+        ids = torch.topk(torch.softmax(c["logits"].float(), -1), 8, -1).indices
+        touched = int(torch.unique(ids).numel())
+        H, I, E = 2048, 768, 128
+        nb = touched * (3 * H * I + 4 * (2 * I + H)) + 4 * Mt * H + 4 * Mt * E
+        ops = 6.0 * Mt * 8 * H * I
+        res["moe_cfg3"][str(Mt)] = {
+            "us": round(t * 1e6, 2), "tokens_per_s": round(Mt / t, 1),
+            "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
+            "touched_experts": touched,
+            "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
+        }
+        log(f"moe cfg3 M={Mt}: {res['moe_cfg3'][str(Mt)]}")
+        del c, layer, h0, h, lg
+
+    # config 4: Qwen3-32B GEMM chain at M = 2080
+    Mc = 2080
+    Wc = {n: (torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev),
+              torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3) for n, K, N in QWEN3_32B_CHAIN}
+    xin = torch.randn(Mc, 5120, generator=gen, device=dev).to(torch.bfloat16)
+
+    def chain():
+        q0, s0 = quant_per_token(xin)
+        qkv = gemm_w8a8(q0, s0, *Wc["qkv"])
+        q1, s1 = quant_per_token(qkv[:, :8192])  # q-slice stands in for the attention output
+        o = gemm_w8a8(q1, s1, *Wc["o_proj"])
+        q2, s2 = quant_per_token(o)
+        gu = gemm_w8a8(q2, s2, *Wc["gate_up"])
+        q3, s3 = act_and_mul_quant(gu)
+        return gemm_w8a8(q3, s3, *Wc["down"])
+
+    t = perf_hip(chain, graph_calls=4) * 1e-3
+    ops = sum(2.0 * Mc * K * N for _, K, N in QWEN3_32B_CHAIN)
+    res["chain_cfg4"] = {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 2),
+                         "mfma_frac": round(ops / t / 1e12 / peak_tops, 4),
+                         "note": "quant + 4 GEMMs + act/requant, attention replaced by the q-slice"}
+    log(f"chain cfg4: {res['chain_cfg4']}")
+    return res
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -47,6 +47,13 @@ const char* mw8_last_error(void);
 int mw8_version(void);
 
 /*
+ * Compute units, peak engine clock (kHz) and L2 bytes of a device; used to
+ * derive the MFMA peak the benchmark reports against.  No reference
+ * counterpart (measurement helper).
+ */
+int mw8_device_info(int32_t device, int32_t* num_cu, int32_t* clock_khz, int64_t* l2_bytes);
+
+/*
  * Per-token dynamic int8 quantizer: x bf16 [M, K] (row stride ldx elements)
  * -> q int8 [M, K] (row stride ldq) and s fp32 [M].
  * No reference counterpart: it is inserted before the reference's
@@ -69,10 +76,18 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
                                float* s, void* act_out, mw8_stream_t stream);
 
 /*
- * Bytes of workspace mw8_gemm_w8a8_* needs for (M, N, K); 0 if none.
- * The workspace must be zero-filled once when allocated; every call leaves
- * its arrival counters at zero again.  Calls that share one workspace must
- * be ordered (same stream).
+ * Tile-configuration override for the dense GEMM, process-wide: decode_cfg
+ * indexes the small-M (M <= 64) configurations, tile_cfg the large-M ones;
+ * -1 restores the automatic choice.  Results do not depend on the
+ * configuration (exact integer accumulation).  Tuning hook; no reference
+ * counterpart.
+ */
+void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg);
+
+/*
+ * Bytes of workspace mw8_gemm_w8a8_* needs for (M, N, K).  The current
+ * kernels need none and return 0; the workspace arguments are kept so that
+ * callers already pass one if a future configuration needs it.
  */
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

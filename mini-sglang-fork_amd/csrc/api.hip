@@ -29,6 +29,7 @@ int check_launch(const char* what) {
 int quant_per_token_bf16(const void*, int64_t, int64_t, int64_t, int8_t*, int64_t, float*, hipStream_t);
 int act_and_mul_quant_bf16(const void*, int64_t, int64_t, int, int8_t*, float*, void*, hipStream_t);
 size_t gemm_workspace_bytes(int64_t, int64_t, int64_t);
+void set_tuning(int, int);
 int gemm_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, const void*, void*,
                    int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 int gemm_w8a8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, void*, size_t,
@@ -60,6 +61,17 @@ const char* mw8_last_error(void) { return mw8::g_last_error; }
 
 int mw8_version(void) { return 100; }
 
+int mw8_device_info(int32_t device, int32_t* num_cu, int32_t* clock_khz, int64_t* l2_bytes) {
+  MW8_REQUIRE(num_cu && clock_khz && l2_bytes, mw8::kErrArg, "device_info: null pointer");
+  hipDeviceProp_t p;
+  const hipError_t e = hipGetDeviceProperties(&p, device);
+  MW8_REQUIRE(e == hipSuccess, mw8::kErrLaunch, "device_info: %s", hipGetErrorString(e));
+  *num_cu = p.multiProcessorCount;
+  *clock_khz = p.clockRate;
+  *l2_bytes = p.l2CacheSize;
+  return mw8::kOk;
+}
+
 int mw8_quant_per_token_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q,
                              int64_t ldq, float* s, mw8_stream_t st) {
   MW8_ENTRY(mw8::quant_per_token_bf16(x, M, K, ldx, q, ldq, s, S(st)));
@@ -69,6 +81,8 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
                                float* s, void* act_out, mw8_stream_t st) {
   MW8_ENTRY(mw8::act_and_mul_quant_bf16(x, R, two_d, act, q, s, act_out, S(st)));
 }
+
+void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg) { mw8::set_tuning(decode_cfg, tile_cfg); }
 
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return mw8::gemm_workspace_bytes(M, N, K);

@@ -1,92 +1,161 @@
-// Dense W8A8 GEMM: dispatch between the weight-streaming core (M <= 64) and
-// the MFMA tile core (M > 64), plus the C-ABI entry points.
+// Dense W8A8 GEMM: dispatch between the decode core (M <= 64: weight
+// streaming, in-block split-K) and the MFMA tile core (M > 64), plus the
+// grouped-tile launchers used by the fused-MoE GEMM.
+#include <atomic>
+
 #include "gemm_kernels.h"
 
 namespace mw8 {
 namespace {
 
-constexpr int64_t kStreamMaxM = 64;
-constexpr int kStreamTargetBlocks = 1024;  // ~4 resident blocks per CU on 256 CUs
+constexpr int64_t kDecodeMaxM = 64;
 
-struct StreamPlan {
-  int mt;        // 16-token groups
-  int splits;    // K splits
-  int kc;        // K bytes per split (multiple of 256)
-  int64_t n_tiles;
-  size_t ws_bytes;  // counters + partials (0 when splits == 1)
+// Tuning override (-1 = automatic); set through mw8_set_tuning.
+std::atomic<int> g_decode_cfg{-1};
+std::atomic<int> g_tile_cfg{-1};
+
+// ------------------------------------------------------------------ decode
+// (rows of 16 per block, waves per block, K steps of loads in flight)
+struct DecodeCfg {
+  int rg, waves, u;
 };
+constexpr DecodeCfg kDecodeCfgs[] = {
+    {1, 4, 8}, {2, 4, 4}, {1, 8, 4}, {2, 8, 4}, {4, 4, 4}, {4, 8, 2}, {2, 8, 2},
+};
+constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
-int kc_max_for(int mt) {
-  switch (mt) {
-    case 1: return stream_kc_max<1>();
-    case 2: return stream_kc_max<2>();
-    case 3: return stream_kc_max<3>();
-    default: return stream_kc_max<4>();
+template <int RG, int TG, int WAVES, int U, int EPI>
+void launch_decode(const GemmArgs& g, hipStream_t st) {
+  const unsigned blocks = static_cast<unsigned>((g.N + 16 * RG - 1) / (16 * RG));
+  hipLaunchKernelGGL((decode_gemm_kernel<RG, TG, WAVES, U, EPI>), dim3(blocks), dim3(64 * WAVES), 0,
+                     st, g);
+}
+
+template <int TG, int EPI>
+void decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
+  switch (cfg) {
+    case 0: launch_decode<1, TG, 4, 8, EPI>(g, st); break;
+    case 1: launch_decode<2, TG, 4, 4, EPI>(g, st); break;
+    case 2: launch_decode<1, TG, 8, 4, EPI>(g, st); break;
+    case 3: launch_decode<2, TG, 8, 4, EPI>(g, st); break;
+    case 4: launch_decode<4, TG, 4, 4, EPI>(g, st); break;
+    case 5: launch_decode<4, TG, 8, 2, EPI>(g, st); break;
+    default: launch_decode<2, TG, 8, 2, EPI>(g, st); break;
   }
 }
 
-constexpr size_t kCounterBytes = 64 * 1024;  // room for 16384 N tiles
-
-StreamPlan plan_stream(int64_t M, int64_t N, int64_t K) {
-  StreamPlan p{};
-  p.mt = static_cast<int>((M + 15) / 16);
-  p.n_tiles = (N + kStreamRows - 1) / kStreamRows;
-  const int64_t ksteps = (K + kStreamStep - 1) / kStreamStep;
-  int64_t splits = (kStreamTargetBlocks + p.n_tiles - 1) / p.n_tiles;
-  splits = splits < 1 ? 1 : (splits > ksteps ? ksteps : splits);
-  int64_t kc = ((ksteps + splits - 1) / splits) * kStreamStep;
-  const int kcm = kc_max_for(p.mt);
-  if (kc > kcm) kc = kcm;
-  p.kc = static_cast<int>(kc);
-  p.splits = static_cast<int>((K + kc - 1) / kc);
-  p.ws_bytes = p.splits > 1 ? kCounterBytes + static_cast<size_t>(p.splits) * M * N * 4 : 0;
-  return p;
-}
-
-template <int MT, int EPI>
-void launch_stream(const GemmArgs& g, const StreamPlan& p, hipStream_t st) {
-  const int ldl = ((p.kc + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
-  const size_t lds = static_cast<size_t>(16 * MT) * ldl;
-  hipLaunchKernelGGL((stream_gemm_kernel<MT, EPI, DenseRows>),
-                     dim3(static_cast<unsigned>(p.n_tiles), static_cast<unsigned>(p.splits)),
-                     dim3(256), lds, st, g);
+int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
+  (void)N;
+  (void)K;
+  if (M <= 16) return 0;
+  return 5;
 }
 
 template <int EPI>
-void dispatch_stream(const GemmArgs& g, const StreamPlan& p, hipStream_t st) {
-  switch (p.mt) {
-    case 1: launch_stream<1, EPI>(g, p, st); break;
-    case 2: launch_stream<2, EPI>(g, p, st); break;
-    case 3: launch_stream<3, EPI>(g, p, st); break;
-    default: launch_stream<4, EPI>(g, p, st); break;
+void dispatch_decode(const GemmArgs& g, hipStream_t st) {
+  const int tg = static_cast<int>((g.M + 15) / 16);
+  int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+  if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(g.M, g.N, g.K);
+  switch (tg) {
+    case 1: decode_by_cfg<1, EPI>(cfg, g, st); break;
+    case 2: decode_by_cfg<2, EPI>(cfg, g, st); break;
+    case 3: decode_by_cfg<3, EPI>(cfg, g, st); break;
+    default: decode_by_cfg<4, EPI>(cfg, g, st); break;
   }
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, class Rows>
-void launch_tile(const GemmArgs& g, unsigned grid_y, hipStream_t st) {
-  using S = TileShape<BM, BN, WM, WN>;
-  auto kern = tile_gemm_kernel<BM, BN, WM, WN, EPI, Rows>;
-  static bool attr_set = false;  // per instantiation; benign race (idempotent)
+// -------------------------------------------------------------------- tile
+template <int BM, int BN, int BK, int WM, int WN, int EPI, class Rows>
+void launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  using S = TileShape<BM, BN, BK, WM, WN>;
+  auto kern = tile_gemm_kernel<BM, BN, BK, WM, WN, EPI, Rows>;
+  static bool attr_set = false;  // per instantiation; idempotent, so a race is benign
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds);
     attr_set = true;
   }
-  const unsigned gx = static_cast<unsigned>((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL(kern, dim3(gx, grid_y), dim3(256), S::kLds, st, g);
+  hipLaunchKernelGGL(kern, grid, dim3(256), S::kLds, st, g);
+}
+
+template <int BM, int BN, int WM, int WN, int NSTAGE, int EPI, class Rows>
+void launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  constexpr int kLds = NSTAGE * (BM + BN) * 64;
+  auto kern = tile3_gemm_kernel<BM, BN, WM, WN, NSTAGE, EPI, Rows>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(256), kLds, st, g);
+}
+
+// 0-4: register-staged tile core (any K % 16 == 0); 5-8: direct-to-LDS ring
+// (K % 64 == 0).
+struct TileCfg {
+  int bm, bn;
+  bool dma;
+};
+constexpr TileCfg kTileCfgs[] = {{256, 256, false}, {256, 256, false}, {128, 128, false},
+                                 {256, 128, false}, {128, 256, false}, {256, 256, true},
+                                 {256, 256, true},  {128, 128, true},  {256, 128, true}};
+constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
+
+// Pick the configuration with the smallest modelled time: waves of
+// resident tiles x per-wave tile area / relative efficiency (measured on
+// MI355X: the 256x256 DMA ring is ~10% faster per op than the 128x128 one
+// at K ~ 5K and ~30% faster at K ~ 17K, where its prologue/epilogue
+// amortise).  Shapes with K % 64 != 0 use the register-staged core.
+int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
+  if (K % 64 != 0) return 2;
+  struct Cand {
+    int cfg, per_cu;
+    double eff;
+  };
+  const Cand cands[] = {{6, 1, K > 8192 ? 1.3 : 1.1}, {7, 2, 1.0}};
+  int best = 7;
+  double best_cost = 1e300;
+  for (const Cand& c : cands) {
+    const TileCfg t = kTileCfgs[c.cfg];
+    const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    const int64_t slots = 256 * static_cast<int64_t>(c.per_cu);
+    const int64_t waves = (tiles + slots - 1) / slots;
+    const double cost = static_cast<double>(waves) * t.bm * t.bn * c.per_cu / c.eff;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = c.cfg;
+    }
+  }
+  return best;
 }
 
 template <int EPI>
 void dispatch_tile(const GemmArgs& g, hipStream_t st) {
-  const unsigned gy = static_cast<unsigned>((g.M + 127) / 128);
-  launch_tile<128, 128, 2, 2, EPI, DenseRows>(g, gy, st);
+  int cfg = g_tile_cfg.load(std::memory_order_relaxed);
+  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && g.K % 64 != 0))
+    cfg = default_tile_cfg(g.M, g.N, g.K);
+  const TileCfg c = kTileCfgs[cfg];
+  const unsigned tiles =
+      static_cast<unsigned>(((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn));
+  switch (cfg) {
+    case 0: launch_tile<256, 256, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 1: launch_tile<256, 256, 64, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 3: launch_tile<256, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 4: launch_tile<128, 256, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 5: launch_tile3<256, 256, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 6: launch_tile3<256, 256, 2, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 7: launch_tile3<128, 128, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 8: launch_tile3<256, 128, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* ws,
-                size_t ws_bytes, hipStream_t st, int epi) {
+                const void* bias, void* out, int64_t M, int64_t N, int64_t K, hipStream_t st,
+                int epi) {
   MW8_REQUIRE(A && W && out, kErrArg, "gemm: null A/W/out");
   MW8_REQUIRE(epi == kEpiI32 || (sa && sw), kErrArg, "gemm: null scales");
   MW8_REQUIRE(M >= 0 && N > 0 && K > 0, kErrShape, "gemm: bad sizes M=%lld N=%lld K=%lld",
@@ -103,23 +172,9 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
   g.bias = static_cast<const uint16_t*>(bias);
   g.out = out; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldo = N;
   g.top_k = 1;
-
-  if (M <= kStreamMaxM) {
-    const StreamPlan p = plan_stream(M, N, K);
-    if (p.splits > 1) {
-      MW8_REQUIRE(ws && ws_bytes >= p.ws_bytes, kErrWorkspace,
-                  "gemm: workspace of %zu bytes needed (got %zu); zero-fill it once at allocation",
-                  p.ws_bytes, ws_bytes);
-      MW8_REQUIRE(p.n_tiles * 4 <= static_cast<int64_t>(kCounterBytes), kErrShape,
-                  "gemm: N too large for the split-K counters");
-      MW8_REQUIRE(aligned16(ws), kErrAlign, "gemm: workspace needs 16-byte alignment");
-      g.counters = static_cast<int32_t*>(ws);
-      g.partials = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + kCounterBytes);
-    }
-    g.splits = p.splits;
-    g.kc = p.kc;
-    if (epi == kEpiBf16) dispatch_stream<kEpiBf16>(g, p, st);
-    else dispatch_stream<kEpiI32>(g, p, st);
+  if (M <= kDecodeMaxM) {
+    if (epi == kEpiBf16) dispatch_decode<kEpiBf16>(g, st);
+    else dispatch_decode<kEpiI32>(g, st);
   } else {
     if (epi == kEpiBf16) dispatch_tile<kEpiBf16>(g, st);
     else dispatch_tile<kEpiI32>(g, st);
@@ -129,33 +184,44 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > kStreamMaxM) return 0;
-  return plan_stream(M, N, K).ws_bytes;
+void set_tuning(int decode_cfg, int tile_cfg) {
+  g_decode_cfg.store(decode_cfg, std::memory_order_relaxed);
+  g_tile_cfg.store(tile_cfg, std::memory_order_relaxed);
 }
 
+size_t gemm_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
+
 int gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                   const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,
-                   size_t ws_bytes, hipStream_t st) {
-  return gemm_common(A, sa, W, sw, bias, y, M, N, K, ws, ws_bytes, st, kEpiBf16);
+                   const void* bias, void* y, int64_t M, int64_t N, int64_t K, void*, size_t,
+                   hipStream_t st) {
+  return gemm_common(A, sa, W, sw, bias, y, M, N, K, st, kEpiBf16);
 }
 
 int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int64_t N,
-                  int64_t K, void* ws, size_t ws_bytes, hipStream_t st) {
-  return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, ws, ws_bytes, st, kEpiI32);
+                  int64_t K, void*, size_t, hipStream_t st) {
+  return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, st, kEpiI32);
 }
 
-// Exposed for the grouped GEMM (moe.hip): tile core over expert-sorted rows.
-void launch_grouped_tile_bf16(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
-void launch_grouped_tile_i32(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
-
-void launch_grouped_tile_bf16(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st) {
-  if (bm == 64) launch_tile<64, 128, 2, 2, kEpiBf16, SortedRows>(g, blocks, st);
-  else launch_tile<128, 128, 2, 2, kEpiBf16, SortedRows>(g, blocks, st);
+// Grouped (fused-MoE) GEMM launchers over expert-sorted rows.
+void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.N + 127) / 128), blocks);
+  if (epi == kEpiBf16) {
+    if (bm == 64) launch_tile<64, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+    else launch_tile<128, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+  } else {
+    if (bm == 64) launch_tile<64, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+    else launch_tile<128, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+  }
 }
-void launch_grouped_tile_i32(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st) {
-  if (bm == 64) launch_tile<64, 128, 2, 2, kEpiI32, SortedRows>(g, blocks, st);
-  else launch_tile<128, 128, 2, 2, kEpiI32, SortedRows>(g, blocks, st);
+
+void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {
+  const int ldl = static_cast<int>(((g.K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16);
+  const size_t lds = static_cast<size_t>(16) * ldl;
+  const dim3 grid(static_cast<unsigned>((g.N + kStreamRows - 1) / kStreamRows), blocks);
+  if (epi == kEpiBf16)
+    hipLaunchKernelGGL(grouped_stream_kernel<kEpiBf16>, grid, dim3(256), lds, st, g);
+  else
+    hipLaunchKernelGGL(grouped_stream_kernel<kEpiI32>, grid, dim3(256), lds, st, g);
 }
 
 }  // namespace mw8

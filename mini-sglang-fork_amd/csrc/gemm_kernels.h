@@ -7,17 +7,19 @@
 //   W  int8 [N, K]      weights (per expert: base + e * N * K)
 //   out[row, n]         bf16 (scaled epilogue) or int32 (raw accumulators)
 //
-// Two cores:
+// Cores:
 //   tile_core   -- large M (prefill): BM x BN x 128 block tile, 4 waves, each
 //                  wave a (BM/WM) x (BN/WN) tile of v_mfma_i32_32x32x32_i8,
 //                  A/W tiles double-buffered in LDS with an XOR swizzle of
 //                  16-byte chunks (chunk ^ (row & 7)) so that the 32 rows
 //                  read by one MFMA fragment load hit distinct banks.
-//   stream_core -- small M (decode): weight streaming with
+//   decode_gemm_kernel   -- dense small M (decode): weight streaming with
 //                  v_mfma_i32_16x16x64_i8, weight rows as the MFMA "A"
-//                  operand (read straight from HBM into registers, 64
-//                  contiguous bytes per lane per 256-K step) and up to 64
-//                  tokens as the "B" operand staged once per block in LDS.
+//                  operand read straight from HBM into registers, up to 64
+//                  tokens as the "B" operand, K split across the waves of a
+//                  block and reduced in LDS.
+//   grouped_stream_kernel -- the same streaming idea for 16-row expert
+//                  blocks of the fused-MoE GEMM (token rows gathered in LDS).
 //
 // MFMA lane layouts (checked on gfx950 by an in-bounds probe):
 //   32x32x32: lane l feeds A row l%32 / B col l%32 with 16 K-bytes of group
@@ -53,11 +55,6 @@ struct GemmArgs {
   int64_t num_valid;           // M * top_k
   int32_t top_k;
   int32_t num_experts;         // blocks owned by an id outside [0, E) are skipped
-  // split-K (stream core, dense only)
-  int32_t* partials;  // [splits][M][N]
-  int32_t* counters;  // [n_tiles], zero between calls
-  int32_t splits;
-  int32_t kc;         // K per split (multiple of 256)
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -81,55 +78,92 @@ struct SortedRows {
 // ------------------------------------------------------------------------
 // Large-M tile core
 // ------------------------------------------------------------------------
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN>
 struct TileShape {
-  static constexpr int kBK = 128;                    // K bytes per stage
+  static constexpr int kBK = BK;                     // K bytes per stage
+  static constexpr int kChunksK = BK / 16;           // 16-byte chunks per tile row
   static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
   static constexpr int kFM = kWaveM / 32, kFN = kWaveN / 32;
-  static constexpr int kAChunks = BM * kBK / 16 / 256;  // 16-byte chunks per thread
-  static constexpr int kBChunks = BN * kBK / 16 / 256;
-  static constexpr int kLdsA = BM * kBK, kLdsB = BN * kBK;
+  static constexpr int kAChunks = BM * BK / 16 / 256;  // 16-byte chunks per thread
+  static constexpr int kBChunks = BN * BK / 16 / 256;
+  static constexpr int kLdsA = BM * BK, kLdsB = BN * BK;
   static constexpr int kLds = 2 * (kLdsA + kLdsB);
+  static_assert(BK == 64 || BK == 128, "BK is 64 or 128 bytes");
   static_assert(WM * WN == 4, "4 waves per block");
   static_assert(kFM >= 1 && kFN >= 1, "wave tile must hold one 32x32 MFMA");
   static_assert(kAChunks >= 1 && kBChunks >= 1, "tile too small");
 };
 
+// LDS byte offset of 16-byte chunk c of tile row r.  The chunk index is
+// XOR-swizzled with low row bits so that the 8 rows read together by one
+// phase of a ds_read_b128 fragment load land in 8 different bank groups.
+template <int BK>
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return row * 128 + ((chunk ^ (row & 7)) << 4);
+  if constexpr (BK == 128) return row * 128 + ((chunk ^ (row & 7)) << 4);
+  else return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, class Rows>
+// Tile order for dense launches (1-D grid of tiles_m * tiles_n blocks).
+// The hardware hands block b to XCD b % 8; each XCD is given a contiguous
+// range of tile ids so that the tiles running together on one XCD share
+// its L2.  Inside the range tiles follow a grouped raster: kGroupM tile
+// rows advance together along N, so one wave of concurrent tiles reuses
+// kGroupM A panels and a handful of W panels.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ void tile_of_block(int64_t b, int64_t tiles_m, int64_t tiles_n,
+                                              int64_t& pid_m, int64_t& pid_n) {
+  const int64_t T = tiles_m * tiles_n;
+  const int64_t xcd = b % kXcds, local = b / kXcds;
+  const int64_t base = T / kXcds, rem = T % kXcds;
+  const int64_t t = xcd * base + (xcd < rem ? xcd : rem) + local;
+  const int64_t per_group = kGroupM * tiles_n;
+  const int64_t group = t / per_group;
+  const int64_t first_m = group * kGroupM;
+  const int64_t gsize = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const int64_t in_group = t % per_group;
+  pid_m = first_m + in_group % gsize;
+  pid_n = in_group / gsize;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int EPI, class Rows>
 __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
-  using S = TileShape<BM, BN, WM, WN>;
+  using S = TileShape<BM, BN, BK, WM, WN>;
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // ---- which tile: x = N tiles (fastest), y = M tiles / expert blocks
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
-  const int64_t mblk = blockIdx.y;
   const int8_t* W = g.W;
   const float* sw = g.sw;
-  int64_t m0 = mblk * BM;
+  int64_t m0, n0, mblk = 0;
   if constexpr (Rows::kGrouped) {
+    // 2-D grid: x = N tiles, y = expert blocks of BM sorted rows
+    n0 = static_cast<int64_t>(blockIdx.x) * BN;
+    mblk = blockIdx.y;
+    m0 = mblk * BM;
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
     const int e = g.expert_ids[mblk];
     if (e < 0 || e >= g.num_experts) return;
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
+  } else {
+    int64_t pm, pn;
+    tile_of_block(blockIdx.x, (g.M + BM - 1) / BM, (g.N + BN - 1) / BN, pm, pn);
+    m0 = pm * BM;
+    n0 = pn * BN;
   }
 
-  // ---- per-thread global source rows for the A and W chunks it loads.
-  // Chunk id = tid + 256 * i -> row id / 8, 16-byte column id % 8 (= tid % 8).
-  const int cc = tid & 7;
+  // ---- per-thread global sources of the 16-byte chunks this thread stages:
+  // chunk id = tid + 256 * i -> tile row id / kChunksK, column id % kChunksK.
+  const int cc = tid % S::kChunksK;
   const int8_t* a_src[S::kAChunks];
   const int8_t* w_src[S::kBChunks];
   int a_lds[S::kAChunks], w_lds[S::kBChunks];
 #pragma unroll
   for (int i = 0; i < S::kAChunks; ++i) {
-    const int r = (tid + 256 * i) >> 3;
+    const int r = (tid + 256 * i) / S::kChunksK;
     int64_t arow;
     if constexpr (Rows::kGrouped) {
       const int32_t p = g.sorted_ids[m0 + r];
@@ -138,14 +172,14 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
       arow = m0 + r < g.M ? m0 + r : g.M - 1;
     }
     a_src[i] = g.A + arow * g.lda + 16 * cc;
-    a_lds[i] = swz(r, cc);
+    a_lds[i] = swz<BK>(r, cc);
   }
 #pragma unroll
   for (int i = 0; i < S::kBChunks; ++i) {
-    const int r = (tid + 256 * i) >> 3;
+    const int r = (tid + 256 * i) / S::kChunksK;
     const int64_t wrow = n0 + r < g.N ? n0 + r : g.N - 1;
     w_src[i] = W + wrow * g.K + 16 * cc;
-    w_lds[i] = swz(r, cc);
+    w_lds[i] = swz<BK>(r, cc);
   }
 
   v16i acc[S::kFM][S::kFN];
@@ -154,11 +188,11 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < S::kFN; ++j) acc[i][j] = v16i{0};
 
-  const int nk = static_cast<int>((g.K + S::kBK - 1) / S::kBK);
+  const int nk = static_cast<int>((g.K + BK - 1) / BK);
   v4i ra[S::kAChunks], rb[S::kBChunks];
 
   auto gload = [&](int kt) {
-    const int64_t k0 = static_cast<int64_t>(kt) * S::kBK;
+    const int64_t k0 = static_cast<int64_t>(kt) * BK;
     const bool in = k0 + 16 * cc < g.K;  // K % 16 == 0: chunks are all-in or all-out
 #pragma unroll
     for (int i = 0; i < S::kAChunks; ++i)
@@ -186,15 +220,15 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
     const unsigned char* la = lds + buf * (S::kLdsA + S::kLdsB);
     const unsigned char* lb = la + S::kLdsA;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < BK / 32; ++ks) {
       const int ch = 2 * ks + fgrp;
       v4i fa[S::kFM], fb[S::kFN];
 #pragma unroll
       for (int i = 0; i < S::kFM; ++i)
-        fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * S::kWaveM + 32 * i + frow, ch));
+        fa[i] = *reinterpret_cast<const v4i*>(la + swz<BK>(wm * S::kWaveM + 32 * i + frow, ch));
 #pragma unroll
       for (int j = 0; j < S::kFN; ++j)
-        fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * S::kWaveN + 32 * j + frow, ch));
+        fb[j] = *reinterpret_cast<const v4i*>(lb + swz<BK>(wn * S::kWaveN + 32 * j + frow, ch));
 #pragma unroll
       for (int i = 0; i < S::kFM; ++i)
 #pragma unroll
@@ -244,92 +278,273 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
-// Small-M weight-streaming core (dense decode and grouped small blocks)
+// Large-M tile core v3: direct-to-LDS loads, NSTAGE-deep ring, BK = 64
 // ------------------------------------------------------------------------
-// Block = 4 waves = 64 weight rows; wave w owns rows n0 + 16w .. +16.
-// MT groups of 16 tokens (MT <= 4) share every weight fragment.
-// Dense: grid (N/64, splits); the K range [split*kc, +kc) is reduced across
-// splits through int32 partials and a per-N-tile arrival counter; the last
-// block to arrive applies the epilogue and re-arms the counter.
-// Grouped: grid (N/64, expert blocks of 16 sorted rows); no split.
-constexpr int kStreamRows = 64;
-constexpr int kStreamStep = 256;  // K bytes per lane step (4 MFMAs)
-
-template <int MT>
-__host__ __device__ constexpr int stream_kc_max() {
-  // keep the LDS token panel at or below 40 KB (4 blocks per CU)
-  return (((40960 / (16 * MT)) - 16) / kStreamStep) * kStreamStep;
+// Every K step of 64 bytes, each wave moves its share of the A and W tiles
+// straight from global memory into LDS with global_load_lds_dwordx4 (one
+// 1 KB contiguous LDS run per wave instruction; lane l fills 16-byte unit
+// l of it, and is pointed at the global chunk that belongs there under the
+// swizzle).  Stages are prefetched NSTAGE-1 K steps ahead and tracked with
+// explicit vmcnt waits; one s_barrier per K step.  MFMA fragments are read
+// from LDS one half-step ahead of the MFMAs that consume them (two register
+// sets F0/F1), so LDS latency hides behind 16 MFMAs.  Requires K % 64 == 0.
+//
+// LDS row = 64 bytes = 4 chunks; chunk c of row r sits at unit
+// r*4 + (c ^ f(r)), f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the 8 (and
+// 16) rows read together by a fragment load on distinct 16-byte bank groups.
+__device__ __forceinline__ int swz64(int row, int chunk) {
+  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
-template <int MT, int EPI, class Rows>
-__global__ __launch_bounds__(256) void stream_gemm_kernel(GemmArgs g) {
+// s_waitcnt vmcnt(n) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+template <int L, int MAXS>
+__device__ __forceinline__ void wait_stages(int n) {  // at most n (<= MAXS) stages in flight
+  if constexpr (MAXS >= 3) { if (n >= 3) { wait_vmcnt<3 * L>(); return; } }
+  if constexpr (MAXS >= 2) { if (n == 2) { wait_vmcnt<2 * L>(); return; } }
+  if constexpr (MAXS >= 1) { if (n == 1) { wait_vmcnt<L>(); return; } }
+  wait_vmcnt<0>();
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Workgroup barrier without the release/acquire fence of __syncthreads()
+// (which would force vmcnt(0) and drain the prefetch ring).  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int NSTAGE, int EPI, class Rows>
+__global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
+  // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
+  // pass only needs the launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
+  constexpr int kFM = kWaveM / 32, kFN = kWaveN / 32;
+  constexpr int kStageA = BM * 64, kStageB = BN * 64, kStage = kStageA + kStageB;
+  constexpr int kLA = BM / 64, kLB = BN / 64;  // DMA instructions per wave per stage
+  constexpr int kL = kLA + kLB;
+  static_assert(WM * WN == 4 && kFM >= 1 && kFN >= 1 && kLA >= 1 && kLB >= 1, "shape");
+  static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStreamRows;
+  const int wm = wave / WN, wn = wave % WN;
+
   const int8_t* W = g.W;
   const float* sw = g.sw;
-  int64_t k_begin = 0, k_end = g.K;
-  int64_t m0 = 0;
+  int64_t m0, n0;
   if constexpr (Rows::kGrouped) {
-    m0 = static_cast<int64_t>(blockIdx.y) * 16;
+    n0 = static_cast<int64_t>(blockIdx.x) * BN;
+    m0 = static_cast<int64_t>(blockIdx.y) * BM;
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
     const int e = g.expert_ids[blockIdx.y];
     if (e < 0 || e >= g.num_experts) return;
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
   } else {
-    k_begin = static_cast<int64_t>(blockIdx.y) * g.kc;
-    k_end = k_begin + g.kc < g.K ? k_begin + g.kc : g.K;
+    int64_t pm, pn;
+    tile_of_block(blockIdx.x, (g.M + BM - 1) / BM, (g.N + BN - 1) / BN, pm, pn);
+    m0 = pm * BM;
+    n0 = pn * BN;
   }
-  const int kc = static_cast<int>(k_end - k_begin);
+
+  // ---- per-lane DMA sources: instruction j of this wave fills LDS units
+  // (j*4 + wave)*64 .. +63 of the tile, i.e. 16 rows; lane -> (row, chunk)
+  const int8_t* a_src[kLA];
+  const int8_t* w_src[kLB];
+#pragma unroll
+  for (int j = 0; j < kLA; ++j) {
+    const int unit = (j * 4 + wave) * 64 + lane, row = unit >> 2;
+    const int c = (unit & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
+    int64_t arow;
+    if constexpr (Rows::kGrouped) {
+      const int32_t p = g.sorted_ids[m0 + row];
+      arow = p < g.num_valid ? p / g.top_k : 0;
+    } else {
+      arow = m0 + row < g.M ? m0 + row : g.M - 1;
+    }
+    a_src[j] = g.A + arow * g.lda + 16 * c;
+  }
+#pragma unroll
+  for (int j = 0; j < kLB; ++j) {
+    const int unit = (j * 4 + wave) * 64 + lane, row = unit >> 2;
+    const int c = (unit & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
+    const int64_t wrow = n0 + row < g.N ? n0 + row : g.N - 1;
+    w_src[j] = W + wrow * g.K + 16 * c;
+  }
+  auto issue = [&](int kt) {
+    unsigned char* base = lds + (kt % NSTAGE) * kStage;
+    const int64_t k0 = static_cast<int64_t>(kt) * 64;
+#pragma unroll
+    for (int j = 0; j < kLA; ++j)
+      __builtin_amdgcn_global_load_lds(a_src[j] + k0, (lds_ptr_t)(base + (j * 4 + wave) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kLB; ++j)
+      __builtin_amdgcn_global_load_lds(w_src[j] + k0, (lds_ptr_t)(base + kStageA + (j * 4 + wave) * 1024), 16, 0, 0);
+  };
+
+  const int frow = lane & 31, fgrp = lane >> 5;
+  int a_off[kFM], b_off[kFN];  // row byte offsets of this lane's fragment rows
+#pragma unroll
+  for (int i = 0; i < kFM; ++i) a_off[i] = wm * kWaveM + 32 * i + frow;
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) b_off[j] = wn * kWaveN + 32 * j + frow;
+  v4i fa[2][kFM], fb[2][kFN];
+  auto read_frags = [&](int kt, int ks) {
+    const unsigned char* la = lds + (kt % NSTAGE) * kStage;
+    const unsigned char* lb = la + kStageA;
+    const int ch = 2 * ks + fgrp;
+#pragma unroll
+    for (int i = 0; i < kFM; ++i) fa[ks][i] = *reinterpret_cast<const v4i*>(la + swz64(a_off[i], ch));
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) fb[ks][j] = *reinterpret_cast<const v4i*>(lb + swz64(b_off[j], ch));
+  };
+
+  v16i acc[kFM][kFN];
+#pragma unroll
+  for (int i = 0; i < kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) acc[i][j] = v16i{0};
+  auto mfmas = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+  };
+
+  const int nk = static_cast<int>(g.K / 64);
+  // prologue: stages 0 .. NSTAGE-1 in flight, stage 0 landed, its fragments read
+#pragma unroll
+  for (int s = 0; s < NSTAGE; ++s)
+    if (s < nk) issue(s);
+  wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
+  raw_barrier();
+  read_frags(0, 0);
+  read_frags(0, 1);
+
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    mfmas(0);
+    // stage kt+1 landed everywhere; every wave holds stage kt in registers
+    const int later = nk - 2 - kt;  // stages after kt+1 already issued
+    wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
+    raw_barrier();
+    if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+    read_frags(kt + 1, 0);
+    mfmas(1);
+    read_frags(kt + 1, 1);
+  }
+  mfmas(0);
+  mfmas(1);
+
+  // ---- epilogue: lane holds column (lane & 31) of each 32x32 block
+#pragma unroll
+  for (int i = 0; i < kFM; ++i) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+      int64_t orow, arow;
+      bool rvalid;
+      float routed = 1.0f;
+      if constexpr (Rows::kGrouped) {
+        const int32_t p = g.sorted_ids[m0 + r];
+        rvalid = p < g.num_valid;
+        orow = p;
+        arow = rvalid ? p / g.top_k : 0;
+        if (rvalid && g.topk_w) routed = g.topk_w[p];
+      } else {
+        orow = m0 + r;
+        arow = orow;
+        rvalid = orow < g.M;
+      }
+      if (!rvalid) continue;
+      const float sa = EPI == kEpiBf16 ? g.sa[arow] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        const int64_t n = n0 + wn * kWaveN + 32 * j + frow;
+        if (n >= g.N) continue;
+        const int32_t a = acc[i][j][v];
+        if constexpr (EPI == kEpiBf16) {
+          static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
+              epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr);
+        } else {
+          static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
+        }
+      }
+    }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// ------------------------------------------------------------------------
+// Grouped small-block core (fused-MoE decode): weight streaming
+// ------------------------------------------------------------------------
+// Block = 4 waves = 64 weight rows of one expert; wave w owns rows
+// n0 + 16w .. +16.  The block's 16 sorted (token, slot) rows are gathered
+// once into an LDS panel [16][K] (zeros for padding rows); per 256-K step a
+// lane streams 64 contiguous weight bytes (4 x 16 B) from HBM into
+// registers and issues 4 v_mfma_i32_16x16x64_i8 with the weight rows as
+// the MFMA rows.  Grid (N/64, expert blocks); blocks past the padded count
+// exit on the device-side count.
+constexpr int kStreamRows = 64;
+constexpr int kStreamStep = 256;  // K bytes per lane step (4 MFMAs)
+
+template <int EPI>
+__global__ __launch_bounds__(256) void grouped_stream_kernel(GemmArgs g) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStreamRows;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16;
+  if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
+  const int e = g.expert_ids[blockIdx.y];
+  if (e < 0 || e >= g.num_experts) return;
+  const int8_t* W = g.W + static_cast<int64_t>(e) * g.N * g.K;
+  const float* sw = g.sw + static_cast<int64_t>(e) * g.N;
+  const int kc = static_cast<int>(g.K);
   const int kc_pad = ((kc + kStreamStep - 1) / kStreamStep) * kStreamStep;
   const int ldl = kc_pad + 16;  // padded LDS row: 16 token rows hit 16 bank groups
 
-  // ---- stage the token panel [16*MT][kc] in LDS (zeros outside)
+  // ---- gather the block's 16 token rows into LDS (zeros outside)
   {
     const int chunks_per_row = kc_pad / 16;
-    for (int id = tid; id < 16 * MT * chunks_per_row; id += 256) {
+    for (int id = tid; id < 16 * chunks_per_row; id += 256) {
       const int r = id / chunks_per_row, c = id % chunks_per_row;
-      int64_t arow = -1;
-      if constexpr (Rows::kGrouped) {
-        const int32_t p = g.sorted_ids[m0 + r];
-        if (p < g.num_valid) arow = p / g.top_k;
-      } else {
-        if (r < g.M) arow = r;
-      }
+      const int32_t p = g.sorted_ids[m0 + r];
       v4i v = v4i{0};
-      if (arow >= 0 && 16 * c < kc) v = *reinterpret_cast<const v4i*>(g.A + arow * g.lda + k_begin + 16 * c);
+      if (p < g.num_valid && 16 * c < kc)
+        v = *reinterpret_cast<const v4i*>(g.A + static_cast<int64_t>(p / g.top_k) * g.lda + 16 * c);
       *reinterpret_cast<v4i*>(lds + r * ldl + 16 * c) = v;
     }
   }
   __syncthreads();
 
-  // ---- stream the weights
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t wrow = n0 + 16 * wave + r16;
-  const int8_t* wp = W + (wrow < g.N ? wrow : g.N - 1) * g.K + k_begin + 64 * grp;
-  v4i acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = v4i{0};
-
+  const int8_t* wp = W + (wrow < g.N ? wrow : g.N - 1) * g.K + 64 * grp;
+  v4i acc = v4i{0};
   const int steps = kc_pad / kStreamStep;
   int s = 0;
   for (; s + 2 <= steps; s += 2) {
     v4i w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int kk = (j >> 2) * kStreamStep + 16 * (j & 3);
-      const int koff = s * kStreamStep + kk;
+      const int koff = s * kStreamStep + (j >> 2) * kStreamStep + 16 * (j & 3);
       w[j] = (koff + 64 * grp < kc) ? *reinterpret_cast<const v4i*>(wp + koff) : v4i{0};
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kk = (s + (j >> 2)) * kStreamStep + 64 * grp + 16 * (j & 3);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const v4i b = *reinterpret_cast<const v4i*>(lds + (16 * t + r16) * ldl + kk);
-        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc[t], 0, 0, 0);
-      }
+      const v4i b = *reinterpret_cast<const v4i*>(lds + r16 * ldl + kk);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc, 0, 0, 0);
     }
   }
   for (; s < steps; ++s) {
@@ -342,89 +557,115 @@ __global__ __launch_bounds__(256) void stream_gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kk = s * kStreamStep + 64 * grp + 16 * j;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const v4i b = *reinterpret_cast<const v4i*>(lds + (16 * t + r16) * ldl + kk);
-        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc[t], 0, 0, 0);
-      }
+      const v4i b = *reinterpret_cast<const v4i*>(lds + r16 * ldl + kk);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc, 0, 0, 0);
     }
   }
 
-  // D reg v of lane l: weight row n0 + 16*wave + 4*(l/16) + v, token 16*t + l%16
+  // D reg v of lane l: weight row n0 + 16*wave + 4*(l/16) + v, token row l%16
   const int64_t nb = n0 + 16 * wave + 4 * grp;
-  if constexpr (Rows::kGrouped) {
+  const int32_t p = g.sorted_ids[m0 + r16];
+  if (p >= g.num_valid) return;
+  const int64_t arow = p / g.top_k;
+  const float sa = EPI == kEpiBf16 ? g.sa[arow] : 0.0f;
+  const float routed = g.topk_w ? g.topk_w[p] : 1.0f;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int32_t p = g.sorted_ids[m0 + 16 * t + r16];
-      if (p >= g.num_valid) continue;
-      const int64_t arow = p / g.top_k;
-      const float sa = EPI == kEpiBf16 ? g.sa[arow] : 0.0f;
-      const float routed = g.topk_w ? g.topk_w[p] : 1.0f;
+  for (int v = 0; v < 4; ++v) {
+    const int64_t n = nb + v;
+    if (n >= g.N) continue;
+    if constexpr (EPI == kEpiBf16)
+      static_cast<uint16_t*>(g.out)[p * g.ldo + n] =
+          epi_bf16(acc[v], sa, sw[n], nullptr, n, routed, g.topk_w != nullptr);
+    else
+      static_cast<int32_t*>(g.out)[p * g.ldo + n] = acc[v];
+  }
+}
+
+// ------------------------------------------------------------------------
+// Dense small-M core: weight streaming with in-block split-K
+// ------------------------------------------------------------------------
+// Block = WAVES waves over the same RG*16 weight rows; wave w accumulates
+// the 64-byte K steps [w*S/WAVES, (w+1)*S/WAVES) of all of them, then the
+// WAVES partial accumulators are summed with LDS integer atomics (exact and
+// order-free) and the epilogue runs once.  No global atomics, fences or
+// workspace.  Per 64-K step lane (r16, grp) loads 16 bytes of each of its
+// RG weight rows and of each of its TG token rows (tokens read straight from
+// L2: the int8 activation matrix is small), then issues RG*TG
+// v_mfma_i32_16x16x64_i8 with the weight rows as the MFMA rows.  U steps
+// of loads are issued before their MFMAs to keep bytes in flight.
+template <int RG, int TG, int WAVES, int U, int EPI>
+__global__ __launch_bounds__(64 * WAVES) void decode_gemm_kernel(GemmArgs g) {
+  constexpr int kAcc = RG * TG * 4;  // int32 accumulators per lane
+  __shared__ int32_t red[kAcc][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
+  __syncthreads();
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * RG);
+  const int64_t steps = (g.K + 63) / 64;
+  const int64_t s_begin = steps * wave / WAVES, s_end = steps * (wave + 1) / WAVES;
+
+  const int8_t* wp[RG];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t n = nb + v;
-        if (n >= g.N) continue;
-        if constexpr (EPI == kEpiBf16)
-          static_cast<uint16_t*>(g.out)[p * g.ldo + n] =
-              epi_bf16(acc[t][v], sa, sw[n], nullptr, n, routed, g.topk_w != nullptr);
-        else
-          static_cast<int32_t*>(g.out)[p * g.ldo + n] = acc[t][v];
-      }
+  for (int rg = 0; rg < RG; ++rg) {
+    const int64_t n = n0 + 16 * rg + r16;
+    wp[rg] = g.W + (n < g.N ? n : g.N - 1) * g.K + 16 * grp;
+  }
+  const int8_t* xp[TG];
+  bool xok[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    const int64_t m = 16 * tg + r16;
+    xok[tg] = m < g.M;
+    xp[tg] = g.A + (xok[tg] ? m : 0) * g.lda + 16 * grp;
+  }
+  v4i acc[RG][TG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) acc[rg][tg] = v4i{0};
+
+  for (int64_t s0 = s_begin; s0 < s_end; s0 += U) {
+    v4i wv[U][RG], xv[U][TG];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = (s0 + u) * 64 + 16 * grp;
+      const bool in = (s0 + u < s_end) && (k < g.K);
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+        wv[u][rg] = in ? *reinterpret_cast<const v4i*>(wp[rg] + (s0 + u) * 64) : v4i{0};
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg)
+        xv[u][tg] = (in && xok[tg]) ? *reinterpret_cast<const v4i*>(xp[tg] + (s0 + u) * 64) : v4i{0};
     }
-    return;
-  } else {
-    if (g.splits == 1) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int64_t m = 16 * t + r16;
-        if (m >= g.M) continue;
-        const float sa = EPI == kEpiBf16 ? g.sa[m] : 0.0f;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t n = nb + v;
-          if (n >= g.N) continue;
-          if constexpr (EPI == kEpiBf16)
-            static_cast<uint16_t*>(g.out)[m * g.ldo + n] =
-                epi_bf16(acc[t][v], sa, sw[n], g.bias, n, 1.0f, false);
-          else
-            static_cast<int32_t*>(g.out)[m * g.ldo + n] = acc[t][v];
-        }
-      }
-      return;
-    }
-    // ---- split-K: publish partials, last arriving block reduces
-    int32_t* part = g.partials + static_cast<int64_t>(blockIdx.y) * g.M * g.N;
+      for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int64_t m = 16 * t + r16;
-      if (m >= g.M) continue;
+        for (int tg = 0; tg < TG; ++tg)
+          acc[rg][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[u][rg], xv[u][tg], acc[rg][tg], 0, 0, 0);
+  }
+
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (nb + v < g.N) part[m * g.N + nb + v] = acc[t][v];
-    }
-    __threadfence();
-    __syncthreads();
-    __shared__ int last;
-    if (tid == 0) {
-      const int old = atomicAdd(g.counters + blockIdx.x, 1);
-      last = (old == g.splits - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const int64_t ncols = g.N - n0 < kStreamRows ? g.N - n0 : kStreamRows;
-    for (int64_t id = tid; id < g.M * kStreamRows; id += 256) {
-      const int64_t m = id / kStreamRows, n = n0 + id % kStreamRows;
-      if (id % kStreamRows >= ncols) continue;
-      int32_t a = 0;
-      for (int sp = 0; sp < g.splits; ++sp)
-        a += g.partials[(static_cast<int64_t>(sp) * g.M + m) * g.N + n];
-      if constexpr (EPI == kEpiBf16)
-        static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], sw[n], g.bias, n, 1.0f, false);
-      else
-        static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
-    }
-    if (tid == 0) g.counters[blockIdx.x] = 0;
+  for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) atomicAdd(&red[(rg * TG + tg) * 4 + v][lane], acc[rg][tg][v]);
+  __syncthreads();
+  // every thread of the block finalises (accumulator index j, lane l) pairs
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) {
+    const int j = e >> 6, l = e & 63;
+    const int32_t a = red[j][l];
+    const int rg = j / (TG * 4), tg = (j / 4) % TG, v = j & 3;
+    const int64_t n = n0 + 16 * rg + 4 * (l >> 4) + v;
+    const int64_t m = 16 * tg + (l & 15);
+    if (n >= g.N || m >= g.M) continue;
+    if constexpr (EPI == kEpiBf16)
+      static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
+    else
+      static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
   }
 }
 

@@ -5,8 +5,8 @@
 
 namespace mw8 {
 
-void launch_grouped_tile_bf16(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
-void launch_grouped_tile_i32(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
+void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
+void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
 
 namespace {
 
@@ -281,21 +281,13 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
   g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
-  g.splits = 1; g.kc = static_cast<int>(K);
   if (bsz == 16) {
-    const int ldl = static_cast<int>(((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16);
-    const size_t lds = static_cast<size_t>(16) * ldl;
-    MW8_REQUIRE(lds <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",
+    const int64_t ldl = ((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
+    MW8_REQUIRE(16 * ldl <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",
                 (long long)K);
-    const dim3 grid(static_cast<unsigned>((N + kStreamRows - 1) / kStreamRows),
-                    static_cast<unsigned>(blocks));
-    if (epi == kEpiBf16)
-      hipLaunchKernelGGL((stream_gemm_kernel<1, kEpiBf16, SortedRows>), grid, dim3(256), lds, st, g);
-    else
-      hipLaunchKernelGGL((stream_gemm_kernel<1, kEpiI32, SortedRows>), grid, dim3(256), lds, st, g);
+    launch_grouped_stream(g, static_cast<unsigned>(blocks), epi, st);
   } else {
-    if (epi == kEpiBf16) launch_grouped_tile_bf16(g, static_cast<unsigned>(blocks), bsz, st);
-    else launch_grouped_tile_i32(g, static_cast<unsigned>(blocks), bsz, st);
+    launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);
   }
   return check_launch("moe_gemm");
 }

@@ -154,3 +154,48 @@ def test_linear_layers_drop_in():
                 None if layer.bias is None else f32(sd["bias"]),
             )
             assert bf16_bits_equal(y, y_ref).all()
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 640, 520), (257, 1024, 300), (129, 192, 64), (1000, 2048, 1000)])
+def test_gemm_every_tile_config(M, K, N):
+    """Each large-M configuration (forced through mw8_set_tuning) on ragged
+    shapes; K % 64 != 0 makes the direct-to-LDS configs fall back."""
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm all tile cfgs M={M} K={K} N={N}")
+    c = linear_case(M, K, N, seed=M)
+    q, s = quant_per_token(c["x"].to(DEV))
+    w, s_w = c["w"].to(DEV), c["s_w"].to(DEV)
+    q_ref, s_ref = orc.quant_per_token(f32(c["x"]))
+    acc_ref = orc.gemm_i32(q_ref, c["w"].numpy())
+    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
+    lib = load()
+    try:
+        for cfg in range(9):
+            lib.mw8_set_tuning(-1, cfg)
+            np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
+            assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
+    finally:
+        lib.mw8_set_tuning(-1, -1)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 64])
+def test_gemm_every_decode_config(M):
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm all decode cfgs M={M}")
+    K, N = 1344, 336  # K not a multiple of 256, N not a multiple of 64
+    c = linear_case(M, K, N, seed=M)
+    q, s = quant_per_token(c["x"].to(DEV))
+    w, s_w = c["w"].to(DEV), c["s_w"].to(DEV)
+    q_ref, s_ref = orc.quant_per_token(f32(c["x"]))
+    acc_ref = orc.gemm_i32(q_ref, c["w"].numpy())
+    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
+    lib = load()
+    try:
+        for cfg in range(7):
+            lib.mw8_set_tuning(cfg, -1)
+            np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
+            assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
+    finally:
+        lib.mw8_set_tuning(-1, -1)
