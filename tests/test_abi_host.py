@@ -1,0 +1,190 @@
+"""CPU tests of the drop-in boundary: libmw8.so loads and exports every
+symbol include/mw8.h declares, argument validation returns the documented
+error codes before any GPU work, and the host-side mirror of the reference
+interface (registry, BaseOP state dicts, layer shapes, MoE regimes)
+behaves like the reference.  No GPU compute happens here."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from minisgl_amd.kernel import lib as mw8lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mw8.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mw8_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return mw8lib.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for n in ("mw8_quant_per_token_bf16", "mw8_gemm_w8a8_bf16", "mw8_moe_align_block_size",
+              "mw8_moe_gemm_w8a8_bf16", "mw8_moe_sum_reduce_bf16", "mw8_topk_softmax"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(mw8lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(raw, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_header():
+    assert set(_declared()) == set(mw8lib.SIGNATURES)
+
+
+def test_version_and_pure_host_helpers(lib):
+    assert lib.mw8_version() >= 100
+    # python/minisgl/moe/fused.py:73: numel + (E + 1) * (B - 1)
+    assert lib.mw8_moe_align_max_padded(12, 5, 4) == 27
+    assert lib.mw8_moe_align_max_padded(128, 129, 16) == 128 + 129 * 15
+    assert lib.mw8_gemm_workspace_bytes(1, 5120, 5120) == 0
+
+
+FAKE_A, FAKE_B, FAKE_C = 4096, 8192, 12288  # aligned non-null stand-ins: never dereferenced
+
+
+def test_argument_errors_return_codes(lib):
+    E = {v: k for k, v in mw8lib.ERROR_NAMES.items()}
+    assert lib.mw8_quant_per_token_bf16(None, 4, 16, 16, None, 16, None, None) == E["MW8_ERR_ARG"]
+    assert b"null" in lib.mw8_last_error()
+    assert lib.mw8_quant_per_token_bf16(FAKE_A, 4, 16, 8, FAKE_B, 16, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    # K % 16 != 0
+    rc = lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 4, 8, 40, None, 0, None)
+    assert rc == E["MW8_ERR_SHAPE"] and b"multiple of 16" in lib.mw8_last_error()
+    # misaligned operand
+    rc = lib.mw8_gemm_w8a8_i32(FAKE_A + 4, FAKE_B, FAKE_C, 4, 8, 64, None, 0, None)
+    assert rc == E["MW8_ERR_ALIGN"]
+    # K beyond the exact int32 accumulation bound
+    rc = lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 4, 8, 1 << 18, None, 0, None)
+    assert rc == E["MW8_ERR_SHAPE"]
+    # bf16 epilogue without scales
+    rc = lib.mw8_gemm_w8a8_bf16(FAKE_A, None, FAKE_B, None, None, FAKE_C, 4, 8, 64, None, 0, None)
+    assert rc == E["MW8_ERR_ARG"]
+    assert lib.mw8_act_and_mul_quant_bf16(FAKE_A, 4, 24, 0, FAKE_B, FAKE_C, None, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_act_and_mul_quant_bf16(FAKE_A, 4, 32, 7, FAKE_B, FAKE_C, None, None) == E["MW8_ERR_ARG"]
+    assert lib.mw8_topk_softmax(FAKE_A, 1, 4, 8, 9, 1, FAKE_B, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_moe_align_block_size(FAKE_A, 16, 600, 16, FAKE_B, FAKE_C, FAKE_A, None) == E["MW8_ERR_SHAPE"]
+    rc = lib.mw8_moe_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 64, 1, 16, 64, 64, 4, 32,
+                                   FAKE_A, None)
+    assert rc == E["MW8_ERR_SHAPE"]  # block size 32 unsupported
+    assert lib.mw8_moe_sum_reduce_bf16(FAKE_A, 4, 8, 12, FAKE_B, None) == E["MW8_ERR_SHAPE"]
+    # empty problems are no-ops
+    assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    """No CPU fallback: the product path raises on host tensors."""
+    from minisgl_amd.kernel import gemm_w8a8, quant_per_token
+
+    with pytest.raises(ValueError, match="GPU"):
+        quant_per_token(torch.zeros(2, 16, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU"):
+        gemm_w8a8(torch.zeros(2, 16, dtype=torch.int8), torch.ones(2), torch.zeros(4, 16, dtype=torch.int8), torch.ones(4))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not found"):
+        mw8lib.load.__wrapped__(str(tmp_path / "libmw8.so"))
+
+
+# ------------------------------------------------------------ host interface
+def test_registry_semantics():
+    from minisgl_amd.moe import SUPPORTED_MOE_BACKENDS, create_moe_backend
+    from minisgl_amd.moe.fused import FusedMoeW8A8
+    from minisgl_amd.utils import Registry
+
+    assert "fused_w8a8" in SUPPORTED_MOE_BACKENDS.supported_names()
+    assert isinstance(create_moe_backend("fused_w8a8"), FusedMoeW8A8)
+    with pytest.raises(KeyError):
+        SUPPORTED_MOE_BACKENDS["nope"]
+    r = Registry("X")
+    r.register("a")(1)
+    with pytest.raises(KeyError):
+        r.register("a")
+    import argparse
+
+    with pytest.raises(argparse.ArgumentTypeError):
+        r.assert_supported(["a", "b"])
+
+
+def test_linear_shapes_match_reference_constructors():
+    from minisgl_amd.layers import (
+        LinearColParallelMerged,
+        LinearOProj,
+        LinearQKVMerged,
+        LinearReplicated,
+        LinearRowParallel,
+    )
+
+    # Qwen3-14B: hidden 5120, 40 q heads / 8 kv heads, head_dim 128, intermediate 17408
+    qkv = LinearQKVMerged(5120, 128, 40, 8, has_bias=False)
+    assert qkv.weight.shape == (7168, 5120) and qkv.weight.dtype == torch.int8
+    assert qkv.weight_scale.shape == (7168,) and qkv.weight_scale.dtype == torch.float32
+    assert qkv.bias is None
+    gu = LinearColParallelMerged(5120, [17408, 17408], has_bias=False)
+    assert gu.weight.shape == (34816, 5120)
+    assert LinearRowParallel(17408, 5120, False).weight.shape == (5120, 17408)
+    assert LinearOProj(5120, 5120, False).weight.shape == (5120, 5120)
+    b = LinearReplicated(16, 8, has_bias=True)
+    assert b.bias.dtype == torch.bfloat16 and b.bias.shape == (8,)
+
+
+def test_state_dict_roundtrip_and_checks():
+    from minisgl_amd.layers import LinearQKVMerged, MoELayer
+
+    layer = LinearQKVMerged(64, 16, 2, 1, has_bias=True)
+    sd = layer.state_dict(prefix="model.layers.0.qkv_proj")
+    assert set(sd) == {"model.layers.0.qkv_proj.weight", "model.layers.0.qkv_proj.weight_scale",
+                       "model.layers.0.qkv_proj.bias"}
+    new = {k: torch.zeros_like(v) for k, v in sd.items()}
+    layer.load_state_dict({k.split("qkv_proj.")[1]: v for k, v in new.items()})
+    with pytest.raises(AssertionError):  # dtype mismatch (bf16 weight into an int8 slot)
+        layer.load_state_dict({"weight": torch.zeros(64, 64, dtype=torch.bfloat16),
+                               "weight_scale": torch.zeros(64), "bias": torch.zeros(64, dtype=torch.bfloat16)})
+    with pytest.raises(RuntimeError, match="Unexpected"):
+        layer.load_state_dict({"weight": torch.zeros(64, 64, dtype=torch.int8), "weight_scale": torch.zeros(64),
+                               "bias": torch.zeros(64, dtype=torch.bfloat16), "extra": torch.zeros(1)})
+    moe = MoELayer(8, 2, 64, 32)
+    assert {k: tuple(v.shape) for k, v in moe.state_dict().items()} == {
+        "gate_up_proj": (8, 64, 64), "down_proj": (8, 64, 32),
+        "gate_up_scale": (8, 64), "down_scale": (8, 64),
+    }
+
+
+def test_moe_default_config_regimes():
+    from minisgl_amd.moe.fused import get_default_config, try_get_optimal_moe_config
+
+    # python/minisgl/moe/fused.py:92-113: M <= E -> small blocks
+    assert get_default_config(16, 128, 2048, 2048, 8)["BLOCK_SIZE_M"] == 16
+    assert get_default_config(256, 128, 2048, 2048, 8)["BLOCK_SIZE_M"] == 64
+    assert try_get_optimal_moe_config((128, 1536, 2048), (128, 2048, 768), 8, 4096)["BLOCK_SIZE_M"] == 64
+
+
+def test_moe_layer_needs_context():
+    from minisgl_amd.core import reset_global_ctx
+    from minisgl_amd.layers import MoELayer
+
+    reset_global_ctx()
+    with pytest.raises(RuntimeError, match="context"):
+        MoELayer(4, 2, 16, 8).forward(torch.zeros(1, 16), torch.zeros(1, 4))
+
+
+def test_backend_requires_scales():
+    from minisgl_amd.moe import create_moe_backend
+
+    with pytest.raises(ValueError, match="scale"):
+        create_moe_backend("fused_w8a8").forward(torch.zeros(1, 16), torch.zeros(4, 16, 16), torch.zeros(4, 16, 8),
+                                                 torch.zeros(1, 4), 2, True)
