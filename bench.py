@@ -17,6 +17,11 @@ measurements (quantizer at config 2, MoE layer tokens/s at config 3, the
 Qwen3-32B GEMM chain at config 4) timed outside the main region.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Profiling helpers (run under rocprofv3):
+  --mode gemm --shape M,N,K [--reps R]  one W8A8 GEMM shape, R launches
+  --mode copy [--reps R]                a plain 1 GiB device copy (calibrates
+                                        FETCH_SIZE / WRITE_SIZE counters)
 """
 
 from __future__ import annotations
@@ -122,6 +127,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
+    ap.add_argument("--mode", choices=["bench", "gemm", "copy"], default="bench")
+    ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
+    ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); "
@@ -129,6 +137,9 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.mode != "bench":
+        return profile_mode(args)
 
     from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES, SWEEP_M
     from minisgl_amd.kernel import gemm_w8a8, load, quant_per_token
@@ -274,6 +285,37 @@ def main() -> int:
         "secondary": secondary,
     }
     print(json.dumps(out), flush=True)
+    return 0
+
+
+def profile_mode(args) -> int:
+    """Single-kernel workloads for rocprofv3 counter passes."""
+    import torch
+
+    from minisgl_amd.kernel import gemm_w8a8, quant_per_token
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if args.mode == "copy":
+        nbytes = 1 << 30
+        src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, generator=gen, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.reps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
+                          "reps": args.reps}))
+        return 0
+    M, N, K = (int(v) for v in args.shape.split(","))
+    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev)
+    sw = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
+    q, s = quant_per_token(torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16))
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    for _ in range(args.reps):
+        gemm_w8a8(q, s, w, sw, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "gemm", "M": M, "N": N, "K": K, "reps": args.reps,
+                      "algorithmic_bytes": gemm_bytes(M, N, K)}))
     return 0
 
 

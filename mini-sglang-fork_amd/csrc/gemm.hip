@@ -78,46 +78,64 @@ void launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL(kern, grid, dim3(256), S::kLds, st, g);
 }
 
-template <int BM, int BN, int WM, int WN, int NSTAGE, int EPI, class Rows>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
 void launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
-  constexpr int kLds = NSTAGE * (BM + BN) * 64;
-  auto kern = tile3_gemm_kernel<BM, BN, WM, WN, NSTAGE, EPI, Rows>;
+  constexpr int kLds = NSTAGE * (BM + BN) * BK;
+  auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, grid, dim3(256), kLds, st, g);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), kLds, st, g);
 }
 
-// 0-4: register-staged tile core (any K % 16 == 0); 5-8: direct-to-LDS ring
-// (K % 64 == 0).
+// 0-4: register-staged tile core (any K % 16 == 0); 5 and up: direct-to-LDS
+// ring (K % bk == 0).
 struct TileCfg {
   int bm, bn;
   bool dma;
+  int bk;
 };
-constexpr TileCfg kTileCfgs[] = {{256, 256, false}, {256, 256, false}, {128, 128, false},
-                                 {256, 128, false}, {128, 256, false}, {256, 256, true},
-                                 {256, 256, true},  {128, 128, true},  {256, 128, true}};
+constexpr TileCfg kTileCfgs[] = {
+    {256, 256, false, 128}, {256, 256, false, 64}, {128, 128, false, 128},
+    {256, 128, false, 128}, {128, 256, false, 128},
+    {256, 256, true, 64},   // 5: 4 waves, 4 stages
+    {256, 256, true, 64},   // 6: 4 waves, 3 stages
+    {128, 128, true, 64},   // 7: 4 waves, 4 stages
+    {256, 128, true, 64},   // 8: 4 waves, 4 stages
+    {256, 256, true, 64},   // 9: 8 waves (2x4), 3 stages
+    {256, 256, true, 64},   // 10: 8 waves (4x2), 3 stages
+    {256, 256, true, 64},   // 11: 8 waves (2x4), 4 stages
+    {256, 128, true, 64},   // 12: 8 waves (4x2), 3 stages
+    {256, 256, true, 64},   // 13: 16 waves (4x4), 3 stages
+    {256, 256, true, 128},  // 14: 8 waves (4x2), 2 stages
+    {256, 128, true, 128},  // 15: 8 waves (4x2), 2 stages
+    {256, 256, true, 128},  // 16: 16 waves (4x4), 2 stages
+    {256, 128, true, 128},  // 17: 8 waves (4x2), 3 stages
+};
 constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
 // Pick the configuration with the smallest modelled time: waves of
-// resident tiles x per-wave tile area / relative efficiency (measured on
-// MI355X: the 256x256 DMA ring is ~10% faster per op than the 128x128 one
-// at K ~ 5K and ~30% faster at K ~ 17K, where its prologue/epilogue
-// amortise).  Shapes with K % 64 != 0 use the register-staged core.
+// resident tiles x per-wave tile area / relative efficiency.  The
+// efficiencies are per-op throughputs measured on MI355X relative to the
+// 128x128 ring (cfg 7, two blocks per CU): the 16-wave 256x256 BK=128 ring
+// (cfg 16, one block per CU) runs ~1.35x faster per op at K ~ 5K and
+// ~1.45x at K ~ 17K; the 8-wave 256x128 ring (cfg 12, two blocks per CU)
+// ~1.2x.  Shapes with K % 64 != 0 use the register-staged core.
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   if (K % 64 != 0) return 2;
   struct Cand {
     int cfg, per_cu;
     double eff;
   };
-  const Cand cands[] = {{6, 1, K > 8192 ? 1.3 : 1.1}, {7, 2, 1.0}};
+  const Cand cands[] = {{16, 1, K > 8192 ? 1.45 : 1.35}, {12, 2, 1.2}, {7, 2, 1.0}};
   int best = 7;
   double best_cost = 1e300;
   for (const Cand& c : cands) {
     const TileCfg t = kTileCfgs[c.cfg];
+    if (K % t.bk != 0) continue;
     const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
     const int64_t slots = 256 * static_cast<int64_t>(c.per_cu);
     const int64_t waves = (tiles + slots - 1) / slots;
@@ -133,7 +151,7 @@ int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
 template <int EPI>
 void dispatch_tile(const GemmArgs& g, hipStream_t st) {
   int cfg = g_tile_cfg.load(std::memory_order_relaxed);
-  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && g.K % 64 != 0))
+  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && g.K % kTileCfgs[cfg].bk != 0))
     cfg = default_tile_cfg(g.M, g.N, g.K);
   const TileCfg c = kTileCfgs[cfg];
   const unsigned tiles =
@@ -143,10 +161,19 @@ void dispatch_tile(const GemmArgs& g, hipStream_t st) {
     case 1: launch_tile<256, 256, 64, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 3: launch_tile<256, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 4: launch_tile<128, 256, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 5: launch_tile3<256, 256, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 6: launch_tile3<256, 256, 2, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 7: launch_tile3<128, 128, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 8: launch_tile3<256, 128, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 5: launch_tile3<256, 256, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 6: launch_tile3<256, 256, 64, 2, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 7: launch_tile3<128, 128, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 8: launch_tile3<256, 128, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 9: launch_tile3<256, 256, 64, 2, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 10: launch_tile3<256, 256, 64, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 11: launch_tile3<256, 256, 64, 2, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 12: launch_tile3<256, 128, 64, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 13: launch_tile3<256, 256, 64, 4, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 14: launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 15: launch_tile3<256, 128, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 16: launch_tile3<256, 256, 128, 4, 4, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 17: launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
 }

@@ -278,38 +278,49 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
-// Large-M tile core v3: direct-to-LDS loads, NSTAGE-deep ring, BK = 64
+// Large-M tile core v3: direct-to-LDS loads, NSTAGE-deep ring
 // ------------------------------------------------------------------------
-// Every K step of 64 bytes, each wave moves its share of the A and W tiles
+// Every K step of BK bytes, each wave moves its share of the A and W tiles
 // straight from global memory into LDS with global_load_lds_dwordx4 (one
 // 1 KB contiguous LDS run per wave instruction; lane l fills 16-byte unit
 // l of it, and is pointed at the global chunk that belongs there under the
 // swizzle).  Stages are prefetched NSTAGE-1 K steps ahead and tracked with
 // explicit vmcnt waits; one s_barrier per K step.  MFMA fragments are read
 // from LDS one half-step ahead of the MFMAs that consume them (two register
-// sets F0/F1), so LDS latency hides behind 16 MFMAs.  Requires K % 64 == 0.
+// sets F0/F1), so LDS latency hides behind the MFMAs.  Requires K % BK == 0.
 //
-// LDS row = 64 bytes = 4 chunks; chunk c of row r sits at unit
-// r*4 + (c ^ f(r)), f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the 8 (and
-// 16) rows read together by a fragment load on distinct 16-byte bank groups.
-__device__ __forceinline__ int swz64(int row, int chunk) {
-  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+// LDS rows are BK bytes (4 or 8 chunks of 16 bytes).  Chunk c of row r sits
+// at unit r*BK/16 + (c ^ f(r)); f keeps the 8 (and the 16) rows read
+// together by one phase of a fragment load on distinct 16-byte bank groups:
+//   BK = 64 : f(r) = ((r >> 1) ^ (r >> 3)) & 3
+//   BK = 128: f(r) = (r & 7) ^ ((r >> 3) & 1)
+template <int BK>
+__device__ __forceinline__ int swz_f(int row) {
+  if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
+  else return (row & 7) ^ ((row >> 3) & 1);
+}
+template <int BK>
+__device__ __forceinline__ int swz_lds(int row, int chunk) {
+  return row * BK + ((chunk ^ swz_f<BK>(row)) << 4);
 }
 
-// s_waitcnt vmcnt(n) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).  Waiting for this
+// wave's LDS reads as well makes the barrier that follows a point after
+// which no wave still reads the stage buffer about to be refilled.
 template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
   asm volatile("" ::: "memory");
 }
 template <int L, int MAXS>
 __device__ __forceinline__ void wait_stages(int n) {  // at most n (<= MAXS) stages in flight
-  if constexpr (MAXS >= 3) { if (n >= 3) { wait_vmcnt<3 * L>(); return; } }
-  if constexpr (MAXS >= 2) { if (n == 2) { wait_vmcnt<2 * L>(); return; } }
-  if constexpr (MAXS >= 1) { if (n == 1) { wait_vmcnt<L>(); return; } }
-  wait_vmcnt<0>();
+  if constexpr (MAXS >= 3) { if (n >= 3) { wait_vmcnt_lgkm0<3 * L>(); return; } }
+  if constexpr (MAXS >= 2) { if (n == 2) { wait_vmcnt_lgkm0<2 * L>(); return; } }
+  if constexpr (MAXS >= 1) { if (n == 1) { wait_vmcnt_lgkm0<L>(); return; } }
+  wait_vmcnt_lgkm0<0>();
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -323,17 +334,23 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int NSTAGE, int EPI, class Rows>
-__global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
+__global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
   // pass only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kWaves = WM * WN;
   constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
   constexpr int kFM = kWaveM / 32, kFN = kWaveN / 32;
-  constexpr int kStageA = BM * 64, kStageB = BN * 64, kStage = kStageA + kStageB;
-  constexpr int kLA = BM / 64, kLB = BN / 64;  // DMA instructions per wave per stage
-  constexpr int kL = kLA + kLB;
-  static_assert(WM * WN == 4 && kFM >= 1 && kFN >= 1 && kLA >= 1 && kLB >= 1, "shape");
+  constexpr int kChunks = BK / 16;                 // 16-byte chunks per LDS row
+  constexpr int kRowsPerInst = 1024 / BK;           // rows one 1 KB DMA instruction fills
+  constexpr int kStageA = BM * BK, kStageB = BN * BK, kStage = kStageA + kStageB;
+  constexpr int kLA = BM / (kRowsPerInst * kWaves), kLB = BN / (kRowsPerInst * kWaves);
+  constexpr int kL = kLA + kLB;                     // DMA instructions per wave per stage
+  static_assert(BK == 64 || BK == 128, "BK");
+  static_assert((kWaves == 4 || kWaves == 8 || kWaves == 16) && kFM >= 1 && kFN >= 1, "shape");
+  static_assert(kLA >= 1 && kLB >= 1 && kLA * kRowsPerInst * kWaves == BM &&
+                kLB * kRowsPerInst * kWaves == BN, "DMA split");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -358,13 +375,13 @@ __global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
   }
 
   // ---- per-lane DMA sources: instruction j of this wave fills LDS units
-  // (j*4 + wave)*64 .. +63 of the tile, i.e. 16 rows; lane -> (row, chunk)
+  // (j*kWaves + wave)*64 .. +63 of the tile; lane -> (row, chunk)
   const int8_t* a_src[kLA];
   const int8_t* w_src[kLB];
 #pragma unroll
   for (int j = 0; j < kLA; ++j) {
-    const int unit = (j * 4 + wave) * 64 + lane, row = unit >> 2;
-    const int c = (unit & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
+    const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
+    const int c = (unit % kChunks) ^ swz_f<BK>(row);
     int64_t arow;
     if constexpr (Rows::kGrouped) {
       const int32_t p = g.sorted_ids[m0 + row];
@@ -376,20 +393,20 @@ __global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
   }
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
-    const int unit = (j * 4 + wave) * 64 + lane, row = unit >> 2;
-    const int c = (unit & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
+    const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
+    const int c = (unit % kChunks) ^ swz_f<BK>(row);
     const int64_t wrow = n0 + row < g.N ? n0 + row : g.N - 1;
     w_src[j] = W + wrow * g.K + 16 * c;
   }
   auto issue = [&](int kt) {
     unsigned char* base = lds + (kt % NSTAGE) * kStage;
-    const int64_t k0 = static_cast<int64_t>(kt) * 64;
+    const int64_t k0 = static_cast<int64_t>(kt) * BK;
 #pragma unroll
     for (int j = 0; j < kLA; ++j)
-      __builtin_amdgcn_global_load_lds(a_src[j] + k0, (lds_ptr_t)(base + (j * 4 + wave) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(a_src[j] + k0, (lds_ptr_t)(base + (j * kWaves + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < kLB; ++j)
-      __builtin_amdgcn_global_load_lds(w_src[j] + k0, (lds_ptr_t)(base + kStageA + (j * 4 + wave) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(w_src[j] + k0, (lds_ptr_t)(base + kStageA + (j * kWaves + wave) * 1024), 16, 0, 0);
   };
 
   const int frow = lane & 31, fgrp = lane >> 5;
@@ -399,14 +416,15 @@ __global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < kFN; ++j) b_off[j] = wn * kWaveN + 32 * j + frow;
   v4i fa[2][kFM], fb[2][kFN];
+  // fragments of k-substep ks (32 K bytes) of stage kt into register set ks & 1
   auto read_frags = [&](int kt, int ks) {
     const unsigned char* la = lds + (kt % NSTAGE) * kStage;
     const unsigned char* lb = la + kStageA;
     const int ch = 2 * ks + fgrp;
 #pragma unroll
-    for (int i = 0; i < kFM; ++i) fa[ks][i] = *reinterpret_cast<const v4i*>(la + swz64(a_off[i], ch));
+    for (int i = 0; i < kFM; ++i) fa[ks & 1][i] = *reinterpret_cast<const v4i*>(la + swz_lds<BK>(a_off[i], ch));
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) fb[ks][j] = *reinterpret_cast<const v4i*>(lb + swz64(b_off[j], ch));
+    for (int j = 0; j < kFN; ++j) fb[ks & 1][j] = *reinterpret_cast<const v4i*>(lb + swz_lds<BK>(b_off[j], ch));
   };
 
   v16i acc[kFM][kFN];
@@ -414,15 +432,16 @@ __global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < kFN; ++j) acc[i][j] = v16i{0};
-  auto mfmas = [&](int ks) {
+  auto mfmas = [&](int set) {
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
       for (int j = 0; j < kFN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
   };
+  constexpr int kSub = BK / 32;  // k-substeps per stage (2 or 4)
 
-  const int nk = static_cast<int>(g.K / 64);
+  const int nk = static_cast<int>(g.K / BK);
   // prologue: stages 0 .. NSTAGE-1 in flight, stage 0 landed, its fragments read
 #pragma unroll
   for (int s = 0; s < NSTAGE; ++s)
@@ -432,19 +451,33 @@ __global__ __launch_bounds__(256) void tile3_gemm_kernel(GemmArgs g) {
   read_frags(0, 0);
   read_frags(0, 1);
 
+  // Steady state for stage kt: the fragments of substeps 0 and 1 are in
+  // registers on entry.  Substep s runs its MFMAs while the fragments of
+  // substep s+2 load; the last substep pairs overlap the next stage's first
+  // fragments, which need that stage landed (vmcnt) and, since its LDS
+  // buffer is then recycled, every wave past its reads of stage kt.
   for (int kt = 0; kt + 1 < nk; ++kt) {
-    mfmas(0);
-    // stage kt+1 landed everywhere; every wave holds stage kt in registers
+#pragma unroll
+    for (int s = 0; s + 2 < kSub; ++s) {
+      mfmas(s & 1);
+      read_frags(kt, s + 2);
+    }
+    mfmas(kSub & 1);  // substep kSub-2
     const int later = nk - 2 - kt;  // stages after kt+1 already issued
     wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
     raw_barrier();
     if (kt + NSTAGE < nk) issue(kt + NSTAGE);
     read_frags(kt + 1, 0);
-    mfmas(1);
+    mfmas((kSub - 1) & 1);  // substep kSub-1
     read_frags(kt + 1, 1);
   }
-  mfmas(0);
-  mfmas(1);
+#pragma unroll
+  for (int s = 0; s + 2 < kSub; ++s) {
+    mfmas(s & 1);
+    read_frags(nk - 1, s + 2);
+  }
+  mfmas(kSub & 1);
+  mfmas((kSub - 1) & 1);
 
   // ---- epilogue: lane holds column (lane & 31) of each 32x32 block
 #pragma unroll

@@ -171,7 +171,7 @@ def test_gemm_every_tile_config(M, K, N):
     y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
     lib = load()
     try:
-        for cfg in range(9):
+        for cfg in range(18):
             lib.mw8_set_tuning(-1, cfg)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
