@@ -5,12 +5,17 @@ One step = the W8A8 GEMM (int8 MFMA + per-token x per-channel scale
 epilogue -> bf16) over the whole Qwen3-14B sweep: {qkv K5120 N7168,
 o_proj K5120 N5120, gate_up K5120 N34816, down K17408 N5120} x
 M in {1, 8, 64, 512, 4096, 8192} -- 24 launches, activations already
-quantized and resident in HBM.  Weights are kept in ``--copies`` distinct
-copies and rotated so that no launch finds its weights in the 256 MB MALL.
+quantized and resident in HBM.  The timed region runs K steps shape by
+shape: each shape's K launches are captured once in a HIP graph (the
+reference times kernels the same way, python/minisgl/benchmark/perf.py:10-51)
+and replayed between two HIP events on the launch stream, so the
+per-launch time carries no host launch overhead.  Every launch of a graph
+reads a distinct weight copy, and each shape keeps at least 600 MB of
+copies, so no launch finds its weights in the 256 MB MALL.
 
 Printed (one JSON line): whole-step throughput in TOPS (value), per-shape
-time / TOPS / GB/s / roofline fraction from HIP events recorded around
-every launch inside the timed region, the dominant kernel's roofline, the
+time / TOPS / GB/s / roofline fraction from the HIP events of the timed
+region, the dominant kernel's roofline, the
 CPU baseline (the CPU oracle, timed on the host on a bounded sample, plus
 the reference's bf16 ``F.linear`` CPU op on the same sample), and secondary
 measurements (quantizer at config 2, MoE layer tokens/s at config 3, the
@@ -123,7 +128,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--copies", type=int, default=2, help="weight copies rotated to defeat the MALL")
+    ap.add_argument("--copy-mb", type=int, default=600, help="MB of distinct weight copies per shape")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
@@ -152,12 +157,14 @@ def main() -> int:
     log(f"device: {peaks}")
 
     gen = torch.Generator(device=dev).manual_seed(0)
-    # weights: R distinct copies per shape (values: uniform int8 in [-127, 127])
+    # weights: distinct copies per shape (uniform int8 in [-127, 127]); each
+    # graph cycles through them, and together they exceed the MALL
     W = {}
     SW = {}
     for name, K, N in QWEN3_14B_SHAPES:
+        ncopy = max(args.steps, -(-args.copy_mb * 10**6 // (N * K)))
         W[name] = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev)
-                   for _ in range(args.copies)]
+                   for _ in range(ncopy)]
         SW[name] = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
     # activations: the outlier recipe, quantized once (resident int8 + fp32 scales)
     A = {}
@@ -172,49 +179,44 @@ def main() -> int:
     Y = {(M, name): torch.empty(M, N, dtype=torch.bfloat16, device=dev)
          for M in SWEEP_M for name, K, N in QWEN3_14B_SHAPES}
     plan = [(M, name, K, N) for M in SWEEP_M for name, K, N in QWEN3_14B_SHAPES]
-    # reserve the split-K workspace for the largest small-M shape before timing
-    from minisgl_amd.kernel.ops import gemm_workspace
-
-    for M, name, K, N in plan:
-        gemm_workspace(M, N, K, dev)
-    torch.cuda.synchronize()
-    log(f"workload ready: {len(plan)} GEMMs per step, {args.copies} weight copies, "
+    stream = torch.cuda.Stream()
+    graphs = []
+    with torch.cuda.stream(stream):
+        for M, name, K, N in plan:  # eager first call per shape (one-time set-up)
+            q, s = A[(M, K)]
+            gemm_w8a8(q, s, W[name][0], SW[name], out=Y[(M, name)])
+        torch.cuda.synchronize()
+        for M, name, K, N in plan:
+            q, s = A[(M, K)]
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(args.steps):
+                    gemm_w8a8(q, s, W[name][i % len(W[name])], SW[name], out=Y[(M, name)])
+            graphs.append(g)
+        torch.cuda.synchronize()
+    log(f"workload ready: {len(plan)} GEMM graphs of {args.steps} launches, "
         f"{torch.cuda.memory_allocated() / 2**30:.2f} GiB allocated")
 
-    launch_no = [0]
-
-    def step(events=None):
-        for i, (M, name, K, N) in enumerate(plan):
-            q, s = A[(M, K)]
-            w = W[name][launch_no[0] % args.copies]
-            launch_no[0] += 1
-            if events is not None:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                gemm_w8a8(q, s, w, SW[name], out=Y[(M, name)])
-                e1.record()
-                events[i].append((e0, e1))
-            else:
-                gemm_w8a8(q, s, w, SW[name], out=Y[(M, name)])
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    events = [[] for _ in plan]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(events)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            for g in graphs:
+                g.replay()
+        torch.cuda.synchronize()
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in plan]
+        t0 = time.perf_counter()
+        for g, (e0, e1) in zip(graphs, events):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ops_step = sum(2.0 * M * N * K for M, _, K, N in plan)
     value = ops_step * args.steps / wall / 1e12
 
     shapes = []
     for i, (M, name, K, N) in enumerate(plan):
-        ts = [a.elapsed_time(b) * 1e-3 for a, b in events[i]]
-        t = sum(ts) / len(ts)
+        t = events[i][0].elapsed_time(events[i][1]) * 1e-3 / args.steps
         ops = 2.0 * M * N * K
         nb = gemm_bytes(M, N, K)
         ai = ops / nb
@@ -223,7 +225,7 @@ def main() -> int:
             "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2),
             "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
             "bound": bound, "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
-            "kernel": "stream_gemm_kernel" if M <= 64 else "tile_gemm_kernel",
+            "kernel": "decode_gemm_kernel" if M <= 64 else "tile3_gemm_kernel",
         })
     dom = max(shapes, key=lambda r: r["us"])
     dom_ops = 2.0 * dom["M"] * dom["N"] * dom["K"]
@@ -235,11 +237,12 @@ def main() -> int:
         "peak": round(peak_tops, 1) if dom["bound"] == "mfma" else HBM_PEAK_GBPS,
         "unit": "TOPS" if dom["bound"] == "mfma" else "GB/s",
         "frac": dom["roofline_frac"],
-        "traffic": None,
+        "traffic": measured_traffic(dom),
         "kernel": f"{dom['kernel']} ({dom['shape']} M={dom['M']} K={dom['K']} N={dom['N']})",
         "per_launch": (f"{dom_ops / 1e9:.1f} GOP = 2*M*N*K and "
                        f"{gemm_bytes(dom['M'], dom['N'], dom['K']) / 1e6:.1f} MB algorithmic "
-                       f"per launch, avg of {args.steps} launches timed with HIP events"),
+                       f"per launch; time = HIP events around a graph of {args.steps} "
+                       f"launches on the launch stream / {args.steps}"),
     }
     log(f"step: {wall / args.steps * 1e3:.3f} ms, {value:.1f} TOPS; dominant {roofline['kernel']} "
         f"{dom['us']} us frac {dom['roofline_frac']}")
@@ -248,7 +251,7 @@ def main() -> int:
             f"{r['gbps']:8.1f} GB/s  {r['bound']} frac={r['roofline_frac']:.3f}")
 
     # release the sweep buffers before the secondary measurements
-    del W, A, Y
+    del W, A, Y, graphs
     torch.cuda.empty_cache()
     secondary = None if args.no_secondary else run_secondary(dev, peak_tops)
     cpu = None if args.no_cpu_baseline else cpu_baseline(QWEN3_14B_SHAPES, 512, args.cpu_budget)
@@ -275,7 +278,8 @@ def main() -> int:
             "workload": ("cfg1 W8A8 linear sweep, Qwen3-14B shapes qkv(5120->7168) "
                          "o_proj(5120->5120) gate_up(5120->34816) down(17408->5120) x "
                          "M in {1,8,64,512,4096,8192}; one step = 24 GEMM launches"),
-            "weight_copies_rotated": args.copies,
+            "weight_copy_mb_per_shape": args.copy_mb,
+            "timing": "per shape: HIP graph of `steps` launches replayed between HIP events",
             "ops_per_step": ops_step,
         },
         "device": peaks,
@@ -286,6 +290,20 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def measured_traffic(dom):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 counter summary (profiles/traffic.json), if it covers it."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    key = f"{dom['M']},{dom['N']},{dom['K']}"
+    entry = table.get(key)
+    return None if entry is None else entry.get("traffic_bytes")
 
 
 def profile_mode(args) -> int:
