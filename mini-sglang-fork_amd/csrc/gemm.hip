@@ -232,12 +232,23 @@ int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int
 // Grouped (fused-MoE) GEMM launchers over expert-sorted rows.
 void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((g.N + 127) / 128), blocks);
+  const bool ring = g.K % 64 == 0;  // direct-to-LDS ring, else register-staged core
   if (epi == kEpiBf16) {
-    if (bm == 64) launch_tile<64, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
-    else launch_tile<128, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+    if (bm == 64) {
+      if (ring) launch_tile3<64, 128, 64, 2, 2, 4, kEpiBf16, SortedRows>(g, grid, st);
+      else launch_tile<64, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+    } else {
+      if (ring) launch_tile3<128, 128, 64, 2, 2, 4, kEpiBf16, SortedRows>(g, grid, st);
+      else launch_tile<128, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+    }
   } else {
-    if (bm == 64) launch_tile<64, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
-    else launch_tile<128, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+    if (bm == 64) {
+      if (ring) launch_tile3<64, 128, 64, 2, 2, 4, kEpiI32, SortedRows>(g, grid, st);
+      else launch_tile<64, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+    } else {
+      if (ring) launch_tile3<128, 128, 64, 2, 2, 4, kEpiI32, SortedRows>(g, grid, st);
+      else launch_tile<128, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+    }
   }
 }
 

@@ -315,8 +315,10 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
   asm volatile("" ::: "memory");
 }
+// Wait until a stage's DMA loads have landed while n (<= MAXS) later stage
+// issues of L loads each may stay in flight.
 template <int L, int MAXS>
-__device__ __forceinline__ void wait_stages(int n) {  // at most n (<= MAXS) stages in flight
+__device__ __forceinline__ void wait_stages(int n) {
   if constexpr (MAXS >= 3) { if (n >= 3) { wait_vmcnt_lgkm0<3 * L>(); return; } }
   if constexpr (MAXS >= 2) { if (n == 2) { wait_vmcnt_lgkm0<2 * L>(); return; } }
   if constexpr (MAXS >= 1) { if (n == 1) { wait_vmcnt_lgkm0<L>(); return; } }
@@ -398,6 +400,7 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     const int64_t wrow = n0 + row < g.N ? n0 + row : g.N - 1;
     w_src[j] = W + wrow * g.K + 16 * c;
   }
+  const int nk = static_cast<int>(g.K / BK);
   auto issue = [&](int kt) {
     unsigned char* base = lds + (kt % NSTAGE) * kStage;
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
@@ -441,7 +444,6 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   };
   constexpr int kSub = BK / 32;  // k-substeps per stage (2 or 4)
 
-  const int nk = static_cast<int>(g.K / BK);
   // prologue: stages 0 .. NSTAGE-1 in flight, stage 0 landed, its fragments read
 #pragma unroll
   for (int s = 0; s < NSTAGE; ++s)
