@@ -76,13 +76,14 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
                                float* s, void* act_out, mw8_stream_t stream);
 
 /*
- * Tile-configuration override for the dense GEMM, process-wide: decode_cfg
- * indexes the small-M (M <= 64) configurations, tile_cfg the large-M ones;
+ * Tile-configuration override, process-wide: decode_cfg indexes the dense
+ * small-M (M <= 64) configurations, tile_cfg the dense large-M ones, moe_cfg
+ * the grouped (fused-MoE) tile configurations for block sizes 64 and 128;
  * -1 restores the automatic choice.  Results do not depend on the
  * configuration (exact integer accumulation).  Tuning hook; no reference
  * counterpart.
  */
-void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg);
+void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 
 /*
  * Bytes of workspace mw8_gemm_w8a8_* needs for (M, N, K).  The current

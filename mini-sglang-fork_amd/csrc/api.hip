@@ -29,7 +29,7 @@ int check_launch(const char* what) {
 int quant_per_token_bf16(const void*, int64_t, int64_t, int64_t, int8_t*, int64_t, float*, hipStream_t);
 int act_and_mul_quant_bf16(const void*, int64_t, int64_t, int, int8_t*, float*, void*, hipStream_t);
 size_t gemm_workspace_bytes(int64_t, int64_t, int64_t);
-void set_tuning(int, int);
+void set_tuning(int, int, int);
 int gemm_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, const void*, void*,
                    int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 int gemm_w8a8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, void*, size_t,
@@ -82,7 +82,9 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
   MW8_ENTRY(mw8::act_and_mul_quant_bf16(x, R, two_d, act, q, s, act_out, S(st)));
 }
 
-void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg) { mw8::set_tuning(decode_cfg, tile_cfg); }
+void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg) {
+  mw8::set_tuning(decode_cfg, tile_cfg, moe_cfg);
+}
 
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return mw8::gemm_workspace_bytes(M, N, K);

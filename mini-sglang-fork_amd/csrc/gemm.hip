@@ -13,6 +13,7 @@ constexpr int64_t kDecodeMaxM = 64;
 // Tuning override (-1 = automatic); set through mw8_set_tuning.
 std::atomic<int> g_decode_cfg{-1};
 std::atomic<int> g_tile_cfg{-1};
+std::atomic<int> g_moe_cfg{-1};
 
 // ------------------------------------------------------------------ decode
 // (rows of 16 per block, waves per block, K steps of loads in flight)
@@ -211,9 +212,10 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
 
 }  // namespace
 
-void set_tuning(int decode_cfg, int tile_cfg) {
+void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
   g_decode_cfg.store(decode_cfg, std::memory_order_relaxed);
   g_tile_cfg.store(tile_cfg, std::memory_order_relaxed);
+  g_moe_cfg.store(moe_cfg, std::memory_order_relaxed);
 }
 
 size_t gemm_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
@@ -229,27 +231,51 @@ int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int
   return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, st, kEpiI32);
 }
 
-// Grouped (fused-MoE) GEMM launchers over expert-sorted rows.
-void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((g.N + 127) / 128), blocks);
-  const bool ring = g.K % 64 == 0;  // direct-to-LDS ring, else register-staged core
-  if (epi == kEpiBf16) {
-    if (bm == 64) {
-      if (ring) launch_tile3<64, 128, 64, 2, 2, 4, kEpiBf16, SortedRows>(g, grid, st);
-      else launch_tile<64, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
-    } else {
-      if (ring) launch_tile3<128, 128, 64, 2, 2, 4, kEpiBf16, SortedRows>(g, grid, st);
-      else launch_tile<128, 128, 128, 2, 2, kEpiBf16, SortedRows>(g, grid, st);
+// Grouped (fused-MoE) GEMM launchers over expert-sorted rows.  BM equals
+// the alignment block size, so every block reads one expert's weights.
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI>
+void launch_grouped3(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.N + BN - 1) / BN), blocks);
+  launch_tile3<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRows>(g, grid, st);
+}
+
+template <int EPI>
+void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st) {
+  int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  if (g.K % 64 != 0) {  // register-staged core
+    const dim3 grid(static_cast<unsigned>((g.N + 127) / 128), blocks);
+    if (bm == 64) launch_tile<64, 128, 128, 2, 2, EPI, SortedRows>(g, grid, st);
+    else launch_tile<128, 128, 128, 2, 2, EPI, SortedRows>(g, grid, st);
+    return;
+  }
+  const bool bk128 = g.K % 128 == 0;
+  if (cfg < 0 || (!bk128 && cfg >= 3)) cfg = 0;
+  if (bm == 64) {
+    switch (cfg) {
+      case 1: launch_grouped3<64, 128, 64, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 2: launch_grouped3<64, 256, 64, 2, 2, 3, EPI>(g, blocks, st); break;
+      case 3: launch_grouped3<64, 256, 128, 2, 4, 2, EPI>(g, blocks, st); break;
+      case 4: launch_grouped3<64, 128, 128, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 5: launch_grouped3<64, 256, 128, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 6: launch_grouped3<64, 128, 128, 2, 4, 3, EPI>(g, blocks, st); break;
+      default: launch_grouped3<64, 128, 64, 2, 2, 4, EPI>(g, blocks, st); break;
     }
   } else {
-    if (bm == 64) {
-      if (ring) launch_tile3<64, 128, 64, 2, 2, 4, kEpiI32, SortedRows>(g, grid, st);
-      else launch_tile<64, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
-    } else {
-      if (ring) launch_tile3<128, 128, 64, 2, 2, 4, kEpiI32, SortedRows>(g, grid, st);
-      else launch_tile<128, 128, 128, 2, 2, kEpiI32, SortedRows>(g, grid, st);
+    switch (cfg) {
+      case 1: launch_grouped3<128, 128, 64, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 2: launch_grouped3<128, 256, 64, 2, 4, 3, EPI>(g, blocks, st); break;
+      case 3: launch_grouped3<128, 256, 128, 2, 4, 2, EPI>(g, blocks, st); break;
+      case 4: launch_grouped3<128, 128, 128, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 5: launch_grouped3<128, 256, 128, 2, 2, 2, EPI>(g, blocks, st); break;
+      case 6: launch_grouped3<128, 128, 128, 2, 4, 3, EPI>(g, blocks, st); break;
+      default: launch_grouped3<128, 128, 64, 2, 2, 4, EPI>(g, blocks, st); break;
     }
   }
+}
+
+void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st) {
+  if (epi == kEpiBf16) launch_grouped_epi<kEpiBf16>(g, blocks, bm, st);
+  else launch_grouped_epi<kEpiI32>(g, blocks, bm, st);
 }
 
 void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {

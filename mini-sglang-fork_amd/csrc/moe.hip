@@ -84,38 +84,69 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, i
 }
 
 // ------------------------------------------------------------ alignment
-// Single 1024-thread block.  Counts per expert slot, exclusive scan of the
-// block-padded counts, sentinel fill, then a stable scatter: pairs are
-// visited in chunks of 1024 flat indices; within a wave, lanes holding the
-// same expert are found with a bitwise ballot match, their rank is the
-// popcount of lower matching lanes; across waves and chunks prefix counts
-// come from LDS.  Segment order is therefore ascending flat index.
+// One launch, no scratch (the reference call passes none that survives the
+// call), no communication between blocks.  Block b owns the flat range
+// [b*R, (b+1)*R) with R = 1024*U pairs: wave w of the block owns the
+// sub-range of 64*U pairs starting at b*R + w*64*U.  Every block histograms
+// the whole id array (it is small and L2-resident) into three parts: pairs
+// before its range, pairs after it, and per-wave counts inside it.  From
+// these every block derives the same padded segment offsets (exclusive scan
+// over slots), the start position of each of its waves inside each expert
+// segment, and the post-padding total.  Waves then place their pairs in
+// flat order: lanes holding the same expert are found with a bitwise ballot
+// match and ranked by the popcount of lower matching lanes.  Segment order
+// is therefore ascending flat index.  The sentinel fill (padding tails and
+// everything past the total) and expert_ids are split over blocks by
+// striding; fill and placement never write the same element.
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignMaxSlots = 512;
 
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int64_t numel, int slots, int bsz,
+    const int32_t* __restrict__ ids, int64_t numel, int slots, int bsz, int unroll,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
     int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks, int nbits) {
+  __shared__ int wpos[kAlignWaves][kAlignMaxSlots];  // counts, then start positions
+  __shared__ int before[kAlignMaxSlots];
+  __shared__ int after[kAlignMaxSlots];
   __shared__ int cnt[kAlignMaxSlots];
   __shared__ int off[kAlignMaxSlots];
-  __shared__ int run[kAlignMaxSlots];
-  __shared__ int wcnt[kAlignWaves][kAlignMaxSlots];
   __shared__ int wave_tot[kAlignWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t wave_span = 64 * static_cast<int64_t>(unroll);
+  const int64_t lo = static_cast<int64_t>(blockIdx.x) * kAlignWaves * wave_span;
+  const int64_t hi = lo + kAlignWaves * wave_span < numel ? lo + kAlignWaves * wave_span : numel;
 
-  for (int e = tid; e < slots; e += kAlignThreads) { cnt[e] = 0; run[e] = 0; }
+  for (int j = tid; j < kAlignWaves * kAlignMaxSlots; j += kAlignThreads) (&wpos[0][0])[j] = 0;
+  for (int j = tid; j < kAlignMaxSlots; j += kAlignThreads) { before[j] = 0; after[j] = 0; }
   __syncthreads();
-  for (int64_t i = tid; i < numel; i += kAlignThreads) {
-    const int e = ids[i];
-    if (e >= 0 && e < slots) atomicAdd(&cnt[e], 1);
+  constexpr int kU = 8;
+  for (int64_t c = 0; c < numel; c += kU * kAlignThreads) {
+    int e[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = c + u * kAlignThreads + tid;
+      e[u] = i < numel ? ids[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = c + u * kAlignThreads + tid;
+      if (e[u] < 0 || e[u] >= slots) continue;
+      int* slot = i < lo ? &before[e[u]]
+                  : i >= hi ? &after[e[u]]
+                            : &wpos[static_cast<int>(i - lo) / static_cast<int>(wave_span)][e[u]];
+      atomicAdd(slot, 1);
+    }
   }
   __syncthreads();
 
-  // exclusive scan of padded counts (slots <= 1024: one per thread)
-  int padded = 0;
-  if (tid < slots) padded = ((cnt[tid] + bsz - 1) / bsz) * bsz;
+  // exclusive scan of padded counts over slots (slots <= 1024: one per thread)
+  int total_e = 0, padded = 0;
+  if (tid < slots) {
+    total_e = before[tid] + after[tid];
+    for (int w = 0; w < kAlignWaves; ++w) total_e += wpos[w][tid];
+    padded = ((total_e + bsz - 1) / bsz) * bsz;
+  }
   int x = padded;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -124,47 +155,57 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
   if (lane == 63) wave_tot[wave] = x;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += wave_tot[w];
-  if (tid < slots) off[tid] = base + x - padded;
-  int total = 0;
-  for (int w = 0; w < kAlignWaves; ++w) total += wave_tot[w];
+  int base = 0, total = 0;
+  for (int w = 0; w < kAlignWaves; ++w) {
+    if (w < wave) base += wave_tot[w];
+    total += wave_tot[w];
+  }
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kAlignThreads;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kAlignThreads + tid;
+  if (tid < slots) {
+    const int start = base + x - padded;
+    off[tid] = start;
+    cnt[tid] = total_e;
+    int p = start + before[tid];
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int c = wpos[w][tid];
+      wpos[w][tid] = p;
+      p += c;
+    }
+  }
+  if (gtid == 0) *npp = total;
+  for (int64_t i = total + gtid; i < max_padded; i += gstride) sorted_ids[i] = static_cast<int32_t>(numel);
+  for (int64_t b = static_cast<int64_t>(total) / bsz + gtid; b < max_blocks; b += gstride) expert_ids[b] = -1;
   __syncthreads();
-  if (tid == 0) *npp = total;
-
-  for (int64_t i = tid; i < max_padded; i += kAlignThreads) sorted_ids[i] = static_cast<int32_t>(numel);
-  for (int64_t b = static_cast<int64_t>(total) / bsz + tid; b < max_blocks; b += kAlignThreads) expert_ids[b] = -1;
-  if (tid < slots && padded > 0)
-    for (int b = off[tid] / bsz; b < (off[tid] + padded) / bsz; ++b) expert_ids[b] = tid;
-  __syncthreads();
+  // expert_ids of the padded segments and the sentinel in each padding tail
+  for (int64_t j = gtid; j < static_cast<int64_t>(slots) * bsz; j += gstride) {  // < 2^21
+    const int s = static_cast<int>(j) / bsz, r = static_cast<int>(j) - s * bsz;
+    const int c = cnt[s];
+    const int padded_s = ((c + bsz - 1) / bsz) * bsz;
+    if (r < padded_s - c) sorted_ids[off[s] + c + r] = static_cast<int32_t>(numel);
+    if (r == 0)
+      for (int b = off[s] / bsz; b < (off[s] + padded_s) / bsz; ++b) expert_ids[b] = s;
+  }
 
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t base_i = 0; base_i < numel; base_i += kAlignThreads) {
-    for (int j = tid; j < kAlignWaves * slots; j += kAlignThreads) (&wcnt[0][0])[(j / slots) * kAlignMaxSlots + j % slots] = 0;
-    __syncthreads();
-    const int64_t i = base_i + tid;
-    const int e = i < numel ? ids[i] : -1;
-    const bool valid = e >= 0 && e < slots;
+  const int64_t wlo = lo + wave * wave_span;
+  const int64_t whi = wlo + wave_span < hi ? wlo + wave_span : hi;
+  for (int64_t c = wlo; c < whi; c += 64) {  // wave-uniform bounds
+    const int64_t i = c + lane;
+    const int ev = i < whi ? ids[i] : -1;
+    const bool valid = ev >= 0 && ev < slots;
     uint64_t m = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
-      const uint64_t bb = __ballot((e >> b) & 1);
-      m &= ((e >> b) & 1) ? bb : ~bb;
+      const bool bit = (ev >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
     }
     const int rank = __popcll(m & below);
-    if (valid && rank == 0) wcnt[wave][e] = __popcll(m);
-    __syncthreads();
-    if (valid) {
-      int pre = 0;
-      for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
-      sorted_ids[off[e] + run[e] + pre + rank] = static_cast<int32_t>(i);
-    }
-    __syncthreads();
-    for (int s = tid; s < slots; s += kAlignThreads) {
-      int add = 0;
-      for (int w = 0; w < kAlignWaves; ++w) add += wcnt[w][s];
-      run[s] += add;
-    }
-    __syncthreads();
+    const int pos = valid ? wpos[wave][ev] : 0;
+    if (valid) sorted_ids[pos + rank] = static_cast<int32_t>(i);
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) wpos[wave][ev] = pos + __popcll(m);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -242,8 +283,13 @@ int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int slots, int 
   const int64_t max_blocks = (max_padded + bsz - 1) / bsz;
   int nbits = 1;
   while ((1 << nbits) < slots) ++nbits;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, numel, slots,
-                     bsz, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits);
+  // each block places R = 1024 * unroll pairs; at most 256 blocks
+  const int64_t unroll64 = (numel + 256ll * kAlignThreads - 1) / (256ll * kAlignThreads);
+  const int unroll = static_cast<int>(unroll64 < 1 ? 1 : unroll64);
+  const int64_t per_block = static_cast<int64_t>(kAlignThreads) * unroll;
+  const unsigned grid = static_cast<unsigned>(numel > 0 ? (numel + per_block - 1) / per_block : 1);
+  hipLaunchKernelGGL(moe_align_kernel, dim3(grid), dim3(kAlignThreads), 0, st, topk_ids, numel,
+                     slots, bsz, unroll, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits);
   return check_launch("moe_align");
 }
 

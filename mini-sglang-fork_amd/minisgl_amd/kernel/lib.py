@@ -30,7 +30,7 @@ SIGNATURES = {
     "mw8_device_info": (ctypes.c_int, [_I32, _P, _P, _P]),
     "mw8_quant_per_token_bf16": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "mw8_act_and_mul_quant_bf16": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _P, _P, _P]),
-    "mw8_set_tuning": (None, [_I32, _I32]),
+    "mw8_set_tuning": (None, [_I32, _I32, _I32]),
     "mw8_gemm_workspace_bytes": (c_size_t, [_I64, _I64, _I64]),
     "mw8_gemm_w8a8_bf16": (
         ctypes.c_int,

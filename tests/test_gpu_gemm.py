@@ -172,11 +172,11 @@ def test_gemm_every_tile_config(M, K, N):
     lib = load()
     try:
         for cfg in range(18):
-            lib.mw8_set_tuning(-1, cfg)
+            lib.mw8_set_tuning(-1, cfg, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
     finally:
-        lib.mw8_set_tuning(-1, -1)
+        lib.mw8_set_tuning(-1, -1, -1)
 
 
 @pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 64])
@@ -194,8 +194,8 @@ def test_gemm_every_decode_config(M):
     lib = load()
     try:
         for cfg in range(7):
-            lib.mw8_set_tuning(cfg, -1)
+            lib.mw8_set_tuning(cfg, -1, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
     finally:
-        lib.mw8_set_tuning(-1, -1)
+        lib.mw8_set_tuning(-1, -1, -1)

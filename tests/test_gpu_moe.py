@@ -54,6 +54,22 @@ def test_align_matches_oracle(M, B):
     assert (expert_ids.cpu().numpy()[n_ref // B:] == -1).all()
 
 
+@pytest.mark.parametrize("numel,B,E", [(320000, 64, 128), (8195, 16, 128), (1025, 128, 511), (70001, 64, 7)])
+def test_align_large_and_ragged(numel, B, E):
+    """Random ids (repeats, a few out of range) over several placement
+    blocks, including more than 256K pairs (several pairs per lane)."""
+    announce(f"align numel={numel} B={B} E={E}")
+    gen = torch.Generator().manual_seed(numel)
+    ids = torch.randint(0, E + 1, (numel,), generator=gen, dtype=torch.int32)
+    ids[::997] = -1
+    ids[5::1999] = E + 7
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids.to(DEV), B, E)
+    s_ref, e_ref, n_ref = orc.moe_align_block_size(ids.numpy(), B, E)
+    assert int(npp.item()) == n_ref
+    np.testing.assert_array_equal(sorted_ids.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(expert_ids.cpu().numpy(), e_ref)
+
+
 @pytest.mark.parametrize("M,E,k,renorm", [(16, 128, 8, True), (256, 128, 8, True), (33, 64, 2, False), (5, 300, 6, True)])
 def test_topk_softmax(M, E, k, renorm):
     announce(f"topk M={M} E={E} k={k}")
@@ -106,6 +122,71 @@ def test_grouped_gemm(M, which):
 def test_grouped_gemm_other_blocks(B):
     announce(f"grouped gemm B={B}")
     _grouped(moe_case(40, seed=40), 40, 8, B, 1)
+
+
+def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
+    gen = torch.Generator().manual_seed(seed)
+    logits = torch.randn(M, E, generator=gen).to(torch.bfloat16)
+    W = torch.randint(-127, 128, (E, N, K), generator=gen, dtype=torch.int8)
+    SW = torch.rand(E, N, generator=gen) * 1e-2 + 1e-4
+    act = torch.randn(M * k, K, generator=gen).to(torch.bfloat16)
+    return logits, W, SW, act
+
+
+@pytest.mark.parametrize("shape", ["cfg3", "ragged"])
+def test_grouped_every_tile_config(shape):
+    """Each grouped tile configuration (forced through mw8_set_tuning) for
+    block sizes 64 and 128, gate_up-style (A row = sorted id // top_k, no
+    routed weight) and down-style (top_k 1, routed weight), bit-exact
+    against one oracle result per case."""
+    from minisgl_amd.kernel import lib as mw8lib
+
+    lib = mw8lib.load()
+    if shape == "cfg3":
+        c = moe_case(96, seed=96)
+        M, k = 96, 8
+        cases = []
+        for which in (1, 2):
+            if which == 1:
+                act, W, SW = c["hidden"], c["w1"], c["s_w1"]
+            else:
+                gen = torch.Generator().manual_seed(99)
+                act = torch.randn(M * k, c["w2"].shape[2], generator=gen).to(torch.bfloat16)
+                W, SW = c["w2"], c["s_w2"]
+            cases.append((which, act, W, SW))
+        logits = c["logits"]
+    else:
+        M, k = 50, 2
+        logits, W, SW, act = _ragged_expert_case(7, M=M, k=k)
+        cases = [(1, act[:M], W, SW), (2, act, W, SW)]
+    E = W.shape[0]
+    w_ref, ids_ref = orc.topk_softmax(f32(logits), k, True)
+    ids = torch.from_numpy(ids_ref).to(DEV)
+    tw = torch.from_numpy(w_ref).to(DEV)
+    try:
+        for which, act, W, SW in cases:
+            q, s = quant_per_token(act.to(DEV))
+            top_k, routed = (k, None) if which == 1 else (1, tw)
+            Wd, SWd = W.to(DEV), SW.to(DEV)
+            N = W.shape[1]
+            y_ref, acc_ref = orc.grouped_gemm_w8a8(
+                q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
+                routed=None if routed is None else w_ref, return_acc=True,
+            )
+            for B in (64, 128):
+                sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, E)
+                for cfg in range(-1, 7):
+                    announce(f"grouped {shape} gemm{which} B={B} cfg={cfg}")
+                    lib.mw8_set_tuning(-1, -1, cfg)
+                    out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
+                    fused_moe_kernel_w8a8(q, s, Wd, SWd, out, tw, sorted_ids, expert_ids, npp,
+                                          routed is not None, top_k, B, M * k)
+                    acc = fused_moe_kernel_w8a8_i32(q, Wd, sorted_ids, expert_ids, npp, top_k, B, M * k)
+                    torch.cuda.synchronize()
+                    np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref)
+                    assert bf16_bits_equal(out, y_ref).all()
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
 
 
 def test_sum_reduce():
