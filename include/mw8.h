@@ -86,9 +86,15 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
 void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 
 /*
- * Bytes of workspace mw8_gemm_w8a8_* needs for (M, N, K).  The current
- * kernels need none and return 0; the workspace arguments are kept so that
- * callers already pass one if a future configuration needs it.
+ * Bytes of workspace mw8_gemm_w8a8_* uses for (M, N, K): the int32 partial
+ * tiles of the tail-wave K split (M > 64, K % 128 == 0, 256 x 256 tiles:
+ * the r = T mod 256 tiles of the last partial wave, all T when T < 256, are
+ * cut into sp = min(256 / r, K / 128, 16) K ranges when sp >= 2; each range
+ * writes one 256 x 256 int32 tile, summed in range order by a second
+ * kernel on the same stream).  0 when no split applies.  A NULL or smaller
+ * workspace is not an error: the GEMM then runs every tile whole (same
+ * result, slower).  The workspace holds no state between calls; calls that
+ * share one must be ordered (one stream).  No reference counterpart.
  */
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

@@ -118,6 +118,34 @@ constexpr TileCfg kTileCfgs[] = {
 };
 constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
+// Split of the last, partial wave of 256 x 256 tiles (one resident tile per
+// CU): the r = T mod 256 tail tiles (all T tiles when T < 256) are cut into
+// sp = min(256 / r, K / 128, 16) K ranges when that gives sp >= 2.
+struct SplitPlan {
+  int64_t full = 0, tail = 0;
+  int sp = 1;
+  size_t ws = 0;
+};
+constexpr int64_t kSlotsPerWave = 256;
+
+SplitPlan plan_split(int64_t M, int64_t N, int64_t K) {
+  SplitPlan p;
+  if (M <= kDecodeMaxM || K % 128 != 0) return p;
+  const int64_t T = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t r = T % kSlotsPerWave;
+  if (r == 0) return p;
+  int64_t sp = kSlotsPerWave / r;
+  const int64_t nkt = K / 128;
+  if (sp > nkt) sp = nkt;
+  if (sp > 16) sp = 16;
+  if (sp < 2) return p;
+  p.full = T - r;
+  p.tail = r;
+  p.sp = static_cast<int>(sp);
+  p.ws = static_cast<size_t>(r) * sp * 65536 * sizeof(int32_t);
+  return p;
+}
+
 // Pick the configuration with the smallest modelled time: waves of
 // resident tiles x per-wave tile area / relative efficiency.  The
 // efficiencies are per-op throughputs measured on MI355X relative to the
@@ -134,13 +162,18 @@ int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   const Cand cands[] = {{16, 1, K > 8192 ? 1.45 : 1.35}, {12, 2, 1.2}, {7, 2, 1.0}};
   int best = 7;
   double best_cost = 1e300;
+  const SplitPlan sp = plan_split(M, N, K);
   for (const Cand& c : cands) {
     const TileCfg t = kTileCfgs[c.cfg];
     if (K % t.bk != 0) continue;
     const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
     const int64_t slots = 256 * static_cast<int64_t>(c.per_cu);
-    const int64_t waves = (tiles + slots - 1) / slots;
-    const double cost = static_cast<double>(waves) * t.bm * t.bn * c.per_cu / c.eff;
+    double waves = static_cast<double>((tiles + slots - 1) / slots);
+    // the 256 x 256 tail split: full waves plus one wave of 1/sp-length units
+    // (and the partial-tile reduction, modelled as a tenth of a wave)
+    if (t.bm == 256 && t.bn == 256 && sp.sp > 1)
+      waves = static_cast<double>(sp.full / kSlotsPerWave) + 1.0 / sp.sp + 0.1;
+    const double cost = waves * t.bm * t.bn * c.per_cu / c.eff;
     if (cost < best_cost) {
       best_cost = cost;
       best = c.cfg;
@@ -150,13 +183,24 @@ int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
 }
 
 template <int EPI>
-void dispatch_tile(const GemmArgs& g, hipStream_t st) {
+void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   int cfg = g_tile_cfg.load(std::memory_order_relaxed);
   if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && g.K % kTileCfgs[cfg].bk != 0))
     cfg = default_tile_cfg(g.M, g.N, g.K);
   const TileCfg c = kTileCfgs[cfg];
-  const unsigned tiles =
+  unsigned tiles =
       static_cast<unsigned>(((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn));
+  // tail split (256 x 256 ring configurations): needs the caller's workspace
+  const SplitPlan sp = plan_split(g.M, g.N, g.K);
+  const bool split = c.dma && c.bm == 256 && c.bn == 256 && sp.sp > 1 && ws != nullptr &&
+                     ws_bytes >= sp.ws && g.K % c.bk == 0;
+  g.tail_split = 1;
+  if (split) {
+    g.part = static_cast<int32_t*>(ws);
+    g.full_tiles = sp.full;
+    g.tail_split = sp.sp;
+    tiles = static_cast<unsigned>(sp.full + sp.tail * sp.sp);
+  }
   switch (cfg) {
     case 0: launch_tile<256, 256, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 1: launch_tile<256, 256, 64, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
@@ -177,13 +221,20 @@ void dispatch_tile(const GemmArgs& g, hipStream_t st) {
     case 17: launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
+  if (split) {
+    const int64_t threads = sp.tail * 256 * 32;
+    hipLaunchKernelGGL(split_reduce_kernel<EPI>, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                       dim3(256), 0, st, g);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+
+
 int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                const void* bias, void* out, int64_t M, int64_t N, int64_t K, hipStream_t st,
-                int epi) {
+                const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* ws,
+                size_t ws_bytes, hipStream_t st, int epi) {
   MW8_REQUIRE(A && W && out, kErrArg, "gemm: null A/W/out");
   MW8_REQUIRE(epi == kEpiI32 || (sa && sw), kErrArg, "gemm: null scales");
   MW8_REQUIRE(M >= 0 && N > 0 && K > 0, kErrShape, "gemm: bad sizes M=%lld N=%lld K=%lld",
@@ -200,12 +251,14 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
   g.bias = static_cast<const uint16_t*>(bias);
   g.out = out; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldo = N;
   g.top_k = 1;
+  g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   if (M <= kDecodeMaxM) {
     if (epi == kEpiBf16) dispatch_decode<kEpiBf16>(g, st);
     else dispatch_decode<kEpiI32>(g, st);
   } else {
-    if (epi == kEpiBf16) dispatch_tile<kEpiBf16>(g, st);
-    else dispatch_tile<kEpiI32>(g, st);
+    MW8_REQUIRE(ws == nullptr || aligned16(ws), kErrAlign, "gemm: workspace needs 16-byte alignment");
+    if (epi == kEpiBf16) dispatch_tile<kEpiBf16>(g, ws, ws_bytes, st);
+    else dispatch_tile<kEpiI32>(g, ws, ws_bytes, st);
   }
   return check_launch("gemm");
 }
@@ -218,17 +271,20 @@ void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
   g_moe_cfg.store(moe_cfg, std::memory_order_relaxed);
 }
 
-size_t gemm_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return plan_split(M, N, K).ws;
+}
 
 int gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                   const void* bias, void* y, int64_t M, int64_t N, int64_t K, void*, size_t,
-                   hipStream_t st) {
-  return gemm_common(A, sa, W, sw, bias, y, M, N, K, st, kEpiBf16);
+                   const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,
+                   size_t ws_bytes, hipStream_t st) {
+  return gemm_common(A, sa, W, sw, bias, y, M, N, K, ws, ws_bytes, st, kEpiBf16);
 }
 
 int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int64_t N,
-                  int64_t K, void*, size_t, hipStream_t st) {
-  return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, st, kEpiI32);
+                  int64_t K, void* ws, size_t ws_bytes, hipStream_t st) {
+  return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, ws, ws_bytes, st, kEpiI32);
 }
 
 // Grouped (fused-MoE) GEMM launchers over expert-sorted rows.  BM equals

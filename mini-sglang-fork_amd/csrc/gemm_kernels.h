@@ -55,6 +55,16 @@ struct GemmArgs {
   int64_t num_valid;           // M * top_k
   int32_t top_k;
   int32_t num_experts;         // blocks owned by an id outside [0, E) are skipped
+  // dense split tail (256 x 256 tilings only): blocks [0, full_tiles) own
+  // whole tiles; block full_tiles + u owns K range u % tail_split of tail
+  // tile full_tiles + u / tail_split and writes its int32 partial tile to
+  // part[u][256][256] (summed by split_reduce_kernel).
+  int32_t* part;
+  int64_t full_tiles;
+  int32_t tail_split;          // <= 1: no split
+  // bf16 output rows are 16-byte aligned with N % 8 == 0: the tile core may
+  // assemble its output tile in LDS and store it with 16-byte row writes
+  int32_t staged_out;
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -111,6 +121,26 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 // kGroupM A panels and a handful of W panels.
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
+
+// Tile index t of the grouped raster -> (pid_m, pid_n).
+__device__ __forceinline__ void tile_of_index(int64_t t, int64_t tiles_m, int64_t tiles_n,
+                                              int64_t& pid_m, int64_t& pid_n) {
+  const int64_t per_group = kGroupM * tiles_n;
+  const int64_t group = t / per_group;
+  const int64_t first_m = group * kGroupM;
+  const int64_t gsize = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const int64_t in_group = t % per_group;
+  pid_m = first_m + in_group % gsize;
+  pid_n = in_group / gsize;
+}
+
+// Block b (b < count) -> tile index in [0, count): XCD b % 8 gets a
+// contiguous range of tile indices.
+__device__ __forceinline__ int64_t xcd_tile_index(int64_t b, int64_t count) {
+  const int64_t xcd = b % kXcds, local = b / kXcds;
+  const int64_t base = count / kXcds, rem = count % kXcds;
+  return xcd * base + (xcd < rem ? xcd : rem) + local;
+}
 
 __device__ __forceinline__ void tile_of_block(int64_t b, int64_t tiles_m, int64_t tiles_n,
                                               int64_t& pid_m, int64_t& pid_n) {
@@ -327,6 +357,9 @@ __device__ __forceinline__ void wait_stages(int n) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Buffer-resource word 3 for raw byte-addressed buffers on gfx9-family parts.
+constexpr int kBufferFlags = 0x00020000;
+
 // Workgroup barrier without the release/acquire fence of __syncthreads()
 // (which would force vmcnt(0) and drain the prefetch ring).  The empty asm
 // statements keep the compiler from moving memory accesses across it.
@@ -361,6 +394,8 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   const int8_t* W = g.W;
   const float* sw = g.sw;
   int64_t m0, n0;
+  int64_t split_unit = -1;  // split-tail unit (writes an int32 partial tile), -1: whole tile
+  int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
   if constexpr (Rows::kGrouped) {
     n0 = static_cast<int64_t>(blockIdx.x) * BN;
     m0 = static_cast<int64_t>(blockIdx.y) * BM;
@@ -370,16 +405,37 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
   } else {
+    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
     int64_t pm, pn;
-    tile_of_block(blockIdx.x, (g.M + BM - 1) / BM, (g.N + BN - 1) / BN, pm, pn);
+    if (g.tail_split > 1) {
+      if (blockIdx.x < g.full_tiles) {
+        tile_of_index(xcd_tile_index(blockIdx.x, g.full_tiles), tm, tn, pm, pn);
+      } else {
+        split_unit = static_cast<int64_t>(blockIdx.x) - g.full_tiles;
+        tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
+        const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
+        kt_begin = static_cast<int>(nkt * sp / g.tail_split);
+        kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
+      }
+    } else {
+      tile_of_block(blockIdx.x, tm, tn, pm, pn);
+    }
     m0 = pm * BM;
     n0 = pn * BN;
   }
 
   // ---- per-lane DMA sources: instruction j of this wave fills LDS units
   // (j*kWaves + wave)*64 .. +63 of the tile; lane -> (row, chunk)
-  const int8_t* a_src[kLA];
-  const int8_t* w_src[kLB];
+  // DMA through buffer views (32-bit per-lane offsets, the K position in the
+  // scalar offset): the A view starts at the tile's first row (row 0 for
+  // gathered rows), the W view at the tile's first weight row.  The host
+  // keeps every offset below 2^31 (gemm_common / moe_gemm_w8a8 checks).
+  const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(g.A + a_base_row * g.lda), 0, 0x7fffffff, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(W + n0 * g.K), 0, 0x7fffffff, kBufferFlags);
+  uint32_t a_doff[kLA], w_doff[kLB];
 #pragma unroll
   for (int j = 0; j < kLA; ++j) {
     const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
@@ -391,25 +447,27 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     } else {
       arow = m0 + row < g.M ? m0 + row : g.M - 1;
     }
-    a_src[j] = g.A + arow * g.lda + 16 * c;
+    a_doff[j] = static_cast<uint32_t>((arow - a_base_row) * g.lda + 16 * c);
   }
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
     const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
     const int c = (unit % kChunks) ^ swz_f<BK>(row);
     const int64_t wrow = n0 + row < g.N ? n0 + row : g.N - 1;
-    w_src[j] = W + wrow * g.K + 16 * c;
+    w_doff[j] = static_cast<uint32_t>((wrow - n0) * g.K + 16 * c);
   }
-  const int nk = static_cast<int>(g.K / BK);
+  const int nk = kt_end - kt_begin;
   auto issue = [&](int kt) {
     unsigned char* base = lds + (kt % NSTAGE) * kStage;
-    const int64_t k0 = static_cast<int64_t>(kt) * BK;
+    const int k0 = (kt_begin + kt) * BK;
 #pragma unroll
     for (int j = 0; j < kLA; ++j)
-      __builtin_amdgcn_global_load_lds(a_src[j] + k0, (lds_ptr_t)(base + (j * kWaves + wave) * 1024), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + (j * kWaves + wave) * 1024), 16,
+                                               a_doff[j], k0, 0, 0);
 #pragma unroll
     for (int j = 0; j < kLB; ++j)
-      __builtin_amdgcn_global_load_lds(w_src[j] + k0, (lds_ptr_t)(base + kStageA + (j * kWaves + wave) * 1024), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(base + kStageA + (j * kWaves + wave) * 1024), 16,
+                                               w_doff[j], k0, 0, 0);
   };
 
   const int frow = lane & 31, fgrp = lane >> 5;
@@ -480,6 +538,104 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   }
   mfmas(kSub & 1);
   mfmas((kSub - 1) & 1);
+
+  if constexpr (!Rows::kGrouped) {
+    if (split_unit >= 0) {  // split-tail unit: raw int32 partial tile, rows/cols unmasked
+      int32_t* pt = g.part + split_unit * (BM * BN);
+#pragma unroll
+      for (int i = 0; i < kFM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+#pragma unroll
+          for (int j = 0; j < kFN; ++j) pt[r * BN + wn * kWaveN + 32 * j + frow] = acc[i][j][v];
+        }
+      return;
+    }
+  }
+
+  // ---- staged bf16 epilogue: the tile is assembled in the (now idle) LDS
+  // ring and written with 16-byte row stores.  Lanes 2k / 2k+1 swap one
+  // value so that each writes two adjacent columns of one row as a 32-bit
+  // word; the staging layout XORs the 16-byte chunk index of row r with
+  // sf(r), which keeps both the word writes (rows R, R+1, R+4, R+5 per
+  // instruction) and the 16-byte row reads on distinct LDS banks.
+  if constexpr (EPI == kEpiBf16 && BM * BN * 2 <= NSTAGE * kStage && BN >= 128) {
+    if (g.staged_out) {
+      constexpr int kRowBytes = BN * 2;
+      auto sf = [](int r) { return 4 * ((r & 1) | (((r >> 2) & 1) << 1)); };
+      __syncthreads();  // every wave is past its last LDS fragment read
+      const bool odd = (lane & 1) != 0;
+#pragma unroll
+      for (int i = 0; i < kFM; ++i) {
+#pragma unroll
+        for (int vp = 0; vp < 8; ++vp) {
+          const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
+          const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
+          float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
+          if constexpr (Rows::kGrouped) {
+            const int32_t p0 = g.sorted_ids[m0 + r0], p1 = g.sorted_ids[m0 + r0 + 1];
+            sa0 = p0 < g.num_valid ? g.sa[p0 / g.top_k] : 0.0f;
+            sa1 = p1 < g.num_valid ? g.sa[p1 / g.top_k] : 0.0f;
+            if (g.topk_w) {
+              rt0 = p0 < g.num_valid ? g.topk_w[p0] : 0.0f;
+              rt1 = p1 < g.num_valid ? g.topk_w[p1] : 0.0f;
+            }
+          } else {
+            const int64_t ma = m0 + r0 < g.M ? m0 + r0 : g.M - 1;
+            const int64_t mb = m0 + r0 + 1 < g.M ? m0 + r0 + 1 : g.M - 1;
+            sa0 = g.sa[ma];
+            sa1 = g.sa[mb];
+          }
+#pragma unroll
+          for (int j = 0; j < kFN; ++j) {
+            const int c = wn * kWaveN + 32 * j + frow;
+            const int64_t n = n0 + c < g.N ? n0 + c : g.N - 1;
+            const float swv = sw[n];
+            float t0 = epi_scale(acc[i][j][v0], sa0, swv);
+            float t1 = epi_scale(acc[i][j][v0 + 1], sa1, swv);
+            if (!Rows::kGrouped && g.bias) {
+              const float b = bf16_to_f32(g.bias[n]);
+              t0 = t0 + b;
+              t1 = t1 + b;
+            }
+            if (Rows::kGrouped && g.topk_w) {
+              t0 = t0 * rt0;
+              t1 = t1 * rt1;
+            }
+            // even lane: row r0, columns (c, c+1); odd lane: row r0+1, columns (c-1, c)
+            const float send = odd ? t0 : t1;
+            const float got = __builtin_bit_cast(
+                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
+            const int rr = odd ? r0 + 1 : r0, cc = odd ? c - 1 : c;
+            *reinterpret_cast<bf16x2*>(lds + rr * kRowBytes + (((cc >> 3) ^ sf(rr)) << 4) + (cc & 7) * 2) = pr;
+          }
+        }
+      }
+      __syncthreads();
+      constexpr int kChunksRow = BN / 8;
+      constexpr int kThreads = 64 * kWaves;
+#pragma unroll
+      for (int q0 = 0; q0 < BM * kChunksRow; q0 += kThreads) {
+        const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
+        int64_t orow;
+        if constexpr (Rows::kGrouped) {
+          const int32_t p = g.sorted_ids[m0 + r];
+          orow = p < g.num_valid ? p : -1;
+        } else {
+          orow = m0 + r < g.M ? m0 + r : -1;
+        }
+        const int64_t n = n0 + ch * 8;
+        if (orow >= 0 && n < g.N) {
+          const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
+          *reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n) = d;
+        }
+      }
+      return;
+    }
+  }
 
   // ---- epilogue: lane holds column (lane & 31) of each 32x32 block
 #pragma unroll
@@ -701,6 +857,54 @@ __global__ __launch_bounds__(64 * WAVES) void decode_gemm_kernel(GemmArgs g) {
       static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
     else
       static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
+  }
+}
+
+// ------------------------------------------------------------------------
+// Split-tail reduction: out[tile rows, tile cols] = epilogue(sum_s part[u0 + s])
+// with the partials summed in split order (exact int32).  One thread per 8
+// consecutive columns of one tile row.
+// ------------------------------------------------------------------------
+template <int EPI>
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
+  const int64_t tm = (g.M + 255) / 256, tn = (g.N + 255) / 256;
+  const int64_t tail = tm * tn - g.full_tiles;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (tile, row, col8)
+  if (idx >= tail * 256 * 32) return;
+  const int64_t tt = idx / (256 * 32);
+  const int r = static_cast<int>((idx / 32) % 256), c8 = static_cast<int>(idx % 32) * 8;
+  int64_t pm, pn;
+  tile_of_index(g.full_tiles + tt, tm, tn, pm, pn);
+  const int64_t m = pm * 256 + r;
+  if (m >= g.M) return;
+  const int32_t* p = g.part + (tt * g.tail_split) * 65536 + r * 256 + c8;
+  int32_t a[8];
+  {
+    const v4i x0 = *reinterpret_cast<const v4i*>(p), x1 = *reinterpret_cast<const v4i*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { a[j] = x0[j]; a[4 + j] = x1[j]; }
+  }
+  for (int s = 1; s < g.tail_split; ++s) {
+    const int32_t* q = p + static_cast<int64_t>(s) * 65536;
+    const v4i x0 = *reinterpret_cast<const v4i*>(q), x1 = *reinterpret_cast<const v4i*>(q + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { a[j] += x0[j]; a[4 + j] += x1[j]; }
+  }
+  const int64_t n0 = pn * 256 + c8;
+  if constexpr (EPI == kEpiBf16) {
+    const float sa = g.sa[m];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t n = n0 + j;
+      if (n < g.N)
+        static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a[j], sa, g.sw[n], g.bias, n, 1.0f, false);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t n = n0 + j;
+      if (n < g.N) static_cast<int32_t*>(g.out)[m * g.ldo + n] = a[j];
+    }
   }
 }
 

@@ -319,6 +319,10 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   MW8_REQUIRE(top_k >= 1 && E >= 1 && num_valid >= 0 && max_sorted >= 0, kErrShape,
               "moe_gemm: bad routing sizes");
   MW8_REQUIRE(aligned16(A) && aligned16(W), kErrAlign, "moe_gemm: A and W need 16-byte alignment");
+  // the tile core addresses A rows through a 32-bit buffer offset
+  MW8_REQUIRE((num_valid / top_k + 1) * K < (1ll << 31), kErrShape,
+              "moe_gemm: token matrix of %lld x %lld bytes exceeds 2^31", (long long)(num_valid / top_k),
+              (long long)K);
   const int64_t blocks = max_sorted / bsz;  // blocks past num_post_pad exit on device
   if (blocks == 0) return kOk;
   MW8_REQUIRE(blocks < 65536, kErrShape, "moe_gemm: too many expert blocks");
@@ -327,6 +331,7 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
   g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   if (bsz == 16) {
     const int64_t ldl = ((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
     MW8_REQUIRE(16 * ldl <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",

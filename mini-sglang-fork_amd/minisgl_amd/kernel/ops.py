@@ -41,11 +41,12 @@ _WORKSPACE: Dict[torch.device, torch.Tensor] = {}
 
 
 def gemm_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
-    """Zero-initialised split-K workspace for (M, N, K), cached per device.
+    """Workspace for the GEMM's tail-wave K split at (M, N, K), cached per
+    device and grown on demand (None when no split applies).
 
-    The kernels leave the workspace's arrival counters at zero after every
-    call, so the buffer is reusable as long as calls sharing it are ordered
-    on one stream.  Reserve the largest size before capturing a graph.
+    It holds int32 partial tiles only for the duration of one call, so it is
+    reusable by any calls ordered on one stream.  Reserve the largest size
+    before capturing a graph (growing it allocates).
     """
     need = int(load().mw8_gemm_workspace_bytes(M, N, K))
     if need == 0:

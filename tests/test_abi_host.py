@@ -51,6 +51,13 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_moe_align_max_padded(12, 5, 4) == 27
     assert lib.mw8_moe_align_max_padded(128, 129, 16) == 128 + 129 * 15
     assert lib.mw8_gemm_workspace_bytes(1, 5120, 5120) == 0
+    # tail split of 256x256 tilings: r = T mod 256 tail tiles, sp = min(256 // r, K / 128, 16)
+    # K ranges each, one int32 256x256 partial tile per (tile, range)
+    assert lib.mw8_gemm_workspace_bytes(512, 7168, 5120) == 56 * 4 * 256 * 256 * 4
+    assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 64 * 4 * 256 * 256 * 4
+    assert lib.mw8_gemm_workspace_bytes(8192, 34816, 5120) == 0  # 4352 tiles: whole waves
+    assert lib.mw8_gemm_workspace_bytes(4096, 7168, 5120) == 0   # 192 tail tiles: no split
+    assert lib.mw8_gemm_workspace_bytes(512, 5120, 5120 + 64) == 0  # K % 128 != 0
 
 
 FAKE_A, FAKE_B, FAKE_C = 4096, 8192, 12288  # aligned non-null stand-ins: never dereferenced

@@ -118,6 +118,39 @@ def test_gemm_workspace_reuse_and_zero_rows():
     assert empty.shape == (0, 32)
 
 
+@pytest.mark.parametrize(
+    "M,K,N", [(512, 5120, 7168), (300, 1280, 600), (1000, 2048, 1000), (4500, 768, 3840), (2304, 1280, 7168)]
+)
+def test_gemm_split_tail(M, K, N):
+    """Tail-wave K split of the 256x256 tilings: the last partial wave's tiles
+    are cut into K ranges whose int32 partial tiles go to the workspace and
+    are summed by the reduction kernel.  Bit-exact against the oracle (row
+    sample for the larger cases) and against the launch without workspace,
+    which runs the tiles whole."""
+    import ctypes
+
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm split tail M={M} K={K} N={N}")
+    lib = load()
+    T = -(-M // 256) * -(-N // 256)
+    r = T % 256
+    sp = min(256 // r, K // 128, 16) if r else 0
+    want_ws = r * sp * 65536 * 4 if sp >= 2 else 0
+    assert lib.mw8_gemm_workspace_bytes(M, N, K) == want_ws
+    rows = None if M <= 1024 else np.unique(np.concatenate([[0, M - 1], np.arange(M - 300, M, 7)]))
+    _run_case(M, K, N, seed=7, rows=rows)
+    c = linear_case(M, K, N, seed=8)
+    q, s = quant_per_token(c["x"].to(DEV))
+    w = c["w"].to(DEV)
+    split = gemm_w8a8_i32(q, w)
+    whole = torch.empty_like(split)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = lib.mw8_gemm_w8a8_i32(q.data_ptr(), w.data_ptr(), whole.data_ptr(), M, N, K, None, 0, st)
+    assert rc == 0
+    assert torch.equal(split, whole)
+
+
 def test_gemm_rejects_bad_k():
     a = torch.zeros(4, 40, dtype=torch.int8, device=DEV)
     w = torch.zeros(8, 40, dtype=torch.int8, device=DEV)
