@@ -16,12 +16,17 @@ std::atomic<int> g_tile_cfg{-1};
 std::atomic<int> g_moe_cfg{-1};
 
 // ------------------------------------------------------------------ decode
-// (rows of 16 per block, waves per block, K steps of loads in flight)
+// (rows of 16 per block, waves per block, K steps per load batch).
+// 0-6: decode_gemm_kernel (U steps loaded, then their MFMAs);
+// 7-12: decode2_gemm_kernel (batches double-buffered, branch-free loads).
 struct DecodeCfg {
   int rg, waves, u;
 };
 constexpr DecodeCfg kDecodeCfgs[] = {
     {1, 4, 8}, {2, 4, 4}, {1, 8, 4}, {2, 8, 4}, {4, 4, 4}, {4, 8, 2}, {2, 8, 2},
+    {1, 16, 4}, {1, 8, 4}, {2, 16, 2}, {1, 16, 2}, {2, 8, 4}, {4, 16, 1},
+    // 13-21: decode3_gemm_kernel (16 rows, LDS DMA ring; u = ring depth)
+    {1, 4, 4}, {1, 4, 3}, {1, 2, 4}, {1, 8, 2}, {1, 4, 2}, {1, 2, 3}, {1, 2, 2}, {1, 1, 4}, {1, 8, 3},
 };
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
@@ -30,6 +35,29 @@ void launch_decode(const GemmArgs& g, hipStream_t st) {
   const unsigned blocks = static_cast<unsigned>((g.N + 16 * RG - 1) / (16 * RG));
   hipLaunchKernelGGL((decode_gemm_kernel<RG, TG, WAVES, U, EPI>), dim3(blocks), dim3(64 * WAVES), 0,
                      st, g);
+}
+
+template <int RG, int TG, int WAVES, int U, int EPI>
+void launch_decode2(const GemmArgs& g, hipStream_t st) {
+  const unsigned blocks = static_cast<unsigned>((g.N + 16 * RG - 1) / (16 * RG));
+  hipLaunchKernelGGL((decode2_gemm_kernel<RG, TG, WAVES, U, EPI>), dim3(blocks), dim3(64 * WAVES), 0,
+                     st, g);
+}
+
+// Ring depth is capped by the token-register ring (D x 4 x TG x 4 VGPRs).
+template <int TG, int WAVES, int D, int EPI>
+void launch_decode3(const GemmArgs& g, hipStream_t st) {
+  constexpr int kD = TG == 1 ? D : (TG == 2 ? (D < 3 ? D : 3) : 2);
+  constexpr int kLds = DecodeRing<TG, WAVES, kD>::kLds;
+  auto kern = decode3_gemm_kernel<TG, WAVES, kD, EPI>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    attr_set = true;
+  }
+  const unsigned blocks = static_cast<unsigned>((g.N + 15) / 16);
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WAVES), kLds, st, g);
 }
 
 template <int TG, int EPI>
@@ -41,15 +69,40 @@ void decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
     case 3: launch_decode<2, TG, 8, 4, EPI>(g, st); break;
     case 4: launch_decode<4, TG, 4, 4, EPI>(g, st); break;
     case 5: launch_decode<4, TG, 8, 2, EPI>(g, st); break;
-    default: launch_decode<2, TG, 8, 2, EPI>(g, st); break;
+    case 6: launch_decode<2, TG, 8, 2, EPI>(g, st); break;
+    case 7: launch_decode2<1, TG, 16, 4, EPI>(g, st); break;
+    case 8: launch_decode2<1, TG, 8, 4, EPI>(g, st); break;
+    case 9: launch_decode2<2, TG, 16, 2, EPI>(g, st); break;
+    case 10: launch_decode2<1, TG, 16, 2, EPI>(g, st); break;
+    case 11: launch_decode2<2, TG, 8, 4, EPI>(g, st); break;
+    case 12: launch_decode2<4, TG, 16, 1, EPI>(g, st); break;
+    case 13: launch_decode3<TG, 4, 4, EPI>(g, st); break;
+    case 14: launch_decode3<TG, 4, 3, EPI>(g, st); break;
+    case 15: launch_decode3<TG, 2, 4, EPI>(g, st); break;
+    case 16: launch_decode3<TG, 8, 2, EPI>(g, st); break;
+    case 17: launch_decode3<TG, 4, 2, EPI>(g, st); break;
+    case 18: launch_decode3<TG, 2, 3, EPI>(g, st); break;
+    case 19: launch_decode3<TG, 2, 2, EPI>(g, st); break;
+    case 20: launch_decode3<TG, 1, 4, EPI>(g, st); break;
+    default: launch_decode3<TG, 8, 3, EPI>(g, st); break;
   }
 }
 
+// Measured on MI355X at the Qwen3-14B shapes (K 5120 / 17408, N 5120 -
+// 34816).  Up to 32 tokens the LDS DMA ring (decode3) streams fastest:
+// at M = 1, 4 waves x 3 slots per block for wide N (gate_up: 32.6 us,
+// 5.5 TB/s) and 2 waves x 2 slots otherwise (o_proj: 7.9 us); for 2-32
+// tokens one wave x 4 slots per block (more resident blocks per CU).
+// From 33 tokens on the token operand, read per wave through the texture
+// path, costs more than the weight stream: the register-streaming core
+// with 32 rows over 8 waves (cfg 3) wins, or 64 rows per block for very
+// wide N (cfg 4), which keeps fewer blocks re-reading the token panel.
 int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
-  (void)N;
   (void)K;
-  if (M <= 16) return 0;
-  return 5;
+  if (M == 1) return N >= 16384 ? 14 : 19;
+  if (M <= 32) return 20;
+  if (M > 48 && N >= 16384) return 4;
+  return 3;
 }
 
 template <int EPI>
@@ -149,17 +202,18 @@ SplitPlan plan_split(int64_t M, int64_t N, int64_t K) {
 // Pick the configuration with the smallest modelled time: waves of
 // resident tiles x per-wave tile area / relative efficiency.  The
 // efficiencies are per-op throughputs measured on MI355X relative to the
-// 128x128 ring (cfg 7, two blocks per CU): the 16-wave 256x256 BK=128 ring
-// (cfg 16, one block per CU) runs ~1.35x faster per op at K ~ 5K and
-// ~1.45x at K ~ 17K; the 8-wave 256x128 ring (cfg 12, two blocks per CU)
-// ~1.2x.  Shapes with K % 64 != 0 use the register-staged core.
+// 128x128 ring (cfg 7, two blocks per CU): the 8-wave 256x256 BK=128 ring
+// with 64x128 wave tiles (cfg 14, one block per CU) runs ~1.35x faster per
+// op at K ~ 5K and ~1.37x at K ~ 17K (3-5% ahead of the 16-wave cfg 16);
+// the 8-wave 256x128 ring (cfg 12, two blocks per CU) ~1.12x.  Shapes with
+// K % 64 != 0 use the register-staged core.
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   if (K % 64 != 0) return 2;
   struct Cand {
     int cfg, per_cu;
     double eff;
   };
-  const Cand cands[] = {{16, 1, K > 8192 ? 1.45 : 1.35}, {12, 2, 1.2}, {7, 2, 1.0}};
+  const Cand cands[] = {{14, 1, K > 8192 ? 1.37 : 1.35}, {12, 2, 1.12}, {7, 2, 1.0}};
   int best = 7;
   double best_cost = 1e300;
   const SplitPlan sp = plan_split(M, N, K);

@@ -357,6 +357,18 @@ __device__ __forceinline__ void wait_stages(int n) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// A pointer the compiler can prove wave-uniform (it lives in SGPRs).  A
+// buffer descriptor built from a pointer it cannot prove uniform is kept in
+// VGPRs, and every buffer load through it is then wrapped in a per-lane
+// "waterfall" loop of readfirstlane/compare/exec-mask instructions.
+template <class T>
+__device__ __forceinline__ T* scalar_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Buffer-resource word 3 for raw byte-addressed buffers on gfx9-family parts.
 constexpr int kBufferFlags = 0x00020000;
 
@@ -388,7 +400,8 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
                 kLB * kRowsPerInst * kWaves == BN, "DMA split");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
   extern __shared__ __align__(16) unsigned char lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave / WN, wn = wave % WN;
 
   const int8_t* W = g.W;
@@ -432,9 +445,9 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // keeps every offset below 2^31 (gemm_common / moe_gemm_w8a8 checks).
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(g.A + a_base_row * g.lda), 0, 0x7fffffff, kBufferFlags);
+      scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(W + n0 * g.K), 0, 0x7fffffff, kBufferFlags);
+      scalar_ptr(const_cast<int8_t*>(W + n0 * g.K)), 0, 0x7fffffff, kBufferFlags);
   uint32_t a_doff[kLA], w_doff[kLB];
 #pragma unroll
   for (int j = 0; j < kLA; ++j) {
@@ -526,9 +539,11 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     const int later = nk - 2 - kt;  // stages after kt+1 already issued
     wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
     raw_barrier();
-    if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+    // MFMAs first after the barrier: the refill DMA of the freed buffer is
+    // issued behind them so that the matrix pipe restarts at once
     read_frags(kt + 1, 0);
     mfmas((kSub - 1) & 1);  // substep kSub-1
+    if (kt + NSTAGE < nk) issue(kt + NSTAGE);
     read_frags(kt + 1, 1);
   }
 #pragma unroll
@@ -858,6 +873,301 @@ __global__ __launch_bounds__(64 * WAVES) void decode_gemm_kernel(GemmArgs g) {
     else
       static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
   }
+}
+
+// ------------------------------------------------------------------------
+// Dense small-M core, pipelined: weight streaming with every load batch in
+// flight while the previous batch's MFMAs run
+// ------------------------------------------------------------------------
+// Same data mapping and in-block K split as decode_gemm_kernel, restructured
+// for memory-level parallelism: wave w streams K steps [s_begin, s_end) of
+// the block's RG*16 weight rows in batches of U 64-byte steps; batch b+1 is
+// requested before the MFMAs of batch b (two register sets, the phase order
+// pinned with scheduling barriers).  No load is predicated: weight loads
+// read a clamped in-bounds address, and the token operand of a step past
+// the wave's range, of K bytes past the row end, or of a token row >= M is
+// read from a block of zeros instead, so its products vanish and no select
+// waits on loaded data.  With WAVES up to 16 (1024-thread blocks) a block
+// keeps WAVES * U * RG KB of weights in flight, enough to request a whole
+// 26-89 MB weight matrix almost at once.
+// Never written: a global (not constant) object, so that a select between it
+// and a kernel-argument pointer still yields a global-memory load.
+__device__ __align__(16) int8_t kZeroChunk[16] = {0};
+
+template <int RG, int TG, int WAVES, int U, int EPI>
+__global__ __launch_bounds__(64 * WAVES) void decode2_gemm_kernel(GemmArgs g) {
+  constexpr int kAcc = RG * TG * 4;  // int32 accumulators per lane
+  __shared__ int32_t red[kAcc][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * RG);
+  const int64_t steps = (g.K + 63) / 64;
+  const int64_t s_begin = steps * wave / WAVES, s_end = steps * (wave + 1) / WAVES;
+  const int64_t k_last = g.K - 16;  // last valid 16-byte chunk start (K % 16 == 0)
+
+  const int8_t* wp[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    const int64_t n = n0 + 16 * rg + r16;
+    wp[rg] = g.W + (n < g.N ? n : g.N - 1) * g.K;
+  }
+  const int8_t* xp[TG];
+  bool xok[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    const int64_t m = 16 * tg + r16;
+    xok[tg] = m < g.M;
+    xp[tg] = g.A + (xok[tg] ? m : 0) * g.lda;
+  }
+  v4i acc[RG][TG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) acc[rg][tg] = v4i{0};
+
+  v4i wv[2][U][RG], xv[2][U][TG];
+  // batch starting at step s0 into register set b
+  auto load_batch = [&](int b, int64_t s0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = (s0 + u) * 64 + 16 * grp;
+      const bool in = (s0 + u < s_end) && (k < g.K);
+      const int64_t kc = k < k_last ? k : k_last;
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) wv[b][u][rg] = *reinterpret_cast<const v4i*>(wp[rg] + kc);
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg)
+        xv[b][u][tg] = *reinterpret_cast<const v4i*>((in && xok[tg]) ? xp[tg] + kc : kZeroChunk);
+    }
+  };
+  auto mfma_batch = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int tg = 0; tg < TG; ++tg)
+          acc[rg][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[b][u][rg], xv[b][u][tg], acc[rg][tg], 0, 0, 0);
+  };
+
+  if (s_begin < s_end) {
+    load_batch(0, s_begin);
+    int64_t s0 = s_begin;
+    // two batches per trip so that the register sets are compile-time indices
+    for (; s0 + 2 * U < s_end; s0 += 2 * U) {
+      load_batch(1, s0 + U);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_batch(0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_batch(0, s0 + 2 * U);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_batch(1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s0 + U < s_end) {
+      load_batch(1, s0 + U);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_batch(0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_batch(1);
+    } else {
+      mfma_batch(0);
+    }
+  }
+
+  __syncthreads();  // red[] zeroed by every thread before any wave adds into it
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) atomicAdd(&red[(rg * TG + tg) * 4 + v][lane], acc[rg][tg][v]);
+  __syncthreads();
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) {
+    const int j = e >> 6, l = e & 63;
+    const int rg = j / (TG * 4), tg = (j / 4) % TG, v = j & 3;
+    const int64_t n = n0 + 16 * rg + 4 * (l >> 4) + v;
+    const int64_t m = 16 * tg + (l & 15);
+    if (n >= g.N || m >= g.M) continue;
+    const int32_t a = red[j][l];
+    if constexpr (EPI == kEpiBf16)
+      static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
+    else
+      static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
+  }
+}
+
+// ------------------------------------------------------------------------
+// Dense small-M core, DMA ring: weights streamed to LDS in row-contiguous
+// 256-byte segments
+// ------------------------------------------------------------------------
+// Block = WAVES waves over 16 weight rows; wave w owns K stages
+// [s_begin, s_end) of 256 bytes each and streams them through a private
+// ring of D LDS slots (16 rows x 256 B = 4 KB per slot) with
+// buffer_load ... lds: one DMA instruction moves 4 rows x 256 contiguous
+// bytes (1 KB), so every request covers whole 128-byte lines, and no VGPR
+// holds data in flight.  The lane that fills LDS chunk c' of row r fetches
+// global chunk c' ^ (r & 15): a fragment read (lane -> row l%16, chunk
+// 4*kb + l/16) then touches 16 distinct 16-byte bank groups.  The token
+// operand of each stage (16 bytes per lane per 64-byte K block, L1/L2
+// resident) is loaded with plain loads into a register ring of the same
+// depth, issued right after the stage's DMA, so one vmcnt wait covers both
+// and the D-1 later stages stay in flight.  Token rows >= M and K bytes
+// past the row end read a block of zeros; weight bytes past a row end read
+// the next row (in bounds, multiplied by zero) and rows past N read as
+// zeros through the buffer range check.  No barrier inside the loop; the
+// waves' int32 partials are summed in LDS as in decode_gemm_kernel.
+constexpr int kRingStage = 4096;  // 16 rows x 256 B
+
+template <int TG, int WAVES, int D>
+struct DecodeRing {
+  static constexpr int kLds = WAVES * D * kRingStage;
+};
+
+// s_waitcnt vmcnt(n) (no lgkm wait), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// Compile-time unrolled drain of a D-slot ring: slot d waits until at most
+// (D-1-d) stages of OPS vector memory ops each remain in flight, then runs.
+template <int D, int OPS, int d>
+struct RingDrain {
+  template <class F>
+  __device__ __forceinline__ static void run(F& consume) {
+    wait_vmcnt<(D - 1 - d) * OPS>();
+    consume(d);
+    RingDrain<D, OPS, d + 1>::run(consume);
+  }
+};
+template <int D, int OPS>
+struct RingDrain<D, OPS, D> {
+  template <class F>
+  __device__ __forceinline__ static void run(F&) {}
+};
+
+template <int TG, int WAVES, int D, int EPI>
+__global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kAcc = TG * 4;
+  constexpr int kOps = 4 + 4 * TG;  // vector memory ops per stage (DMA + token loads)
+  static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
+  extern __shared__ __align__(16) unsigned char ring[];
+  __shared__ int32_t red[kAcc][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t rows = g.N - n0 < 16 ? g.N - n0 : 16;
+  const int steps = static_cast<int>((g.K + 255) / 256);
+  const int s_begin = steps * wave / WAVES, s_end = steps * (wave + 1) / WAVES;
+  unsigned char* my_ring = ring + wave * (D * kRingStage);
+
+  // weight DMA: instruction j of a stage fills LDS rows 4j .. 4j+3; lane l
+  // fills row 4j + l/16, chunk l%16 from global chunk (l%16) ^ row
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      scalar_ptr(const_cast<int8_t*>(g.W + n0 * g.K)), 0,
+      static_cast<int>(rows * g.K), kBufferFlags);
+  uint32_t w_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    w_off[j] = static_cast<uint32_t>(row * g.K + 16 * ((lane & 15) ^ row));
+  }
+  // token operand: lane (token r16 of group tg, 16-byte group grp).  The
+  // address is chosen by an integer select (no branch) and read through a
+  // global-address-space pointer.
+  typedef const v4i __attribute__((address_space(1)))* gv4i_ptr;
+  const uint64_t zero_addr = reinterpret_cast<uint64_t>(kZeroChunk);
+  uint64_t xrow[TG];
+  bool mok[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    const int64_t m = 16 * tg + r16;
+    mok[tg] = m < g.M;
+    xrow[tg] = reinterpret_cast<uint64_t>(g.A + (mok[tg] ? m : 0) * g.lda);
+  }
+  v4i xr[D][4][TG];  // token chunks of the stages in flight, per ring slot
+
+  auto issue = [&](int d, int st) {
+    unsigned char* slot = my_ring + d * kRingStage;
+    // a padding stage (st >= s_end) reads past the buffer range: zeros, no traffic
+    const int soff = st < s_end ? st * 256 : 0x7fff0000;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0, 0);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
+      const bool kin = k < g.K;
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        const uint64_t a = (mok[tg] & kin) ? xrow[tg] + static_cast<uint64_t>(k) : zero_addr;
+        xr[d][kb][tg] = *reinterpret_cast<gv4i_ptr>(a);
+      }
+    }
+  };
+  v4i acc[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) acc[tg] = v4i{0};
+  auto consume = [&](int d) {
+    const unsigned char* slot = my_ring + d * kRingStage;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const v4i w = *reinterpret_cast<const v4i*>(slot + r16 * 256 + 16 * ((4 * kb + grp) ^ r16));
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg)
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, xr[d][kb][tg], acc[tg], 0, 0, 0);
+    }
+  };
+
+  // The wave's stages, padded to a multiple of D with zero-weight stages,
+  // run branch-free: D stages in flight, refill after each consume; the last
+  // D stages drain with compile-time waits.
+  const int n_st = s_end - s_begin;
+  if (n_st > 0) {
+    const int n_pad = ((n_st + D - 1) / D) * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, s_begin + d);
+    for (int st0 = s_begin; st0 < s_begin + n_pad - D; st0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        wait_vmcnt<(D - 1) * kOps>();
+        consume(d);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): fragments read before the refill
+        issue(d, st0 + d + D);
+      }
+    }
+    // drain: stage d of the last group waits with D-1-d later stages in flight
+    RingDrain<D, kOps, 0>::run(consume);
+  }
+
+  __syncthreads();  // red[] zeroed by every thread before any wave adds into it
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) atomicAdd(&red[tg * 4 + v][lane], acc[tg][v]);
+  __syncthreads();
+  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) {
+    const int j = e >> 6, l = e & 63;
+    const int tg = j / 4, v = j & 3;
+    const int64_t n = n0 + 4 * (l >> 4) + v;
+    const int64_t m = 16 * tg + (l & 15);
+    if (n >= g.N || m >= g.M) continue;
+    const int32_t a = red[j][l];
+    if constexpr (EPI == kEpiBf16)
+      static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
+    else
+      static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
+  }
+#endif  // __HIP_DEVICE_COMPILE__
 }
 
 // ------------------------------------------------------------------------

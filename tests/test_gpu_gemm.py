@@ -212,12 +212,19 @@ def test_gemm_every_tile_config(M, K, N):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
-@pytest.mark.parametrize("M", [1, 5, 16, 17, 33, 64])
-def test_gemm_every_decode_config(M):
+NUM_DECODE_CFGS = 22  # kDecodeCfgs in csrc/gemm.hip
+
+
+@pytest.mark.parametrize(
+    "M,K,N",
+    [(1, 1344, 336), (5, 1344, 336), (16, 1344, 336), (17, 1344, 336), (33, 1344, 336), (64, 1344, 336),
+     (1, 1328, 200), (8, 1328, 200), (40, 1328, 200),  # K % 64 == 48: partial last step
+     (3, 4160, 72), (16, 4160, 72)],  # 65 steps: several pipelined batches per wave
+)
+def test_gemm_every_decode_config(M, K, N):
     from minisgl_amd.kernel.lib import load
 
-    announce(f"gemm all decode cfgs M={M}")
-    K, N = 1344, 336  # K not a multiple of 256, N not a multiple of 64
+    announce(f"gemm all decode cfgs M={M} K={K} N={N}")
     c = linear_case(M, K, N, seed=M)
     q, s = quant_per_token(c["x"].to(DEV))
     w, s_w = c["w"].to(DEV), c["s_w"].to(DEV)
@@ -226,7 +233,7 @@ def test_gemm_every_decode_config(M):
     y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
     lib = load()
     try:
-        for cfg in range(7):
+        for cfg in range(NUM_DECODE_CFGS):
             lib.mw8_set_tuning(cfg, -1, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
