@@ -349,6 +349,28 @@ void launch_grouped3(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   launch_tile3<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRows>(g, grid, st);
 }
 
+// Run tiles: one block per alignment block; a tile spans up to BM / bm
+// consecutive alignment blocks of one expert (SortedRunRows).
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI>
+void launch_grouped_runs(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.N + BN - 1) / BN), blocks);
+  launch_tile3<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows>(g, grid, st);
+}
+
+// Grouped configurations (mw8_set_tuning moe_cfg): 0-6 one tile per
+// alignment block (tile height = block size), 7 and 8 run tiles of 256 and
+// 128 rows on the 8-wave 256-wide ring (K % 128 == 0).  Automatic choice:
+// cfg 0.  Measured on MI355X at config 3 (E 128, top-8, H 2048, I 768) the
+// run tiles lose at 256, 1024 and 4096 tokens (226 / 308 / 614 us per layer
+// against 169 / 238 / 548 us): three of every four run-tile blocks only
+// read the routing metadata and exit, each holding the CU's LDS through a
+// chain of dependent loads of arrays the alignment kernel has just written.
+int default_moe_cfg(const GemmArgs& g, int bm) {
+  (void)g;
+  (void)bm;
+  return 0;
+}
+
 template <int EPI>
 void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st) {
   int cfg = g_moe_cfg.load(std::memory_order_relaxed);
@@ -359,7 +381,16 @@ void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t 
     return;
   }
   const bool bk128 = g.K % 128 == 0;
-  if (cfg < 0 || (!bk128 && cfg >= 3)) cfg = 0;
+  if (cfg < 0) cfg = default_moe_cfg(g, bm);
+  if (!bk128 && cfg >= 3) cfg = 0;
+  if (cfg == 7 || (cfg == 8 && bm == 128)) {  // 256-row run tiles (bm 64 or 128)
+    launch_grouped_runs<256, 256, 128, 4, 2, 2, EPI>(g, blocks, st);
+    return;
+  }
+  if (cfg == 8) {  // 128-row run tiles over 64-row blocks
+    launch_grouped_runs<128, 256, 128, 2, 4, 2, EPI>(g, blocks, st);
+    return;
+  }
   if (bm == 64) {
     switch (cfg) {
       case 1: launch_grouped3<64, 128, 64, 2, 2, 2, EPI>(g, blocks, st); break;

@@ -65,6 +65,10 @@ struct GemmArgs {
   // bf16 output rows are 16-byte aligned with N % 8 == 0: the tile core may
   // assemble its output tile in LDS and store it with 16-byte row writes
   int32_t staged_out;
+  // grouped GEMM over expert runs (SortedRunRows): rows of the alignment
+  // blocks behind expert_ids / num_post_pad (the tile height BM is a
+  // multiple of it)
+  int32_t align_bsz;
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -80,9 +84,21 @@ __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, co
 // ------------------------------------------------------------------------
 struct DenseRows {
   static constexpr bool kGrouped = false;
+  static constexpr bool kRuns = false;
 };
+// One tile per alignment block (BM == alignment block size).
 struct SortedRows {
   static constexpr bool kGrouped = true;
+  static constexpr bool kRuns = false;
+};
+// One tile per run of up to BM / align_bsz consecutive alignment blocks of
+// one expert: the tile covers sorted rows [m0, m0 + rows_valid) and rows
+// past the run are neither loaded, multiplied nor stored.  The grid has one
+// block per alignment block; a block whose alignment block is not at a
+// multiple of BM / align_bsz from the start of its expert's segment exits.
+struct SortedRunRows {
+  static constexpr bool kGrouped = true;
+  static constexpr bool kRuns = true;
 };
 
 // ------------------------------------------------------------------------
@@ -409,11 +425,46 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   int64_t m0, n0;
   int64_t split_unit = -1;  // split-tail unit (writes an int32 partial tile), -1: whole tile
   int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
-  if constexpr (Rows::kGrouped) {
-    n0 = static_cast<int64_t>(blockIdx.x) * BN;
-    m0 = static_cast<int64_t>(blockIdx.y) * BM;
+  int rows_valid = BM;      // tile rows that hold sorted positions of this tile's run
+  // grouped grids: x = N tile, y = alignment block (an XCD-contiguous walk
+  // of the (block, N tile) pairs measured slower at 256 and 1024 tokens)
+  const int64_t gx = blockIdx.x, gy = blockIdx.y;
+  if constexpr (Rows::kRuns) {
+    n0 = gx * BN;
+    const int ab = g.align_bsz;
+    const int64_t y = gy;
+    const int64_t npp = *g.num_post_pad;
+    if (y * ab >= npp) return;
+    const int e = g.expert_ids[y];
+    if (e < 0 || e >= g.num_experts) return;
+    // distance j from the first alignment block of expert e: expert_ids is
+    // non-decreasing over the used blocks, so scan back 64 blocks per step
+    // for the nearest block of another expert (index < 0 counts as one)
+    int64_t first = 0;
+    for (int64_t base = y;; base -= 64) {
+      const int64_t idx = base - lane;
+      const int v = idx >= 0 ? g.expert_ids[idx] : -2;
+      const uint64_t other = __ballot(v != e);
+      if (other != 0) {
+        first = base - (__ffsll(static_cast<unsigned long long>(other)) - 1) + 1;
+        break;
+      }
+    }
+    const int per_tile = BM / ab;
+    if ((y - first) % per_tile != 0) return;
+    const int64_t used = npp / ab;
+    const int64_t nxt = y + lane;
+    const int same = (lane < per_tile && nxt < used) ? (g.expert_ids[nxt] == e) : 0;
+    const uint64_t run = __ballot(same != 0);
+    rows_valid = ab * __popcll(run);  // the run's blocks are contiguous from y
+    m0 = y * ab;
+    W += static_cast<int64_t>(e) * g.N * g.K;
+    sw += static_cast<int64_t>(e) * g.N;
+  } else if constexpr (Rows::kGrouped) {
+    n0 = gx * BN;
+    m0 = gy * BM;
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
-    const int e = g.expert_ids[blockIdx.y];
+    const int e = g.expert_ids[gy];
     if (e < 0 || e >= g.num_experts) return;
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
@@ -454,13 +505,15 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
     const int c = (unit % kChunks) ^ swz_f<BK>(row);
     int64_t arow;
+    bool a_live = true;  // false: the DMA reads past the buffer range (zeros, no traffic)
     if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + row];
-      arow = p < g.num_valid ? p / g.top_k : 0;
+      const int32_t p = row < rows_valid ? g.sorted_ids[m0 + row] : static_cast<int32_t>(g.num_valid);
+      a_live = p < g.num_valid;
+      arow = a_live ? p / g.top_k : 0;
     } else {
       arow = m0 + row < g.M ? m0 + row : g.M - 1;
     }
-    a_doff[j] = static_cast<uint32_t>((arow - a_base_row) * g.lda + 16 * c);
+    a_doff[j] = a_live ? static_cast<uint32_t>((arow - a_base_row) * g.lda + 16 * c) : 0x80000000u;
   }
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
@@ -506,7 +559,10 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < kFN; ++j) acc[i][j] = v16i{0};
+  // a wave whose rows all lie past an expert run has no MFMA work
+  const bool wave_live = !Rows::kRuns || wm * kWaveM < rows_valid;
   auto mfmas = [&](int set) {
+    if (!wave_live) return;
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
@@ -589,7 +645,8 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
           const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
           float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
           if constexpr (Rows::kGrouped) {
-            const int32_t p0 = g.sorted_ids[m0 + r0], p1 = g.sorted_ids[m0 + r0 + 1];
+            const int32_t p0 = r0 < rows_valid ? g.sorted_ids[m0 + r0] : static_cast<int32_t>(g.num_valid);
+            const int32_t p1 = r0 + 1 < rows_valid ? g.sorted_ids[m0 + r0 + 1] : static_cast<int32_t>(g.num_valid);
             sa0 = p0 < g.num_valid ? g.sa[p0 / g.top_k] : 0.0f;
             sa1 = p1 < g.num_valid ? g.sa[p1 / g.top_k] : 0.0f;
             if (g.topk_w) {
@@ -637,7 +694,7 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
         const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
         int64_t orow;
         if constexpr (Rows::kGrouped) {
-          const int32_t p = g.sorted_ids[m0 + r];
+          const int32_t p = r < rows_valid ? g.sorted_ids[m0 + r] : static_cast<int32_t>(g.num_valid);
           orow = p < g.num_valid ? p : -1;
         } else {
           orow = m0 + r < g.M ? m0 + r : -1;
@@ -662,7 +719,7 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
       bool rvalid;
       float routed = 1.0f;
       if constexpr (Rows::kGrouped) {
-        const int32_t p = g.sorted_ids[m0 + r];
+        const int32_t p = r < rows_valid ? g.sorted_ids[m0 + r] : static_cast<int32_t>(g.num_valid);
         rvalid = p < g.num_valid;
         orow = p;
         arow = rvalid ? p / g.top_k : 0;

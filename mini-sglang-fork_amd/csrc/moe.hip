@@ -11,9 +11,40 @@ void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStrea
 namespace {
 
 // ------------------------------------------------------------------ top-k
+// Full-wave reductions without LDS: DPP quad permutes and row mirrors
+// combine within each 16-lane row, then the gfx950 permlane16/32 swaps
+// combine rows; every lane ends with the result.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x, Op op) {
+  x = op(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false)));  // quad [1,0,3,2]
+  x = op(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, false)));  // quad [2,3,0,1]
+  x = op(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xF, 0xF, false)));  // row half mirror
+  x = op(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xF, 0xF, false)));  // row mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = op(r16[0], r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return op(r32[0], r32[1]);
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __builtin_bit_cast(float, wave_reduce_u32(__builtin_bit_cast(uint32_t, v), [](uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+  }));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __builtin_bit_cast(float, wave_reduce_u32(__builtin_bit_cast(uint32_t, v), [](uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b));
+  }));
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  return static_cast<int>(wave_reduce_u32(static_cast<uint32_t>(v), [](uint32_t a, uint32_t b) {
+    return static_cast<int>(a) < static_cast<int>(b) ? a : b;
+  }));
+}
+
 // One wave per token.  Softmax in fp32 over E logits (bf16 or fp32 input),
 // then k rounds of a wave arg-max (larger value wins, lower expert index
-// wins ties), then the two renormalisations of the reference
+// wins ties: a max over values, then a min over the indices holding it),
+// then the two renormalisations of the reference
 // (python/minisgl/moe/fused.py:22-24).
 template <int VPL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, int is_bf16,
@@ -37,16 +68,14 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, i
   float mx = v[0];
 #pragma unroll
   for (int j = 1; j < VPL; ++j) mx = fmaxf(mx, v[j]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max_f32(mx);
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     v[j] = (lane + 64 * j < E) ? expf(v[j] - mx) : 0.0f;
     sum += v[j];
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  sum = wave_sum_f32(sum);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) v[j] = (lane + 64 * j < E) ? v[j] / sum : -1.0f;
 
@@ -58,23 +87,17 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, i
 #pragma unroll
     for (int j = 1; j < VPL; ++j)
       if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == i) { w_sel = bv; id_sel = bi; }
+    const float best = wave_max_f32(bv);
+    const int sel = wave_min_i32(bv == best ? bi : 0x7fffffff);
+    if (lane == i) { w_sel = best; id_sel = sel; }
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
-      if (lane + 64 * j == bi) v[j] = -1.0f;
+      if (lane + 64 * j == sel) v[j] = -1.0f;
   }
   if (renorm) {
-    float s1 = 0.0f;
-    for (int i = 0; i < topk; ++i) s1 += __shfl(w_sel, i, 64);
+    const float s1 = wave_sum_f32(lane < topk ? w_sel : 0.0f);
     w_sel = w_sel / s1;
-    float s2 = 0.0f;
-    for (int i = 0; i < topk; ++i) s2 += __shfl(w_sel, i, 64);
+    const float s2 = wave_sum_f32(lane < topk ? w_sel : 0.0f);
     w_sel = w_sel / (s2 + 1e-8f);
   }
   if (lane < topk) {
@@ -332,6 +355,7 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
+  g.align_bsz = bsz;
   if (bsz == 16) {
     const int64_t ldl = ((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
     MW8_REQUIRE(16 * ldl <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",

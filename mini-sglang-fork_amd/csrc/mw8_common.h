@@ -53,25 +53,40 @@ MW8_HD RowScale row_scale(float amax) {
   return rs;
 }
 
+// Clamp of an integral fp32 value to [-127, 127] (finite inputs): one
+// v_med3_f32 on the device.
+MW8_HD float clamp127(float t) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+#else
+  t = t < -127.0f ? -127.0f : t;
+  return t > 127.0f ? 127.0f : t;
+#endif
+}
+
 // rint(x / s) with x / s the correctly rounded fp32 quotient, clamped to
 // [-127, 127].  Fast path: q0 = RN(x * r) is within one ulp of x / s when r
 // is the correctly rounded reciprocal; e = x - q0 * s is exact (FMA) and
 // RN(q0 + e * r) is then the correctly rounded quotient (Markstein, "IA-64
 // and Elementary Functions", Theorem 8.10).  Exhaustively checked against
-// IEEE division for every bf16 input on the CPU (tests/test_quant_math.py).
-MW8_HD float quant_div_rne(float x, const RowScale& rs) {
+// IEEE division for every bf16 input on the CPU (tests/native).
+// The FAST flag is per row: kernels branch once per row on rs.fast and
+// instantiate both variants, so no element pays for the division path.
+template <bool FAST>
+MW8_HD float quant_div_rne_t(float x, const RowScale& rs) {
   float t;
-  if (rs.fast) {
+  if (FAST) {
     float q0 = x * rs.r;
     float e = __builtin_fmaf(-q0, rs.s, x);
     t = __builtin_fmaf(e, rs.r, q0);
   } else {
     t = rs.s > 0.0f ? x / rs.s : 0.0f;
   }
-  t = __builtin_rintf(t);
-  t = t < -127.0f ? -127.0f : t;
-  t = t > 127.0f ? 127.0f : t;
-  return t;
+  return clamp127(__builtin_rintf(t));
+}
+
+MW8_HD float quant_div_rne(float x, const RowScale& rs) {
+  return rs.fast ? quant_div_rne_t<true>(x, rs) : quant_div_rne_t<false>(x, rs);
 }
 
 // ---------------------------------------------------------------- epilogue

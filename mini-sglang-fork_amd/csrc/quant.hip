@@ -66,19 +66,28 @@ __device__ __forceinline__ uint32_t absmax8(const U16x8& v, uint32_t m) {
   return m;
 }
 
+// bf16 element 2j / 2j+1 of a packed word as fp32 (one shift or one mask)
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+
+// Four integral fp32 values in [-127, 127] -> four int8 bytes of a word.
+__device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d) {
+  const uint32_t lo = (static_cast<uint32_t>(static_cast<int>(a)) & 0xFFu) |
+                      ((static_cast<uint32_t>(static_cast<int>(b)) & 0xFFu) << 8);
+  const uint32_t hi = (static_cast<uint32_t>(static_cast<int>(c)) & 0xFFu) |
+                      ((static_cast<uint32_t>(static_cast<int>(d)) & 0xFFu) << 8);
+  return lo | (hi << 16);
+}
+
+template <bool FAST>
 __device__ __forceinline__ uint2 quant8(const U16x8& v, const RowScale& rs) {
-  uint32_t lo = 0, hi = 0;
+  float f[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    int q = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(v.get(j))), rs));
-    lo |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * j);
+    f[2 * j] = quant_div_rne_t<FAST>(bf16_lo(v.w[j]), rs);
+    f[2 * j + 1] = quant_div_rne_t<FAST>(bf16_hi(v.w[j]), rs);
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int q = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(v.get(4 + j))), rs));
-    hi |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * j);
-  }
-  return make_uint2(lo, hi);
+  return make_uint2(pack4_i8(f[0], f[1], f[2], f[3]), pack4_i8(f[4], f[5], f[6], f[7]));
 }
 
 // ------------------------------------------------------------ quantizer
@@ -108,10 +117,18 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(
   if (!live) return;
   const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
   uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+  if (rs.fast) {  // row-uniform: one branch per row, not a select per element
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
-    if (idx < nvec) qr[idx] = quant8(v[i], rs);
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) qr[idx] = quant8<true>(v[i], rs);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) qr[idx] = quant8<false>(v[i], rs);
+    }
   }
   if (t == 0) s[row] = rs.s;
 }
@@ -136,14 +153,18 @@ __global__ __launch_bounds__(kBlock) void quant_rows_generic_kernel(
 }
 
 // --------------------------------------------------- activation + requant
-__device__ __forceinline__ float act_fn(float g, int act) {
-  if (act == 0) return g / (1.0f + __expf(-g));  // silu
-  return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f));  // gelu (erf)
+// silu(g) = g * 1 / (1 + e^-g) with the hardware reciprocal (1 ulp) in place
+// of an IEEE division: the activation is rounded to bf16 next and is held
+// to a tolerance, while the requant that follows is exact on its bf16 value.
+template <int ACT>
+__device__ __forceinline__ float act_fn(float g) {
+  if constexpr (ACT == 0) return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));  // silu
+  else return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f));  // gelu (erf)
 }
 
-template <int TPR, int VPT>
+template <int TPR, int VPT, int ACT>
 __global__ __launch_bounds__(kBlock) void act_rows_kernel(
-    const uint16_t* __restrict__ x, int64_t R, int64_t d, int act,
+    const uint16_t* __restrict__ x, int64_t R, int64_t d,
     int8_t* __restrict__ q, float* __restrict__ s, uint16_t* __restrict__ a_out) {
   __shared__ uint32_t red[kBlock / 64];
   constexpr int kRowsPerBlock = kBlock / TPR;
@@ -164,9 +185,9 @@ __global__ __launch_bounds__(kBlock) void act_rows_kernel(
       const U16x8 u = ur[idx];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float a0 = act_fn(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j))), act) *
+        const float a0 = act_fn<ACT>(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j)))) *
                          bf16_to_f32(static_cast<uint16_t>(u.get(2 * j)));
-        const float a1 = act_fn(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j + 1))), act) *
+        const float a1 = act_fn<ACT>(bf16_to_f32(static_cast<uint16_t>(g.get(2 * j + 1)))) *
                          bf16_to_f32(static_cast<uint16_t>(u.get(2 * j + 1)));
         v[i].w[j] = static_cast<uint32_t>(f32_to_bf16(a0)) |
                     (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
@@ -179,12 +200,24 @@ __global__ __launch_bounds__(kBlock) void act_rows_kernel(
   const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
   uint2* qr = reinterpret_cast<uint2*>(q + row * d);
   U16x8* ar = a_out ? reinterpret_cast<U16x8*>(a_out + row * d) : nullptr;
+  if (rs.fast) {
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
-    if (idx < nvec) {
-      qr[idx] = quant8(v[i], rs);
-      if (ar) ar[idx] = v[i];
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) qr[idx] = quant8<true>(v[i], rs);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) qr[idx] = quant8<false>(v[i], rs);
+    }
+  }
+  if (ar) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) ar[idx] = v[i];
     }
   }
   if (t == 0) s[row] = rs.s;
@@ -226,8 +259,12 @@ template <int TPR, int VPT>
 struct ActLaunch {
   static void run(dim3 grid, hipStream_t st, const uint16_t* x, int64_t R, int64_t d, int act,
                   int8_t* q, float* s, uint16_t* a_out) {
-    hipLaunchKernelGGL((act_rows_kernel<TPR, VPT>), grid, dim3(kBlock), 0, st, x, R, d, act, q,
-                       s, a_out);
+    if (act == 0)
+      hipLaunchKernelGGL((act_rows_kernel<TPR, VPT, 0>), grid, dim3(kBlock), 0, st, x, R, d, q, s,
+                         a_out);
+    else
+      hipLaunchKernelGGL((act_rows_kernel<TPR, VPT, 1>), grid, dim3(kBlock), 0, st, x, R, d, q, s,
+                         a_out);
   }
 };
 

@@ -133,6 +133,9 @@ def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
     return logits, W, SW, act
 
 
+NUM_MOE_CFGS = 9  # grouped configurations in csrc/gemm.hip (7, 8: run tiles)
+
+
 @pytest.mark.parametrize("shape", ["cfg3", "ragged"])
 def test_grouped_every_tile_config(shape):
     """Each grouped tile configuration (forced through mw8_set_tuning) for
@@ -175,7 +178,7 @@ def test_grouped_every_tile_config(shape):
             )
             for B in (64, 128):
                 sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, E)
-                for cfg in range(-1, 7):
+                for cfg in range(-1, NUM_MOE_CFGS):
                     announce(f"grouped {shape} gemm{which} B={B} cfg={cfg}")
                     lib.mw8_set_tuning(-1, -1, cfg)
                     out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
@@ -185,6 +188,59 @@ def test_grouped_every_tile_config(shape):
                     torch.cuda.synchronize()
                     np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref)
                     assert bf16_bits_equal(out, y_ref).all()
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+
+
+@pytest.mark.parametrize("B", [64, 128])
+def test_grouped_run_tiles(B):
+    """Run tiles (one tile over up to 256 / B consecutive alignment blocks
+    of one expert) on skewed routing: one expert owns 68+ blocks (the
+    backward scan for its first block crosses 64 blocks and its runs split
+    into several tiles), others own 1-3 blocks (short runs), some none;
+    N and the pair count are not tile multiples.  Bit-exact int32 and bf16
+    for every grouped configuration, gate_up-style (A row = pair // top_k)
+    and down-style (top_k 1, routed weight)."""
+    from minisgl_amd.kernel import lib as mw8lib
+
+    announce(f"grouped run tiles B={B}")
+    lib = mw8lib.load()
+    gen = torch.Generator().manual_seed(1234)
+    M, k, E, N, K = 4500, 2, 6, 320, 512
+    ids = torch.full((M, k), 2, dtype=torch.int32)  # expert 2: 4435 pairs (70 blocks of 64)
+    ids[:65, 0] = 0          # expert 0: 65 + 70 pairs
+    ids[:65, 1] = 4          # expert 4: 65 pairs (2 blocks of 64)
+    ids[65:230, 1] = 5       # expert 5: 165 pairs
+    ids[230:300, 1] = 0
+    ids[300:, 1] = 3         # expert 3: 4200 pairs; expert 1: none
+    perm = torch.randperm(M * k, generator=gen)
+    ids = ids.view(-1)[perm].view(M, k).contiguous()
+    tw = torch.rand(M, k, generator=gen)
+    W = torch.randint(-127, 128, (E, N, K), generator=gen, dtype=torch.int8)
+    SW = torch.rand(E, N, generator=gen) * 1e-2 + 1e-4
+    ids_ref = ids.numpy()
+    idsd, twd, Wd, SWd = ids.to(DEV), tw.to(DEV), W.to(DEV), SW.to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(idsd, B, E)
+    try:
+        for which in (1, 2):
+            rows = M if which == 1 else M * k
+            act = torch.randn(rows, K, generator=gen).to(torch.bfloat16)
+            q, s = quant_per_token(act.to(DEV))
+            top_k, routed = (k, None) if which == 1 else (1, tw.numpy())
+            y_ref, acc_ref = orc.grouped_gemm_w8a8(
+                q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
+                routed=routed, return_acc=True,
+            )
+            for cfg in (-1, 0, 7, 8):
+                announce(f"run tiles B={B} gemm{which} cfg={cfg}")
+                lib.mw8_set_tuning(-1, -1, cfg)
+                out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
+                fused_moe_kernel_w8a8(q, s, Wd, SWd, out, twd, sorted_ids, expert_ids, npp,
+                                      routed is not None, top_k, B, M * k)
+                acc = fused_moe_kernel_w8a8_i32(q, Wd, sorted_ids, expert_ids, npp, top_k, B, M * k)
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
+                assert bf16_bits_equal(out, y_ref).all(), f"cfg {cfg}"
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
 
