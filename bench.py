@@ -66,6 +66,60 @@ def device_peaks(lib):
             "hbm_peak_gbps": HBM_PEAK_GBPS}
 
 
+def device_ceilings(lib, dev):
+    """Live device ceilings from the library's measurement kernels, timed
+    with HIP events on the launch stream: the int8 MFMA rate with constant
+    operands (nominal clock) and with random operands (the power-limited
+    clock real int8 data runs at), and the streaming-read rate over 1 GiB
+    (past the 256 MB MALL)."""
+    import torch
+
+    from minisgl_amd.kernel.lib import check
+
+    n = int(lib.mw8_calib_sink_len())
+    sink = torch.empty(n, dtype=torch.int32, device=dev)
+    st = torch.cuda.Stream()
+    iters, reps = 4000, 10
+    ops = 256 * 1024 / 64 * iters * 32 * 65536.0
+    res = {}
+
+    def timed(launch, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            launch()
+        e0.record(st)
+        for _ in range(reps):
+            launch()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    with torch.cuda.stream(st):
+        for rnd, key in ((0, "mfma_i8_const_tops"), (1, "mfma_i8_random_tops")):
+            t = timed(lambda: check(lib.mw8_calib_mfma_i8(rnd, iters, sink.data_ptr(), n, st.cuda_stream)), reps)
+            res[key] = round(ops / t / 1e12, 1)
+        nbytes = 1 << 30
+        buf = torch.empty(3 << 29, dtype=torch.uint8, device=dev)
+        t = timed(lambda: check(lib.mw8_calib_read(buf.data_ptr(), nbytes, sink.data_ptr(), n, st.cuda_stream)), reps)
+        res["stream_read_gbps"] = round(nbytes / t / 1e9, 1)
+        # at the decode weight sizes (o_proj, qkv, down, gate_up of the sweep),
+        # back-to-back launches over 8 distinct slices (> the 256 MB MALL)
+        res["stream_read_gbps_at_mb"] = {}
+        for size in (5120 * 5120, 7168 * 5120, 5120 * 17408, 34816 * 5120):
+            slot = [0]
+
+            def launch(size=size):
+                off = (slot[0] % 8) * size
+                slot[0] += 1
+                check(lib.mw8_calib_read(buf.data_ptr() + off, size, sink.data_ptr(), n, st.cuda_stream))
+
+            t = timed(launch, 24)
+            res["stream_read_gbps_at_mb"][f"{size / 1e6:.1f}"] = round(size / t / 1e9, 1)
+        del buf
+    torch.cuda.synchronize()
+    return res
+
+
 def roofline_frac(ops: float, nbytes: float, t_s: float, peak_tops: float) -> float:
     attainable = min(peak_tops * 1e12, HBM_PEAK_GBPS * 1e9 * ops / nbytes)
     return (ops / t_s) / attainable
@@ -154,6 +208,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     peaks = device_peaks(lib)
     peak_tops = peaks["int8_peak_tops"]
+    peaks["measured"] = device_ceilings(lib, dev)
     log(f"device: {peaks}")
 
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -237,6 +292,10 @@ def main() -> int:
         "peak": round(peak_tops, 1) if dom["bound"] == "mfma" else HBM_PEAK_GBPS,
         "unit": "TOPS" if dom["bound"] == "mfma" else "GB/s",
         "frac": dom["roofline_frac"],
+        "frac_of_measured_ceiling": round(
+            dom_ops / dom_t / 1e12 / peaks["measured"]["mfma_i8_random_tops"], 4)
+        if dom["bound"] == "mfma" else round(
+            gemm_bytes(dom["M"], dom["N"], dom["K"]) / dom_t / 1e9 / peaks["measured"]["stream_read_gbps"], 4),
         "traffic": measured_traffic(dom),
         "kernel": f"{dom['kernel']} ({dom['shape']} M={dom['M']} K={dom['K']} N={dom['N']})",
         "per_launch": (f"{dom_ops / 1e9:.1f} GOP = 2*M*N*K and "

@@ -41,6 +41,9 @@ int moe_sum_reduce_bf16(const void*, int64_t, int, int64_t, void*, hipStream_t);
 int moe_gemm_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
                   const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                   int64_t, int, int, void*, int, hipStream_t);
+int64_t calib_sink_len();
+int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
+int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
 
 }  // namespace mw8
 
@@ -136,6 +139,17 @@ int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorte
 int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, void* out,
                             mw8_stream_t st) {
   MW8_ENTRY(mw8::moe_sum_reduce_bf16(in, M, k, H, out, S(st)));
+}
+
+int64_t mw8_calib_sink_len(void) { return mw8::calib_sink_len(); }
+
+int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int64_t sink_len,
+                      mw8_stream_t st) {
+  MW8_ENTRY(mw8::calib_mfma_i8(random_operands, iters, sink, sink_len, S(st)));
+}
+
+int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, mw8_stream_t st) {
+  MW8_ENTRY(mw8::calib_read(buf, bytes, sink, sink_len, S(st)));
 }
 
 }  // extern "C"
