@@ -424,6 +424,20 @@ def run_secondary(dev, peak_tops):
     log(f"quant cfg2: {res['quant_cfg2']}")
     del x, q, s
 
+    # fused RMSNorm + residual add + requant (the input of qkv / gate_up) at
+    # the config-4 row count: reads x and residual, writes residual, q, s
+    from minisgl_amd.kernel import rmsnorm_quant
+    Mn, Hn = 2080, 5120
+    xn = torch.randn(Mn, Hn, generator=gen, device=dev).to(torch.bfloat16)
+    rn = torch.randn(Mn, Hn, generator=gen, device=dev).to(torch.bfloat16)
+    wn = torch.rand(Hn, generator=gen, device=dev).to(torch.bfloat16)
+    t = perf_hip(lambda: rmsnorm_quant(xn, wn, 1e-6, residual=rn)) * 1e-3
+    nb = 7 * Mn * Hn + 4 * Mn + 2 * Hn
+    res["rmsnorm_quant_2080x5120"] = {"us": round(t * 1e6, 2), "gbps": round(nb / t / 1e9, 1),
+                                      "roofline_frac": round(nb / t / 1e9 / HBM_PEAK_GBPS, 4)}
+    log(f"rmsnorm+quant: {res['rmsnorm_quant_2080x5120']}")
+    del xn, rn, wn
+
     # config 3: MoE layer tokens/s
     res["moe_cfg3"] = {}
     for Mt in (16, 256, 4096):

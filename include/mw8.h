@@ -76,6 +76,24 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
                                float* s, void* act_out, mw8_stream_t stream);
 
 /*
+ * Fused RMSNorm + per-token requant: x bf16 [M, H], weight bf16 [H].
+ *   h = x, or h = bf16(x + residual) written back to residual (in place)
+ *   ss = sum_k h_k^2 accumulated in fp64 (each square exact),
+ *   r  = 1 / sqrt(fp32(ss / H) + eps)      (IEEE fp32),
+ *   y  = bf16((h * r) * weight)            (each product rounded)
+ * then y is quantized like mw8_quant_per_token_bf16 into q int8 [M, H] and
+ * s fp32 [M]; y (bf16 [M, H], may alias x) is written only if non-NULL.
+ * q and s may both be NULL (plain RMSNorm; y required).  H % 8 == 0,
+ * H <= 32768.
+ * Replaces flashinfer rmsnorm / fused_add_rmsnorm (RMSNorm / RMSNormFused,
+ * python/minisgl/layers/norm.py:8-38, called at
+ * python/minisgl/models/qwen3.py:37-40) together with the input quantizer
+ * of the W8A8 linear that follows them.
+ */
+int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, float eps, int64_t M,
+                           int64_t H, int8_t* q, float* s, void* y, mw8_stream_t stream);
+
+/*
  * Tile-configuration override, process-wide: decode_cfg indexes the dense
  * small-M (M <= 64) configurations, tile_cfg the dense large-M ones, moe_cfg
  * the grouped (fused-MoE) tile configurations for block sizes 64 and 128;

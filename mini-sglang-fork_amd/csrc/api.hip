@@ -41,6 +41,8 @@ int moe_sum_reduce_bf16(const void*, int64_t, int, int64_t, void*, hipStream_t);
 int moe_gemm_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
                   const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                   int64_t, int, int, void*, int, hipStream_t);
+int rmsnorm_quant_bf16(const void*, void*, const void*, float, int64_t, int64_t, int8_t*, float*, void*,
+                       hipStream_t);
 int64_t calib_sink_len();
 int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
 int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
@@ -139,6 +141,11 @@ int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorte
 int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, void* out,
                             mw8_stream_t st) {
   MW8_ENTRY(mw8::moe_sum_reduce_bf16(in, M, k, H, out, S(st)));
+}
+
+int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, float eps, int64_t M,
+                           int64_t H, int8_t* q, float* s, void* y, mw8_stream_t st) {
+  MW8_ENTRY(mw8::rmsnorm_quant_bf16(x, residual, weight, eps, M, H, q, s, y, S(st)));
 }
 
 int64_t mw8_calib_sink_len(void) { return mw8::calib_sink_len(); }

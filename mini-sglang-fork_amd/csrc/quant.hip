@@ -223,6 +223,127 @@ __global__ __launch_bounds__(kBlock) void act_rows_kernel(
   if (t == 0) s[row] = rs.s;
 }
 
+// ------------------------------------------------- RMSNorm + requant
+// h = x (or bf16(x + residual), written back to residual), then
+//   ss = sum_k h_k^2 in fp64 (every square of a bf16 value is exact),
+//   r  = 1 / sqrt(fp32(ss / H) + eps)         (IEEE fp32 sqrt and division)
+//   y  = bf16((h * r) * w)                    (each product rounded)
+// and y is quantized per row exactly like quant_rows_kernel.  y is written
+// only if y_out is given.  Replaces flashinfer rmsnorm / fused_add_rmsnorm
+// (python/minisgl/layers/norm.py:8-38) followed by the quantizer of the
+// next W8A8 linear.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int TPR>
+__device__ __forceinline__ double row_sum_f64(double v, double* red) {
+  v = wave_sum_f64(v);
+  if constexpr (TPR == 64) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    double t = red[0];
+#pragma unroll
+    for (int w = 1; w < TPR / 64; ++w) t += red[w];
+    return t;
+  }
+}
+
+template <int TPR, int VPT, bool RES, bool QUANT>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ res, const uint16_t* __restrict__ w,
+    float eps, int64_t M, int64_t H, int8_t* __restrict__ q, float* __restrict__ s,
+    uint16_t* __restrict__ y_out) {
+  __shared__ double dred[kBlock / 64];
+  __shared__ uint32_t red[kBlock / 64];
+  constexpr int kRowsPerBlock = kBlock / TPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  const bool live = row < M;  // uniform per wave (TPR >= 64)
+  const int64_t nvec = H >> 3;
+  const U16x8* xr = reinterpret_cast<const U16x8*>(x + (live ? row : 0) * H);
+  U16x8* rr = RES ? reinterpret_cast<U16x8*>(res + (live ? row : 0) * H) : nullptr;
+  const U16x8* wr = reinterpret_cast<const U16x8*>(w);
+
+  U16x8 v[VPT];
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (live && idx < nvec) {
+      v[i] = xr[idx];
+      if constexpr (RES) {
+        const U16x8 r0 = rr[idx];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = bf16_lo(v[i].w[j]) + bf16_lo(r0.w[j]);
+          const float a1 = bf16_hi(v[i].w[j]) + bf16_hi(r0.w[j]);
+          v[i].w[j] = static_cast<uint32_t>(f32_to_bf16(a0)) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
+        }
+        rr[idx] = v[i];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const double lo = static_cast<double>(bf16_lo(v[i].w[j]));
+        const double hi = static_cast<double>(bf16_hi(v[i].w[j]));
+        ss = __builtin_fma(lo, lo, ss);
+        ss = __builtin_fma(hi, hi, ss);
+      }
+    }
+  }
+  ss = row_sum_f64<TPR>(ss, dred);
+  const float ms = static_cast<float>(ss / static_cast<double>(H));
+  const float r = 1.0f / __builtin_sqrtf(ms + eps);
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+    if (live && idx < nvec) {
+      const U16x8 wv = wr[idx];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float y0 = (bf16_lo(v[i].w[j]) * r) * bf16_lo(wv.w[j]);
+        const float y1 = (bf16_hi(v[i].w[j]) * r) * bf16_hi(wv.w[j]);
+        v[i].w[j] = static_cast<uint32_t>(f32_to_bf16(y0)) | (static_cast<uint32_t>(f32_to_bf16(y1)) << 16);
+      }
+      if constexpr (QUANT) m = absmax8(v[i], m);
+    }
+  }
+  if constexpr (QUANT) m = row_max<TPR>(m, red);
+  if (!live) return;
+  if constexpr (QUANT) {
+    const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
+    uint2* qr = reinterpret_cast<uint2*>(q + row * H);
+    if (rs.fast) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+        if (idx < nvec) qr[idx] = quant8<true>(v[i], rs);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+        if (idx < nvec) qr[idx] = quant8<false>(v[i], rs);
+      }
+    }
+    if (t == 0) s[row] = rs.s;
+  }
+  if (y_out) {
+    U16x8* yr = reinterpret_cast<U16x8*>(y_out + row * H);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) yr[idx] = v[i];
+    }
+  }
+}
+
 // Pick (TPR, VPT) for a row of nvec 16-byte vectors; false if none fits.
 template <template <int, int> class Launch, typename... Args>
 bool dispatch_rows(int64_t nvec, int64_t rows, hipStream_t st, Args... args) {
@@ -268,6 +389,25 @@ struct ActLaunch {
   }
 };
 
+template <int TPR, int VPT>
+struct NormLaunch {
+  static void run(dim3 grid, hipStream_t st, const uint16_t* x, uint16_t* res, const uint16_t* w,
+                  float eps, int64_t M, int64_t H, int8_t* q, float* s, uint16_t* y) {
+    if (res && q)
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, true, true>), grid, dim3(kBlock), 0, st, x, res,
+                         w, eps, M, H, q, s, y);
+    else if (res)
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, true, false>), grid, dim3(kBlock), 0, st, x, res,
+                         w, eps, M, H, q, s, y);
+    else if (q)
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, false, true>), grid, dim3(kBlock), 0, st, x, res,
+                         w, eps, M, H, q, s, y);
+    else
+      hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, false, false>), grid, dim3(kBlock), 0, st, x, res,
+                         w, eps, M, H, q, s, y);
+  }
+};
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
@@ -307,6 +447,28 @@ int act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int act, int
   MW8_REQUIRE(ok, kErrShape, "act_and_mul_quant: d=%lld exceeds the register-resident limit 32768",
               (long long)d);
   return check_launch("act_and_mul_quant");
+}
+
+int rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, float eps, int64_t M,
+                       int64_t H, int8_t* q, float* s, void* y, hipStream_t st) {
+  MW8_REQUIRE(x && weight, kErrArg, "rmsnorm_quant: null pointer");
+  MW8_REQUIRE((q == nullptr) == (s == nullptr) && (q || y), kErrArg,
+              "rmsnorm_quant: q and s both given or both NULL, and q or y given");
+  MW8_REQUIRE(M >= 0 && H > 0 && H % 8 == 0, kErrShape, "rmsnorm_quant: need H %% 8 == 0 (H=%lld)",
+              (long long)H);
+  MW8_REQUIRE(eps >= 0.0f, kErrArg, "rmsnorm_quant: eps must be >= 0");
+  if (M == 0) return kOk;
+  MW8_REQUIRE(M < (1ll << 31), kErrShape, "rmsnorm_quant: too many rows");
+  MW8_REQUIRE(aligned16(x) && aligned16(weight) && (!q || aligned8(q)) && (!residual || aligned16(residual)) &&
+                  (!y || aligned16(y)),
+              kErrAlign, "rmsnorm_quant: x/residual/weight/y need 16-byte and q 8-byte alignment");
+  const bool ok = dispatch_rows<NormLaunch>(H / 8, M, st, static_cast<const uint16_t*>(x),
+                                            static_cast<uint16_t*>(residual),
+                                            static_cast<const uint16_t*>(weight), eps, M, H, q, s,
+                                            static_cast<uint16_t*>(y));
+  MW8_REQUIRE(ok, kErrShape, "rmsnorm_quant: H=%lld exceeds the register-resident limit 32768",
+              (long long)H);
+  return check_launch("rmsnorm_quant");
 }
 
 }  // namespace mw8

@@ -9,6 +9,7 @@ from .ops import (
     moe_align_block_size,
     moe_sum_reduce,
     quant_per_token,
+    rmsnorm_quant,
     topk_softmax,
 )
 
@@ -24,5 +25,6 @@ __all__ = [
     "moe_align_block_size",
     "moe_sum_reduce",
     "quant_per_token",
+    "rmsnorm_quant",
     "topk_softmax",
 ]

@@ -103,6 +103,48 @@ def act_and_mul_quant(
     return (q, s, a) if return_act else (q, s)
 
 
+def rmsnorm_quant(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+    residual: Optional[torch.Tensor] = None,
+    y: Optional[torch.Tensor] = None,
+    return_y: bool = False,
+    quantize: bool = True,
+):
+    """Fused RMSNorm (+ residual add, in place) and per-token int8 quant.
+
+    bf16 x [M, H] -> (int8 q [M, H], fp32 s [M][, bf16 y [M, H]]).  With
+    ``residual`` the norm runs on ``bf16(x + residual)``, which is written
+    back into ``residual`` (the reference's fused_add_rmsnorm contract,
+    python/minisgl/layers/norm.py:33-38).  ``y`` may be ``x`` itself.
+    ``quantize=False`` skips the quantizer and returns ``y`` only.
+    """
+    _on_gpu(x, weight, residual, y)
+    _need(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x: bf16 [M, H] contiguous")
+    M, H = x.shape
+    _need(weight.dtype == torch.bfloat16 and weight.shape == (H,) and weight.is_contiguous(), "weight: bf16 [H]")
+    if residual is not None:
+        _need(residual.dtype == torch.bfloat16 and residual.shape == (M, H) and residual.is_contiguous(),
+              "residual: bf16 [M, H] contiguous")
+    if (return_y or not quantize) and y is None:
+        y = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+    if y is not None:
+        _need(y.dtype == torch.bfloat16 and y.shape == (M, H) and y.is_contiguous(), "y: bf16 [M, H]")
+    q = torch.empty((M, H), dtype=torch.int8, device=x.device) if quantize else None
+    s = torch.empty((M,), dtype=torch.float32, device=x.device) if quantize else None
+    if M > 0:
+        check(
+            load().mw8_rmsnorm_quant_bf16(
+                _ptr(x), _ptr(residual), _ptr(weight), float(eps), M, H, _ptr(q), _ptr(s), _ptr(y),
+                _stream(x),
+            )
+        )
+    if not quantize:
+        return y
+    return (q, s, y) if (return_y or y is not None) else (q, s)
+
+
 # ----------------------------------------------------------------- dense GEMM
 def _check_gemm(q: torch.Tensor, w: torch.Tensor) -> Tuple[int, int, int]:
     _on_gpu(q, w)
@@ -290,6 +332,7 @@ __all__ = [
     "gemm_workspace",
     "quant_per_token",
     "act_and_mul_quant",
+    "rmsnorm_quant",
     "gemm_w8a8",
     "gemm_w8a8_i32",
     "topk_softmax",

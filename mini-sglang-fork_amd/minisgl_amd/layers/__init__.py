@@ -10,6 +10,7 @@ from .linear import (
 )
 from .mlp import GatedMLPW8A8
 from .moe import MoELayer
+from .norm import RMSNorm, RMSNormFused, RMSNormQuant
 
 __all__ = [
     "BaseOP",
@@ -23,6 +24,9 @@ __all__ = [
     "quantize_weight",
     "GatedMLPW8A8",
     "MoELayer",
+    "RMSNorm",
+    "RMSNormFused",
+    "RMSNormQuant",
     "silu_and_mul",
     "gelu_and_mul",
     "silu_and_mul_quant",

@@ -35,6 +35,10 @@ checks live in tests/test_oracle.py):
 * moe_sum_reduce    -- a rounding-order case whose sequential fp32 result
                        differs from the exact sum; small-integer exact sums.
 * fused_moe_w8a8    -- brute-force per-(token, slot) loop on tiny shapes.
+* rmsnorm_quant     -- exact rational sum of squares (fractions), a torch
+                       fp64 RMSNorm cross-check, the residual add against
+                       torch's bf16 add, and planted mistakes (eps outside
+                       the square root, mean over H-1, no weight).
 
 Top-k tie-breaking and the order of pairs inside one expert segment are
 internals of the third-party ``sgl_kernel`` (>=0.3.17.post1, not vendored):
@@ -65,6 +69,7 @@ __all__ = [
     "moe_sum_reduce",
     "grouped_gemm_w8a8",
     "fused_moe_w8a8",
+    "rmsnorm_quant",
 ]
 
 _F32 = np.float32
@@ -357,3 +362,42 @@ def fused_moe_w8a8(
             q_a=q_a, s_a=s_a, cache3=c3,
         )
     return out
+
+
+# --------------------------------------------------------------------------
+# Fused RMSNorm (+ residual) and per-token requant: the next step upstream
+# of the path.  Replaces flashinfer rmsnorm / fused_add_rmsnorm
+# (python/minisgl/layers/norm.py:8-38; called at
+# python/minisgl/models/qwen3.py:37-40) followed by the quantizer of the
+# W8A8 linear that consumes the normalised activations.
+# --------------------------------------------------------------------------
+def rmsnorm_quant(
+    x: np.ndarray,
+    weight: np.ndarray,
+    eps: float,
+    residual: Optional[np.ndarray] = None,
+):
+    """Closed form (every value a float32 array holding bf16 values):
+
+    ``h = x`` or ``h = bf16(x + residual)`` (fp32 add, RNE narrowing; the
+    new residual), ``ss = sum_k h_k^2`` exactly, ``ms = fp32(ss / H)``,
+    ``r = 1 / sqrt(ms + eps)`` in fp32 IEEE arithmetic,
+    ``y = bf16((h * r) * w)`` with each product rounded to fp32, then
+    ``(q, s) = quant_per_token(y)``.
+
+    ``ss`` is summed in float64 here: each square of a bf16 value is exact
+    in float64, and the sum of at most 32768 of them is exact unless the
+    squares span more than ~2^38 in magnitude, far outside activations.
+
+    Returns (q int8 [M, H], s fp32 [M], y fp32 [M, H], h fp32 [M, H]).
+    """
+    x = np.asarray(x, _F32)
+    M, H = x.shape
+    w = np.asarray(weight, _F32).reshape(1, H)
+    h = x if residual is None else bf16_round((x + np.asarray(residual, _F32)).astype(_F32))
+    ss = (h.astype(np.float64) ** 2).sum(axis=1)
+    ms = (ss / np.float64(H)).astype(_F32)
+    r = (_F32(1.0) / np.sqrt(ms + _F32(eps), dtype=_F32)).astype(_F32)
+    y = bf16_round(((h * r[:, None]).astype(_F32) * w).astype(_F32))
+    q, s_ = quant_per_token(y)
+    return q, s_, y, h

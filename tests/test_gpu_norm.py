@@ -1,0 +1,113 @@
+"""GPU parity of the fused RMSNorm (+ residual) + per-token requant kernel
+against the CPU oracle: q int8, s fp32, the normalised bf16 y and the
+updated residual all bit-exact (the closed form sums squares exactly and
+rounds every fp32 step the way the oracle does)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, bf16_bits_equal, f32
+from minisgl_amd.kernel import rmsnorm_quant
+from minisgl_amd.layers import RMSNorm, RMSNormFused, RMSNormQuant
+from oracle import w8a8 as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _case(M, H, seed, outliers=True):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, H, generator=gen)
+    if outliers:
+        x[torch.rand(M, H, generator=gen) < 1e-3] *= 20
+    res = torch.randn(M, H, generator=gen).to(torch.bfloat16)
+    w = (torch.rand(H, generator=gen) * 1.5 + 0.25).to(torch.bfloat16)
+    return x.to(torch.bfloat16), res, w
+
+
+@pytest.mark.parametrize("M,H", [(1, 5120), (7, 5120), (300, 2048), (2080, 5120), (33, 1032), (5, 40), (3, 17408)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm_quant_bit_exact(M, H, with_res):
+    announce(f"rmsnorm_quant M={M} H={H} res={with_res}")
+    x, res, w = _case(M, H, seed=M * 7 + H)
+    eps = 1e-6
+    xd, rd, wd = x.to(DEV), res.to(DEV), w.to(DEV)
+    q, s, y = rmsnorm_quant(xd, wd, eps, residual=rd if with_res else None, return_y=True)
+    torch.cuda.synchronize()
+    q_ref, s_ref, y_ref, h_ref = orc.rmsnorm_quant(f32(x), f32(w), eps, residual=f32(res) if with_res else None)
+    assert bf16_bits_equal(y, y_ref).all()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    if with_res:
+        assert bf16_bits_equal(rd, h_ref).all()
+
+
+def test_rmsnorm_zero_row_and_in_place_output():
+    """A zero row (ss = 0: r = 1/sqrt(eps), y = 0, s = 0, q = 0) and y written
+    over x itself."""
+    announce("rmsnorm zero row / in place")
+    x, res, w = _case(4, 1024, seed=11, outliers=False)
+    x[2] = 0
+    xd, wd = x.to(DEV), w.to(DEV)
+    q, s = rmsnorm_quant(xd, wd, 1e-5, y=xd)[:2]
+    torch.cuda.synchronize()
+    q_ref, s_ref, y_ref, _ = orc.rmsnorm_quant(f32(x), f32(w), 1e-5)
+    assert bf16_bits_equal(xd, y_ref).all()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    assert s.cpu()[2] == 0 and not q.cpu()[2].any()
+
+
+def test_norm_layers_follow_the_reference_contract():
+    """RMSNorm / RMSNormFused / RMSNormQuant (python/minisgl/layers/norm.py:8-38):
+    out-of-place norm, fused add with residual updated in place and the
+    normalised value written over x, and the quantized variant."""
+    announce("norm layers")
+    M, H, eps = 9, 2048, 1e-6
+    x, res, w = _case(M, H, seed=13)
+    for cls in (RMSNorm, RMSNormFused, RMSNormQuant):
+        layer = cls(H, eps)
+        layer.load_state_dict({"weight": w.to(DEV)})
+        xd, rd = x.to(DEV), res.to(DEV)
+        if cls is RMSNorm:
+            y = layer.forward(xd)
+            _, _, y_ref, _ = orc.rmsnorm_quant(f32(x), f32(w), eps)
+            assert bf16_bits_equal(y, y_ref).all() and torch.equal(xd.cpu(), x)
+            layer.forward_inplace(xd)
+            assert bf16_bits_equal(xd, y_ref).all()
+        elif cls is RMSNormFused:
+            y, r0 = layer.forward(xd)
+            _, _, y_ref, _ = orc.rmsnorm_quant(f32(x), f32(w), eps)
+            assert bf16_bits_equal(y, y_ref).all() and r0 is xd
+            y2, r2 = layer.forward(xd, rd)
+            _, _, y2_ref, h_ref = orc.rmsnorm_quant(f32(x), f32(w), eps, residual=f32(res))
+            assert y2 is xd and r2 is rd
+            assert bf16_bits_equal(xd, y2_ref).all() and bf16_bits_equal(rd, h_ref).all()
+        else:
+            q, s, r0 = layer.forward(xd, rd)
+            q_ref, s_ref, _, h_ref = orc.rmsnorm_quant(f32(x), f32(w), eps, residual=f32(res))
+            np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+            np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+            assert r0 is rd and bf16_bits_equal(rd, h_ref).all()
+
+
+def test_rmsnorm_quant_in_a_graph():
+    """Captured in a HIP graph and replayed, with eager work between replays."""
+    announce("rmsnorm graph replay")
+    x, res, w = _case(64, 5120, seed=17)
+    xd, wd = x.to(DEV), w.to(DEV)
+    q_ref, s_ref, _, _ = orc.rmsnorm_quant(f32(x), f32(w), 1e-6)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        q, s = rmsnorm_quant(xd, wd, 1e-6)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            q, s = rmsnorm_quant(xd, wd, 1e-6)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        q.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+        np.testing.assert_array_equal(s.cpu().numpy(), s_ref)

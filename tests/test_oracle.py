@@ -326,3 +326,85 @@ def test_fused_moe_brute_force_tiny():
             a = g1[:I] / (1 + np.exp(-g1[:I])) * g1[I:]
             f[t] += tw[t, i] * ((w2[e].astype(np.float64) * s2[e][:, None]) @ a)
     assert np.linalg.norm(out - f) / np.linalg.norm(f) < 0.05
+
+
+# ------------------------------------------------------- RMSNorm + requant
+def _rms_torch64(h, w, eps):
+    """Independent restatement in torch float64 (no fp32 rounding steps)."""
+    h64 = torch.from_numpy(np.asarray(h, np.float64))
+    w64 = torch.from_numpy(np.asarray(w, np.float64))
+    r = torch.rsqrt((h64 * h64).mean(dim=1, keepdim=True) + eps)
+    return (h64 * r * w64).numpy()
+
+
+def test_rmsnorm_closed_forms():
+    """Constant rows give r exactly: c = 2, eps = 0 -> r = 1/2 and y = w;
+    eps = 12 -> r = 1/sqrt(16) = 1/4 and y = w / 2."""
+    H = 64
+    w = _bf16(np.linspace(-3, 3, H).astype(np.float32))
+    x = np.full((2, H), 2.0, np.float32)
+    _, _, y0, _ = orc.rmsnorm_quant(x, w, 0.0)
+    np.testing.assert_array_equal(y0, np.broadcast_to(w, (2, H)))
+    _, _, y1, _ = orc.rmsnorm_quant(x, w, 12.0)
+    np.testing.assert_array_equal(y1, np.broadcast_to(_bf16(w / 2), (2, H)))
+
+
+def test_rmsnorm_matches_torch_float64():
+    """Seeded rows with outliers: the fp32 closed form agrees with a torch
+    float64 RMSNorm to bf16 rounding, and the sum of squares it uses is the
+    exact rational one."""
+    from fractions import Fraction
+
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(16, 2048, generator=gen)
+    x[torch.rand(16, 2048, generator=gen) < 1e-3] *= 20
+    x = x.to(torch.bfloat16).float().numpy()
+    w = (torch.rand(2048, generator=gen) + 0.5).to(torch.bfloat16).float().numpy()
+    q, s, y, h = orc.rmsnorm_quant(x, w, 1e-6)
+    ref = _rms_torch64(x, w, 1e-6)
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) <= 2.0 ** -8 + 1e-6
+    exact = sum(Fraction(float(v)) ** 2 for v in x[3])
+    assert float(exact) == float((x[3].astype(np.float64) ** 2).sum())
+    q2, s2 = orc.quant_per_token(y)
+    np.testing.assert_array_equal(q, q2)
+    np.testing.assert_array_equal(s, s2)
+
+
+def test_rmsnorm_residual_add_matches_torch_bf16():
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(4, 512, generator=gen).to(torch.bfloat16)
+    res = torch.randn(4, 512, generator=gen).to(torch.bfloat16)
+    w = torch.ones(512).to(torch.bfloat16)
+    _, _, y, h = orc.rmsnorm_quant(x.float().numpy(), w.float().numpy(), 1e-5, residual=res.float().numpy())
+    np.testing.assert_array_equal(h, (x + res).float().numpy())  # torch: fp32 add, RNE to bf16
+    ref = _rms_torch64(h, w.float().numpy(), 1e-5)
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) <= 2.0 ** -8 + 1e-6
+
+
+@pytest.mark.parametrize("mistake", ["eps_outside_sqrt", "mean_over_h_minus_1", "no_weight"])
+def test_planted_rmsnorm_mistakes_are_caught(mistake):
+    """Plant a plausible mistake into a copy of the closed form: the float64
+    torch cross-check catches each (H = 16: a mean over H - 1 is then off by
+    3%, beyond bf16 rounding)."""
+    H = 16
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(8, H, generator=gen).to(torch.bfloat16).float().numpy()
+    w = (torch.rand(H, generator=gen) + 0.5).to(torch.bfloat16).float().numpy()
+    eps = 0.5  # large enough that misplacing it matters
+
+    def planted(xx):
+        ss = (xx.astype(np.float64) ** 2).sum(axis=1)
+        div = H - 1 if mistake == "mean_over_h_minus_1" else H
+        ms = (ss / div).astype(np.float32)
+        if mistake == "eps_outside_sqrt":
+            r = (np.float32(1) / np.sqrt(ms, dtype=np.float32) + np.float32(eps)).astype(np.float32)
+        else:
+            r = (np.float32(1) / np.sqrt(ms + np.float32(eps), dtype=np.float32)).astype(np.float32)
+        ww = np.ones_like(w) if mistake == "no_weight" else w
+        return orc.bf16_round((xx * r[:, None]).astype(np.float32) * ww)
+
+    ref = _rms_torch64(x, w, eps)
+    good = orc.rmsnorm_quant(x, w, eps)[2]
+    assert np.max(np.abs(good - ref) / (np.abs(ref) + 1e-30)) <= 2.0 ** -8 + 1e-6
+    bad = planted(x)
+    assert np.max(np.abs(bad - ref) / (np.abs(ref) + 1e-30)) > 2.0 ** -6
