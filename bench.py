@@ -280,7 +280,10 @@ def main() -> int:
             "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2),
             "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
             "bound": bound, "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
-            "kernel": "decode_gemm_kernel" if M <= 64 else "tile3_gemm_kernel",
+            # the library's path choice: the LDS-ring decode core up to 32 rows
+            # (the register decode core at 33-64 rows when K % 128 != 0)
+            "kernel": ("decode3_gemm_kernel" if M <= 32 else
+                       "decode_gemm_kernel" if M <= 64 and K % 128 else "tile3_gemm_kernel"),
         })
     dom = max(shapes, key=lambda r: r["us"])
     dom_ops = 2.0 * dom["M"] * dom["N"] * dom["K"]

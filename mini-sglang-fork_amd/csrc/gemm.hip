@@ -1,6 +1,6 @@
-// Dense W8A8 GEMM: dispatch between the decode core (M <= 64: weight
-// streaming, in-block split-K) and the MFMA tile core (M > 64), plus the
-// grouped-tile launchers used by the fused-MoE GEMM.
+// Dense W8A8 GEMM: dispatch between the decode core (M <= 32, or up to 64
+// when K % 128 != 0: weight streaming, in-block split-K) and the MFMA tile
+// core, plus the grouped-tile launchers used by the fused-MoE GEMM.
 #include <atomic>
 
 #include "gemm_kernels.h"
@@ -146,108 +146,154 @@ void launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
 }
 
 // 0-4: register-staged tile core (any K % 16 == 0); 5 and up: direct-to-LDS
-// ring (K % bk == 0).
+// ring (K % bk == 0).  per_cu: resident blocks per CU (LDS-bound).
 struct TileCfg {
   int bm, bn;
   bool dma;
-  int bk;
+  int bk, per_cu;
 };
 constexpr TileCfg kTileCfgs[] = {
-    {256, 256, false, 128}, {256, 256, false, 64}, {128, 128, false, 128},
-    {256, 128, false, 128}, {128, 256, false, 128},
-    {256, 256, true, 64},   // 5: 4 waves, 4 stages
-    {256, 256, true, 64},   // 6: 4 waves, 3 stages
-    {128, 128, true, 64},   // 7: 4 waves, 4 stages
-    {256, 128, true, 64},   // 8: 4 waves, 4 stages
-    {256, 256, true, 64},   // 9: 8 waves (2x4), 3 stages
-    {256, 256, true, 64},   // 10: 8 waves (4x2), 3 stages
-    {256, 256, true, 64},   // 11: 8 waves (2x4), 4 stages
-    {256, 128, true, 64},   // 12: 8 waves (4x2), 3 stages
-    {256, 256, true, 64},   // 13: 16 waves (4x4), 3 stages
-    {256, 256, true, 128},  // 14: 8 waves (4x2), 2 stages
-    {256, 128, true, 128},  // 15: 8 waves (4x2), 2 stages
-    {256, 256, true, 128},  // 16: 16 waves (4x4), 2 stages
-    {256, 128, true, 128},  // 17: 8 waves (4x2), 3 stages
+    {256, 256, false, 128, 1}, {256, 256, false, 64, 1}, {128, 128, false, 128, 2},
+    {256, 128, false, 128, 1}, {128, 256, false, 128, 1},
+    {256, 256, true, 64, 1},   // 5: 4 waves, 4 stages
+    {256, 256, true, 64, 1},   // 6: 4 waves, 3 stages
+    {128, 128, true, 64, 2},   // 7: 4 waves, 4 stages
+    {256, 128, true, 64, 1},   // 8: 4 waves, 4 stages
+    {256, 256, true, 64, 1},   // 9: 8 waves (2x4), 3 stages
+    {256, 256, true, 64, 1},   // 10: 8 waves (4x2), 3 stages
+    {256, 256, true, 64, 1},   // 11: 8 waves (2x4), 4 stages
+    {256, 128, true, 64, 2},   // 12: 8 waves (4x2), 3 stages
+    {256, 256, true, 64, 1},   // 13: 16 waves (4x4), 3 stages
+    {256, 256, true, 128, 1},  // 14: 8 waves (4x2), 2 stages
+    {256, 128, true, 128, 1},  // 15: 8 waves (4x2), 2 stages
+    {256, 256, true, 128, 1},  // 16: 16 waves (4x4), 2 stages
+    {256, 128, true, 128, 1},  // 17: 8 waves (4x2), 3 stages
+    {64, 256, true, 128, 1},   // 18: 4 waves (1x4), 3 stages
+    {64, 128, true, 128, 2},   // 19: 4 waves (1x4), 3 stages
+    {128, 256, true, 128, 1},  // 20: 8 waves (2x4), 2 stages
+    {128, 128, true, 128, 2},  // 21: 4 waves (2x2), 2 stages
+    {64, 256, true, 64, 2},    // 22: 4 waves (1x4), 3 stages
+    {128, 256, true, 64, 2},   // 23: 8 waves (2x4), 3 stages
+    {64, 256, true, 128, 1},   // 24: 4 waves (1x4), 4 stages
+    {64, 128, true, 128, 1},   // 25: 4 waves (1x4), 4 stages
 };
 constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
-// Split of the last, partial wave of 256 x 256 tiles (one resident tile per
-// CU): the r = T mod 256 tail tiles (all T tiles when T < 256) are cut into
-// sp = min(256 / r, K / 128, 16) K ranges when that gives sp >= 2.
+// K split of a ring tiling.  With T tiles and S = 256 * per_cu resident
+// slots: T >= S cuts the r = T mod S tiles of the last, partial wave into
+// sp = min(S / r, K / bk, 16) K ranges; T < S cuts every tile into
+// sp = min(S / T, K / bk, 16) ranges.  No split when sp < 2.
 struct SplitPlan {
   int64_t full = 0, tail = 0;
   int sp = 1;
   size_t ws = 0;
 };
-constexpr int64_t kSlotsPerWave = 256;
 
-SplitPlan plan_split(int64_t M, int64_t N, int64_t K) {
+SplitPlan plan_split(int64_t M, int64_t N, int64_t K, const TileCfg& c) {
   SplitPlan p;
-  if (M <= kDecodeMaxM || K % 128 != 0) return p;
-  const int64_t T = ((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t r = T % kSlotsPerWave;
+  if (!c.dma || K % c.bk != 0) return p;
+  const int64_t T = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+  const int64_t slots = 256 * static_cast<int64_t>(c.per_cu);
+  const int64_t r = T >= slots ? T % slots : T;
   if (r == 0) return p;
-  int64_t sp = kSlotsPerWave / r;
-  const int64_t nkt = K / 128;
+  int64_t sp = slots / r;
+  const int64_t nkt = K / c.bk;
   if (sp > nkt) sp = nkt;
   if (sp > 16) sp = 16;
   if (sp < 2) return p;
   p.full = T - r;
   p.tail = r;
   p.sp = static_cast<int>(sp);
-  p.ws = static_cast<size_t>(r) * sp * 65536 * sizeof(int32_t);
+  p.ws = static_cast<size_t>(r) * sp * c.bm * c.bn * sizeof(int32_t);
   return p;
 }
 
-// Pick the configuration with the smallest modelled time: waves of
-// resident tiles x per-wave tile area / relative efficiency.  The
-// efficiencies are per-op throughputs measured on MI355X relative to the
-// 128x128 ring (cfg 7, two blocks per CU): the 8-wave 256x256 BK=128 ring
-// with 64x128 wave tiles (cfg 14, one block per CU) runs ~1.35x faster per
-// op at K ~ 5K and ~1.37x at K ~ 17K (3-5% ahead of the 16-wave cfg 16);
-// the 8-wave 256x128 ring (cfg 12, two blocks per CU) ~1.12x.  Shapes with
-// K % 64 != 0 use the register-staged core.
+// Only the 256 x 256 rings split automatically; the skinny rings (18-25)
+// split whenever their plan does.
+bool split_enabled(int cfg) {
+  const TileCfg& c = kTileCfgs[cfg];
+  return c.dma && ((c.bm == 256 && c.bn == 256) || cfg >= 18);
+}
+
+// Modelled time (us) of one ring configuration: waves of resident blocks,
+// each wave costing c0 + b x (block ops) / (per-CU rate with b blocks
+// resident on the busiest CU), plus the K split's partial tiles (written
+// and read back at ~4 TB/s) and its reduction launch, floored by the
+// weight stream (~3.6 TB/s for these tilings).  Rates (TOPS per CU) fitted
+// to MI355X sweeps of the Qwen3-14B shapes at M = 40 - 8192.
+struct ModelCfg {
+  int cfg;
+  double c0, r1, r2;  // us per wave; rate with one / two blocks per CU
+};
+constexpr ModelCfg kModelCfgs[] = {
+    {14, 5.0, 9.2, 9.2},  // 256x256, 8 waves
+    {21, 3.0, 3.7, 6.1},  // 128x128 BK 128, 2 stages, two per CU
+    {7, 3.0, 4.6, 5.9},   // 128x128 BK 64, 4 stages, two per CU
+    {25, 3.0, 3.36, 3.36},  // 64x128, 4 stages
+};
+
+double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
+  const TileCfg& t = kTileCfgs[mc.cfg];
+  const int64_t T = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+  const int64_t slots = 256 * static_cast<int64_t>(t.per_cu);
+  const double blk_ops = 2.0 * t.bm * t.bn * static_cast<double>(K);
+  auto wave_us = [&](int64_t units, double kfrac) {
+    int64_t b = (units + 255) / 256;
+    if (b > t.per_cu) b = t.per_cu;
+    const double r = b >= 2 ? mc.r2 : mc.r1;
+    return mc.c0 + static_cast<double>(b) * blk_ops * kfrac / (r * 1e6);
+  };
+  const SplitPlan sp = split_enabled(mc.cfg) ? plan_split(M, N, K, t) : SplitPlan{};
+  const int64_t whole = sp.sp > 1 ? sp.full : T;
+  double us = static_cast<double>(whole / slots) * wave_us(slots, 1.0);
+  if (whole % slots) us += wave_us(whole % slots, 1.0);
+  if (sp.sp > 1) {
+    us += wave_us(sp.tail * sp.sp, 1.0 / sp.sp);
+    us += 2.0 * static_cast<double>(sp.ws) / 4e6 + 3.0;
+  }
+  const double stream_us = static_cast<double>(N) * static_cast<double>(K) / 3.6e6;
+  return us > stream_us ? us : stream_us;
+}
+
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   if (K % 64 != 0) return 2;
-  struct Cand {
-    int cfg, per_cu;
-    double eff;
-  };
-  const Cand cands[] = {{14, 1, K > 8192 ? 1.37 : 1.35}, {12, 2, 1.12}, {7, 2, 1.0}};
   int best = 7;
-  double best_cost = 1e300;
-  const SplitPlan sp = plan_split(M, N, K);
-  for (const Cand& c : cands) {
-    const TileCfg t = kTileCfgs[c.cfg];
-    if (K % t.bk != 0) continue;
-    const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-    const int64_t slots = 256 * static_cast<int64_t>(c.per_cu);
-    double waves = static_cast<double>((tiles + slots - 1) / slots);
-    // the 256 x 256 tail split: full waves plus one wave of 1/sp-length units
-    // (and the partial-tile reduction, modelled as a tenth of a wave)
-    if (t.bm == 256 && t.bn == 256 && sp.sp > 1)
-      waves = static_cast<double>(sp.full / kSlotsPerWave) + 1.0 / sp.sp + 0.1;
-    const double cost = waves * t.bm * t.bn * c.per_cu / c.eff;
-    if (cost < best_cost) {
-      best_cost = cost;
-      best = c.cfg;
+  double best_us = 1e300;
+  for (const ModelCfg& mc : kModelCfgs) {
+    if (K % kTileCfgs[mc.cfg].bk != 0) continue;
+    const double us = model_us(M, N, K, mc);
+    if (us < best_us) {
+      best_us = us;
+      best = mc.cfg;
     }
   }
   return best;
 }
 
+// The ring configuration a dense call at (M, N, K) runs (override first).
+int select_tile_cfg(int64_t M, int64_t N, int64_t K) {
+  const int cfg = g_tile_cfg.load(std::memory_order_relaxed);
+  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && K % kTileCfgs[cfg].bk != 0))
+    return default_tile_cfg(M, N, K);
+  return cfg;
+}
+
+template <int BM, int BN, int EPI>
+void launch_split_reduce(const GemmArgs& g, const SplitPlan& sp, hipStream_t st) {
+  const int64_t threads = sp.tail * BM * (BN / 8);
+  hipLaunchKernelGGL((split_reduce_kernel<EPI, BM, BN>),
+                     dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, st, g);
+}
+
 template <int EPI>
 void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
-  int cfg = g_tile_cfg.load(std::memory_order_relaxed);
-  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && g.K % kTileCfgs[cfg].bk != 0))
-    cfg = default_tile_cfg(g.M, g.N, g.K);
+  const int cfg = select_tile_cfg(g.M, g.N, g.K);
   const TileCfg c = kTileCfgs[cfg];
   unsigned tiles =
       static_cast<unsigned>(((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn));
-  // tail split (256 x 256 ring configurations): needs the caller's workspace
-  const SplitPlan sp = plan_split(g.M, g.N, g.K);
-  const bool split = c.dma && c.bm == 256 && c.bn == 256 && sp.sp > 1 && ws != nullptr &&
-                     ws_bytes >= sp.ws && g.K % c.bk == 0;
+  // K split (ring configurations): needs the caller's workspace
+  const SplitPlan sp = plan_split(g.M, g.N, g.K, c);
+  const bool split = split_enabled(cfg) && sp.sp > 1 && ws != nullptr && ws_bytes >= sp.ws;
   g.tail_split = 1;
   if (split) {
     g.part = static_cast<int32_t*>(ws);
@@ -273,18 +319,38 @@ void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     case 15: launch_tile3<256, 128, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 16: launch_tile3<256, 256, 128, 4, 4, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 17: launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 18: launch_tile3<64, 256, 128, 1, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 19: launch_tile3<64, 128, 128, 1, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 20: launch_tile3<128, 256, 128, 2, 4, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 21: launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 22: launch_tile3<64, 256, 64, 1, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 23: launch_tile3<128, 256, 64, 2, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 24: launch_tile3<64, 256, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 25: launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
   if (split) {
-    const int64_t threads = sp.tail * 256 * 32;
-    hipLaunchKernelGGL(split_reduce_kernel<EPI>, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                       dim3(256), 0, st, g);
+    switch (c.bm * 1000 + c.bn) {
+      case 64256: launch_split_reduce<64, 256, EPI>(g, sp, st); break;
+      case 64128: launch_split_reduce<64, 128, EPI>(g, sp, st); break;
+      case 128256: launch_split_reduce<128, 256, EPI>(g, sp, st); break;
+      case 128128: launch_split_reduce<128, 128, EPI>(g, sp, st); break;
+      default: launch_split_reduce<256, 256, EPI>(g, sp, st); break;
+    }
   }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-
+// Decode core up to 32 tokens, the tile core above 64.  In between the
+// tile core when K % 128 == 0 (its 64-row rings stream 1.2-2x faster than
+// the decode core at 33-64 tokens on MI355X), unless a decode
+// configuration is forced; a forced tile configuration takes it for any K.
+bool use_tile_path(int64_t M, int64_t K) {
+  if (M > kDecodeMaxM) return true;
+  if (M <= 32 || g_decode_cfg.load(std::memory_order_relaxed) >= 0) return false;
+  return K % 128 == 0 || g_tile_cfg.load(std::memory_order_relaxed) >= 0;
+}
 
 int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
                 const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* ws,
@@ -306,7 +372,7 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
   g.out = out; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldo = N;
   g.top_k = 1;
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
-  if (M <= kDecodeMaxM) {
+  if (!use_tile_path(M, K)) {
     if (epi == kEpiBf16) dispatch_decode<kEpiBf16>(g, st);
     else dispatch_decode<kEpiI32>(g, st);
   } else {
@@ -326,8 +392,9 @@ void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
 }
 
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return plan_split(M, N, K).ws;
+  if (M <= 0 || N <= 0 || K <= 0 || !use_tile_path(M, K)) return 0;
+  const int cfg = select_tile_cfg(M, N, K);
+  return split_enabled(cfg) ? plan_split(M, N, K, kTileCfgs[cfg]).ws : 0;
 }
 
 int gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,

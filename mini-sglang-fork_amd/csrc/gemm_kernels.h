@@ -55,10 +55,11 @@ struct GemmArgs {
   int64_t num_valid;           // M * top_k
   int32_t top_k;
   int32_t num_experts;         // blocks owned by an id outside [0, E) are skipped
-  // dense split tail (256 x 256 tilings only): blocks [0, full_tiles) own
-  // whole tiles; block full_tiles + u owns K range u % tail_split of tail
-  // tile full_tiles + u / tail_split and writes its int32 partial tile to
-  // part[u][256][256] (summed by split_reduce_kernel).
+  // dense K split (ring tile core): blocks [0, full_tiles) own whole
+  // tiles; block full_tiles + u owns K range u % tail_split of tile
+  // full_tiles + u / tail_split and writes its int32 partial tile to
+  // part[u][BM][BN] (summed in split order by split_reduce_kernel).
+  // full_tiles = 0 splits every tile (grids with fewer tiles than CUs).
   int32_t* part;
   int64_t full_tiles;
   int32_t tail_split;          // <= 1: no split
@@ -1228,23 +1229,24 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
-// Split-tail reduction: out[tile rows, tile cols] = epilogue(sum_s part[u0 + s])
+// K-split reduction: out[tile rows, tile cols] = epilogue(sum_s part[u0 + s])
 // with the partials summed in split order (exact int32).  One thread per 8
 // consecutive columns of one tile row.
 // ------------------------------------------------------------------------
-template <int EPI>
+template <int EPI, int BM, int BN>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
-  const int64_t tm = (g.M + 255) / 256, tn = (g.N + 255) / 256;
+  constexpr int kC8 = BN / 8;
+  const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   const int64_t tail = tm * tn - g.full_tiles;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (tile, row, col8)
-  if (idx >= tail * 256 * 32) return;
-  const int64_t tt = idx / (256 * 32);
-  const int r = static_cast<int>((idx / 32) % 256), c8 = static_cast<int>(idx % 32) * 8;
+  if (idx >= tail * BM * kC8) return;
+  const int64_t tt = idx / (BM * kC8);
+  const int r = static_cast<int>((idx / kC8) % BM), c8 = static_cast<int>(idx % kC8) * 8;
   int64_t pm, pn;
   tile_of_index(g.full_tiles + tt, tm, tn, pm, pn);
-  const int64_t m = pm * 256 + r;
+  const int64_t m = pm * BM + r;
   if (m >= g.M) return;
-  const int32_t* p = g.part + (tt * g.tail_split) * 65536 + r * 256 + c8;
+  const int32_t* p = g.part + (tt * g.tail_split) * (BM * BN) + r * BN + c8;
   int32_t a[8];
   {
     const v4i x0 = *reinterpret_cast<const v4i*>(p), x1 = *reinterpret_cast<const v4i*>(p + 4);
@@ -1252,19 +1254,30 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
     for (int j = 0; j < 4; ++j) { a[j] = x0[j]; a[4 + j] = x1[j]; }
   }
   for (int s = 1; s < g.tail_split; ++s) {
-    const int32_t* q = p + static_cast<int64_t>(s) * 65536;
+    const int32_t* q = p + static_cast<int64_t>(s) * (BM * BN);
     const v4i x0 = *reinterpret_cast<const v4i*>(q), x1 = *reinterpret_cast<const v4i*>(q + 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) { a[j] += x0[j]; a[4 + j] += x1[j]; }
   }
-  const int64_t n0 = pn * 256 + c8;
+  const int64_t n0 = pn * BN + c8;
   if constexpr (EPI == kEpiBf16) {
     const float sa = g.sa[m];
+    uint16_t o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int64_t n = n0 + j;
-      if (n < g.N)
-        static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a[j], sa, g.sw[n], g.bias, n, 1.0f, false);
+      const int64_t n = n0 + j < g.N ? n0 + j : g.N - 1;
+      o[j] = epi_bf16(a[j], sa, g.sw[n], g.bias, n, 1.0f, false);
+    }
+    uint16_t* dst = static_cast<uint16_t*>(g.out) + m * g.ldo + n0;
+    if (g.staged_out && n0 + 8 <= g.N) {  // 16-byte aligned full chunk
+      v4i v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = static_cast<int>(o[2 * j] | (static_cast<uint32_t>(o[2 * j + 1]) << 16));
+      *reinterpret_cast<v4i*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (n0 + j < g.N) dst[j] = o[j];
     }
   } else {
 #pragma unroll

@@ -122,7 +122,7 @@ def test_gemm_workspace_reuse_and_zero_rows():
     "M,K,N", [(512, 5120, 7168), (300, 1280, 600), (1000, 2048, 1000), (4500, 768, 3840), (2304, 1280, 7168)]
 )
 def test_gemm_split_tail(M, K, N):
-    """Tail-wave K split of the 256x256 tilings: the last partial wave's tiles
+    """Tail-wave K split of the 256x256 tiling (forced): the last partial wave's tiles
     are cut into K ranges whose int32 partial tiles go to the workspace and
     are summed by the reduction kernel.  Bit-exact against the oracle (row
     sample for the larger cases) and against the launch without workspace,
@@ -137,18 +137,22 @@ def test_gemm_split_tail(M, K, N):
     r = T % 256
     sp = min(256 // r, K // 128, 16) if r else 0
     want_ws = r * sp * 65536 * 4 if sp >= 2 else 0
-    assert lib.mw8_gemm_workspace_bytes(M, N, K) == want_ws
-    rows = None if M <= 1024 else np.unique(np.concatenate([[0, M - 1], np.arange(M - 300, M, 7)]))
-    _run_case(M, K, N, seed=7, rows=rows)
-    c = linear_case(M, K, N, seed=8)
-    q, s = quant_per_token(c["x"].to(DEV))
-    w = c["w"].to(DEV)
-    split = gemm_w8a8_i32(q, w)
-    whole = torch.empty_like(split)
-    st = torch.cuda.current_stream().cuda_stream
-    rc = lib.mw8_gemm_w8a8_i32(q.data_ptr(), w.data_ptr(), whole.data_ptr(), M, N, K, None, 0, st)
-    assert rc == 0
-    assert torch.equal(split, whole)
+    lib.mw8_set_tuning(-1, 14, -1)  # the 8-wave 256x256 ring
+    try:
+        assert lib.mw8_gemm_workspace_bytes(M, N, K) == want_ws
+        rows = None if M <= 1024 else np.unique(np.concatenate([[0, M - 1], np.arange(M - 300, M, 7)]))
+        _run_case(M, K, N, seed=7, rows=rows)
+        c = linear_case(M, K, N, seed=8)
+        q, s = quant_per_token(c["x"].to(DEV))
+        w = c["w"].to(DEV)
+        split = gemm_w8a8_i32(q, w)
+        whole = torch.empty_like(split)
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.mw8_gemm_w8a8_i32(q.data_ptr(), w.data_ptr(), whole.data_ptr(), M, N, K, None, 0, st)
+        assert rc == 0
+        assert torch.equal(split, whole)
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
 
 
 def test_gemm_rejects_bad_k():
@@ -189,10 +193,19 @@ def test_linear_layers_drop_in():
             assert bf16_bits_equal(y, y_ref).all()
 
 
-@pytest.mark.parametrize("M,K,N", [(300, 640, 520), (257, 1024, 300), (129, 192, 64), (1000, 2048, 1000)])
+NUM_TILE_CFGS = 26  # kTileCfgs in csrc/gemm.hip
+
+
+@pytest.mark.parametrize(
+    "M,K,N",
+    [(300, 640, 520), (257, 1024, 300), (129, 192, 64), (1000, 2048, 1000),
+     (40, 1024, 520), (64, 2560, 1100), (130, 3072, 700)],
+)
 def test_gemm_every_tile_config(M, K, N):
-    """Each large-M configuration (forced through mw8_set_tuning) on ragged
-    shapes; K % 64 != 0 makes the direct-to-LDS configs fall back."""
+    """Each tile configuration (forced through mw8_set_tuning) on ragged
+    shapes; K % 64 != 0 makes the direct-to-LDS configs fall back.  33-64
+    rows take the tile core only when a tile configuration is forced; with
+    few tiles the skinny rings (18-23) split every tile's K range."""
     from minisgl_amd.kernel.lib import load
 
     announce(f"gemm all tile cfgs M={M} K={K} N={N}")
@@ -204,7 +217,7 @@ def test_gemm_every_tile_config(M, K, N):
     y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
     lib = load()
     try:
-        for cfg in range(18):
+        for cfg in range(NUM_TILE_CFGS):
             lib.mw8_set_tuning(-1, cfg, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
