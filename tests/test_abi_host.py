@@ -53,11 +53,20 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_gemm_workspace_bytes(1, 5120, 5120) == 0
     # tail split of 256x256 tilings: r = T mod 256 tail tiles, sp = min(256 // r, K / 128, 16)
     # K ranges each, one int32 256x256 partial tile per (tile, range)
-    assert lib.mw8_gemm_workspace_bytes(512, 7168, 5120) == 56 * 4 * 256 * 256 * 4
+    assert lib.mw8_gemm_workspace_bytes(1024, 34816, 5120) == 32 * 8 * 256 * 256 * 4
     assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 64 * 4 * 256 * 256 * 4
     assert lib.mw8_gemm_workspace_bytes(8192, 34816, 5120) == 0  # 4352 tiles: whole waves
     assert lib.mw8_gemm_workspace_bytes(4096, 7168, 5120) == 0   # 192 tail tiles: no split
     assert lib.mw8_gemm_workspace_bytes(512, 5120, 5120 + 64) == 0  # K % 128 != 0
+    assert lib.mw8_gemm_workspace_bytes(512, 7168, 5120) == 0  # 128x128 ring (no split) chosen
+    # the 64x128 ring (forced): 272 tiles, 16 in the tail, 16 K ranges each
+    lib.mw8_set_tuning(-1, 25, -1)
+    try:
+        assert lib.mw8_gemm_workspace_bytes(64, 34816, 5120) == 16 * 16 * 64 * 128 * 4
+        assert lib.mw8_gemm_workspace_bytes(40, 1024, 1024) == 8 * 8 * 64 * 128 * 4  # all 8 tiles split
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+    assert lib.mw8_gemm_workspace_bytes(32, 34816, 5120) == 0  # decode core
 
 
 FAKE_A, FAKE_B, FAKE_C = 4096, 8192, 12288  # aligned non-null stand-ins: never dereferenced
