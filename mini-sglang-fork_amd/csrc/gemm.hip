@@ -424,17 +424,40 @@ void launch_grouped_runs(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   launch_tile3<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows>(g, grid, st);
 }
 
+// Persistent grouped GEMM: 256 x per_cu blocks walk the (expert chunk,
+// column tile) items.
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems = false, int kPerCu = 1>
+void launch_grouped_persist(const GemmArgs& g, hipStream_t st) {
+  constexpr int kLds = NSTAGE * (BM + BN) * BK;
+  auto kern = grouped_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, kChunkItems, kPerCu>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(256 * kPerCu)), dim3(64 * WM * WN), kLds, st, g);
+}
+
 // Grouped configurations (mw8_set_tuning moe_cfg): 0-6 one tile per
 // alignment block (tile height = block size), 7 and 8 run tiles of 256 and
-// 128 rows on the 8-wave 256-wide ring (K % 128 == 0).  Automatic choice:
-// cfg 0.  Measured on MI355X at config 3 (E 128, top-8, H 2048, I 768) the
-// run tiles lose at 256, 1024 and 4096 tokens (226 / 308 / 614 us per layer
-// against 169 / 238 / 548 us): three of every four run-tile blocks only
-// read the routing metadata and exit, each holding the CU's LDS through a
-// chain of dependent loads of arrays the alignment kernel has just written.
+// 128 rows on the 8-wave 256-wide ring (K % 128 == 0), 9-12 the persistent
+// item walk with 256x256, 128x256, 256x128 and 128x128 tiles (K % 128 == 0),
+// 13 as 9 with chunk items, 14-17 4-wave 128x256 / 256x128 tiles on
+// 64-byte K stages, two blocks per CU (expert items, chunk items).
+//
+// Automatic choice, measured on MI355X at config 3 (E 128, top-8, H 2048,
+// I 768; whole layer): with at least 32 pairs per expert on average the
+// persistent chunk walk on 128x256 tiles, two blocks per CU (cfg 15):
+// 1024 tokens 237 -> 215 us, 4096 tokens 536 -> 459 us against cfg 0; at
+// 16 pairs per expert (256 tokens) cfg 0 (167 us against 177).  The
+// 256-row run tiles (cfg 7/8) lose at every size: three of every four of
+// their blocks only read routing metadata and exit.
 int default_moe_cfg(const GemmArgs& g, int bm) {
-  (void)g;
   (void)bm;
+  if (g.K % 64 == 0 && g.num_experts < kPersistMaxSlots &&
+      g.num_valid >= 32 * static_cast<int64_t>(g.num_experts))
+    return 15;
   return 0;
 }
 
@@ -450,6 +473,21 @@ void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t 
   const bool bk128 = g.K % 128 == 0;
   if (cfg < 0) cfg = default_moe_cfg(g, bm);
   if (!bk128 && cfg >= 3) cfg = 0;
+  if (cfg >= 9 && (cfg >= 14 || bk128) && g.num_experts < kPersistMaxSlots) {  // persistent item walk
+    switch (cfg) {
+      case 9: launch_grouped_persist<256, 256, 128, 4, 2, 2, EPI>(g, st); break;
+      case 10: launch_grouped_persist<128, 256, 128, 2, 4, 2, EPI>(g, st); break;
+      case 11: launch_grouped_persist<256, 128, 128, 4, 2, 2, EPI>(g, st); break;
+      case 12: launch_grouped_persist<128, 128, 128, 2, 2, 2, EPI, false, 2>(g, st); break;
+      case 13: launch_grouped_persist<256, 256, 128, 4, 2, 2, EPI, true>(g, st); break;
+      case 14: launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, false, 2>(g, st); break;
+      case 15: launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, true, 2>(g, st); break;
+      case 16: launch_grouped_persist<256, 128, 64, 2, 2, 3, EPI, false, 2>(g, st); break;
+      default: launch_grouped_persist<256, 128, 64, 2, 2, 3, EPI, true, 2>(g, st); break;
+    }
+    return;
+  }
+  if (cfg >= 9) cfg = 0;
   if (cfg == 7 || (cfg == 8 && bm == 128)) {  // 256-row run tiles (bm 64 or 128)
     launch_grouped_runs<256, 256, 128, 4, 2, 2, EPI>(g, blocks, st);
     return;

@@ -398,10 +398,18 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// One BM x BN output tile over K stages [kt_begin, kt_end) of the ring core.
+struct TileJob {
+  int64_t m0, n0;     // first (sorted) row and first output column
+  const int8_t* W;    // weight rows of the tile's expert (dense: all of W)
+  const float* sw;
+  int kt_begin, kt_end;
+  int rows_valid;     // rows of the tile that hold sorted positions (runs)
+  int64_t split_unit; // >= 0: write the int32 partial tile part[split_unit]
+};
+
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
-__global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
-  // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
-  // pass only needs the launch stub.
+__device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds, const TileJob& job) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kWaves = WM * WN;
   constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
@@ -416,78 +424,14 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   static_assert(kLA >= 1 && kLB >= 1 && kLA * kRowsPerInst * kWaves == BM &&
                 kLB * kRowsPerInst * kWaves == BN, "DMA split");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
-  extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave / WN, wn = wave % WN;
 
-  const int8_t* W = g.W;
-  const float* sw = g.sw;
-  int64_t m0, n0;
-  int64_t split_unit = -1;  // split-tail unit (writes an int32 partial tile), -1: whole tile
-  int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
-  int rows_valid = BM;      // tile rows that hold sorted positions of this tile's run
-  // grouped grids: x = N tile, y = alignment block (an XCD-contiguous walk
-  // of the (block, N tile) pairs measured slower at 256 and 1024 tokens)
-  const int64_t gx = blockIdx.x, gy = blockIdx.y;
-  if constexpr (Rows::kRuns) {
-    n0 = gx * BN;
-    const int ab = g.align_bsz;
-    const int64_t y = gy;
-    const int64_t npp = *g.num_post_pad;
-    if (y * ab >= npp) return;
-    const int e = g.expert_ids[y];
-    if (e < 0 || e >= g.num_experts) return;
-    // distance j from the first alignment block of expert e: expert_ids is
-    // non-decreasing over the used blocks, so scan back 64 blocks per step
-    // for the nearest block of another expert (index < 0 counts as one)
-    int64_t first = 0;
-    for (int64_t base = y;; base -= 64) {
-      const int64_t idx = base - lane;
-      const int v = idx >= 0 ? g.expert_ids[idx] : -2;
-      const uint64_t other = __ballot(v != e);
-      if (other != 0) {
-        first = base - (__ffsll(static_cast<unsigned long long>(other)) - 1) + 1;
-        break;
-      }
-    }
-    const int per_tile = BM / ab;
-    if ((y - first) % per_tile != 0) return;
-    const int64_t used = npp / ab;
-    const int64_t nxt = y + lane;
-    const int same = (lane < per_tile && nxt < used) ? (g.expert_ids[nxt] == e) : 0;
-    const uint64_t run = __ballot(same != 0);
-    rows_valid = ab * __popcll(run);  // the run's blocks are contiguous from y
-    m0 = y * ab;
-    W += static_cast<int64_t>(e) * g.N * g.K;
-    sw += static_cast<int64_t>(e) * g.N;
-  } else if constexpr (Rows::kGrouped) {
-    n0 = gx * BN;
-    m0 = gy * BM;
-    if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
-    const int e = g.expert_ids[gy];
-    if (e < 0 || e >= g.num_experts) return;
-    W += static_cast<int64_t>(e) * g.N * g.K;
-    sw += static_cast<int64_t>(e) * g.N;
-  } else {
-    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-    int64_t pm, pn;
-    if (g.tail_split > 1) {
-      if (blockIdx.x < g.full_tiles) {
-        tile_of_index(xcd_tile_index(blockIdx.x, g.full_tiles), tm, tn, pm, pn);
-      } else {
-        split_unit = static_cast<int64_t>(blockIdx.x) - g.full_tiles;
-        tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
-        const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
-        kt_begin = static_cast<int>(nkt * sp / g.tail_split);
-        kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
-      }
-    } else {
-      tile_of_block(blockIdx.x, tm, tn, pm, pn);
-    }
-    m0 = pm * BM;
-    n0 = pn * BN;
-  }
+  const int8_t* W = job.W;
+  const float* sw = job.sw;
+  const int64_t m0 = job.m0, n0 = job.n0, split_unit = job.split_unit;
+  const int kt_begin = job.kt_begin, kt_end = job.kt_end, rows_valid = job.rows_valid;
 
   // ---- per-lane DMA sources: instruction j of this wave fills LDS units
   // (j*kWaves + wave)*64 .. +63 of the tile; lane -> (row, chunk)
@@ -560,15 +504,29 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < kFN; ++j) acc[i][j] = v16i{0};
-  // a wave whose rows all lie past an expert run has no MFMA work
-  const bool wave_live = !Rows::kRuns || wm * kWaveM < rows_valid;
-  auto mfmas = [&](int set) {
-    if (!wave_live) return;
+  // Run tiles: the sorted positions of a run are real pairs up to the
+  // expert's padding, which ends it, so the real rows of this wave's range
+  // form a prefix of length live_w; 32-row fragments past it (padding or
+  // past the run) have no MFMA work.  live_w is wave-uniform (ballot).
+  int live_w = kWaveM;
+  if constexpr (Rows::kRuns) {
+    live_w = 0;
 #pragma unroll
-    for (int i = 0; i < kFM; ++i)
+    for (int h = 0; h < kWaveM; h += 64) {
+      const int r = wm * kWaveM + h + lane;
+      const bool real = h + lane < kWaveM && r < rows_valid && g.sorted_ids[m0 + r] < g.num_valid;
+      live_w += __popcll(__ballot(real));
+    }
+    live_w = __builtin_amdgcn_readfirstlane(live_w);
+  }
+  auto mfmas = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < kFM; ++i) {
+      if (Rows::kRuns && 32 * i >= live_w) break;
 #pragma unroll
       for (int j = 0; j < kFN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    }
   };
   constexpr int kSub = BK / 32;  // k-substeps per stage (2 or 4)
 
@@ -744,6 +702,203 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
       }
+    }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
+__global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
+  // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
+  // pass only needs the launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int lane = threadIdx.x & 63;
+  const int8_t* W = g.W;
+  const float* sw = g.sw;
+  int64_t m0, n0;
+  int64_t split_unit = -1;  // split-tail unit (writes an int32 partial tile), -1: whole tile
+  int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
+  int rows_valid = BM;      // tile rows that hold sorted positions of this tile's run
+  // grouped grids: x = N tile, y = alignment block (an XCD-contiguous walk
+  // of the (block, N tile) pairs measured slower at 256 and 1024 tokens)
+  const int64_t gx = blockIdx.x, gy = blockIdx.y;
+  if constexpr (Rows::kRuns) {
+    n0 = gx * BN;
+    const int ab = g.align_bsz;
+    const int64_t y = gy;
+    const int64_t npp = *g.num_post_pad;
+    if (y * ab >= npp) return;
+    const int e = g.expert_ids[y];
+    if (e < 0 || e >= g.num_experts) return;
+    // distance j from the first alignment block of expert e: expert_ids is
+    // non-decreasing over the used blocks, so scan back 64 blocks per step
+    // for the nearest block of another expert (index < 0 counts as one)
+    int64_t first = 0;
+    for (int64_t base = y;; base -= 64) {
+      const int64_t idx = base - lane;
+      const int v = idx >= 0 ? g.expert_ids[idx] : -2;
+      const uint64_t other = __ballot(v != e);
+      if (other != 0) {
+        first = base - (__ffsll(static_cast<unsigned long long>(other)) - 1) + 1;
+        break;
+      }
+    }
+    const int per_tile = BM / ab;
+    if ((y - first) % per_tile != 0) return;
+    const int64_t used = npp / ab;
+    const int64_t nxt = y + lane;
+    const int same = (lane < per_tile && nxt < used) ? (g.expert_ids[nxt] == e) : 0;
+    const uint64_t run = __ballot(same != 0);
+    rows_valid = ab * __popcll(run);  // the run's blocks are contiguous from y
+    m0 = y * ab;
+    W += static_cast<int64_t>(e) * g.N * g.K;
+    sw += static_cast<int64_t>(e) * g.N;
+  } else if constexpr (Rows::kGrouped) {
+    n0 = gx * BN;
+    m0 = gy * BM;
+    if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
+    const int e = g.expert_ids[gy];
+    if (e < 0 || e >= g.num_experts) return;
+    W += static_cast<int64_t>(e) * g.N * g.K;
+    sw += static_cast<int64_t>(e) * g.N;
+  } else {
+    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    int64_t pm, pn;
+    if (g.tail_split > 1) {
+      if (blockIdx.x < g.full_tiles) {
+        tile_of_index(xcd_tile_index(blockIdx.x, g.full_tiles), tm, tn, pm, pn);
+      } else {
+        split_unit = static_cast<int64_t>(blockIdx.x) - g.full_tiles;
+        tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
+        const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
+        kt_begin = static_cast<int>(nkt * sp / g.tail_split);
+        kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
+      }
+    } else {
+      tile_of_block(blockIdx.x, tm, tn, pm, pn);
+    }
+    m0 = pm * BM;
+    n0 = pn * BN;
+  }
+
+  TileJob job{m0, n0, W, sw, kt_begin, kt_end, rows_valid, split_unit};
+  tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// ------------------------------------------------------------------------
+// Persistent grouped GEMM (fused-MoE, 64/128-row alignment blocks).
+// ------------------------------------------------------------------------
+// An expert's alignment blocks form ceil(blocks / per_tile) chunks of
+// near-equal size (per_tile = BM / align_bsz).  Work item = (expert with
+// at least one block, BN-column tile), the block running all its chunks in
+// turn (re-reading the weight tile it has just streamed), or, with
+// kChunkItems, (expert, column tile, chunk), the chunks of one weight tile
+// adjacent in the list and so running side by side on one XCD.
+// Every block derives the item list from expert_ids on its own (no
+// workspace, no extra launch): expert e's blocks are the run
+// [run_start[e], run_start[e + 1]) (expert_ids is non-decreasing over the
+// used blocks).  Items are numbered expert-major, and each XCD's blocks
+// (block b runs on XCD b % 8) deal one contiguous range of them, so all
+// column tiles of an expert share its gathered rows in one L2.  Each block
+// walks its items with a static stride: no queue, no inter-block waiting.
+constexpr int kPersistMaxSlots = 512;  // expert slots (moe_gemm checks E < this)
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems, int kPerCu>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(kPerCu * WM * WN / 4)))
+void grouped_persist_kernel(GemmArgs g) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int run_start[kPersistMaxSlots + 1];  // first alignment block of expert e
+  __shared__ int act_base[kPersistMaxSlots + 1];   // units (experts or chunks) before e
+  __shared__ int wave_tot[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = g.num_experts, ab = g.align_bsz, per_tile = BM / ab;
+  const int used = *g.num_post_pad / ab;  // alignment blocks in use
+  // run starts: the block b where expert_ids steps from p to c starts the
+  // runs of experts p+1 .. c (a virtual block `used` starts every later one)
+  for (int b = tid; b <= used; b += kThreads) {
+    const int prev = b == 0 ? -1 : g.expert_ids[b - 1];
+    int cur = b == used ? E : g.expert_ids[b];
+    if (cur > E) cur = E;
+    for (int e = prev + 1; e <= cur; ++e) run_start[e] = b;
+  }
+  __syncthreads();
+  // exclusive prefix over experts of their unit count: 1 if the expert has
+  // blocks (expert items), or its chunk count (chunk items); two-level scan
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += kThreads) {
+    const int e = e0 + tid;
+    const int len = e < E ? run_start[e + 1] - run_start[e] : 0;
+    const int act = kChunkItems ? (len + per_tile - 1) / per_tile : (len > 0 ? 1 : 0);
+    const int incl = wave_incl_scan(act);
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int before = carry;
+    for (int w = 0; w < wave; ++w) before += wave_tot[w];
+    if (e < E) act_base[e] = before + incl - act;
+    int tot = 0;
+    for (int w = 0; w < kWaves; ++w) tot += wave_tot[w];
+    carry += tot;
+    __syncthreads();
+  }
+  if (tid == 0) act_base[E] = carry;
+  __syncthreads();
+  const int tn = static_cast<int>((g.N + BN - 1) / BN);
+  const int total = carry * tn;
+
+  // this block's share: XCD x deals items [begin, begin + count)
+  const int G = gridDim.x, xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds, per_xcd = G / kXcds;
+  const int base = total / kXcds, rem = total % kXcds;
+  const int begin = xcd * base + (xcd < rem ? xcd : rem), count = base + (xcd < rem ? 1 : 0);
+  for (int j = local; j < count; j += per_xcd) {
+    const int item = begin + j;
+    const int a = item / tn;  // expert items: the active-expert index
+    // the expert: last e with act_base[e] * tn <= item (act_base[e + 1] * tn > item)
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (act_base[mid] * tn <= item) lo = mid; else hi = mid - 1;
+    }
+    const int e = __builtin_amdgcn_readfirstlane(lo);
+    const int b_first = __builtin_amdgcn_readfirstlane(run_start[e]);
+    const int nblocks = __builtin_amdgcn_readfirstlane(run_start[e + 1]) - b_first;
+    const int nch = (nblocks + per_tile - 1) / per_tile;
+    int n_tile, c_lo, c_hi;
+    if constexpr (kChunkItems) {  // item = (expert, column tile, chunk), chunk fastest
+      const int off = item - act_base[e] * tn;
+      n_tile = __builtin_amdgcn_readfirstlane(off / nch);
+      c_lo = __builtin_amdgcn_readfirstlane(off % nch);
+      c_hi = c_lo + 1;
+    } else {  // item = (expert, column tile): all chunks in turn
+      n_tile = __builtin_amdgcn_readfirstlane(item - a * tn);
+      c_lo = 0;
+      c_hi = nch;
+    }
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int c0 = b_first + c * nblocks / nch, c1 = b_first + (c + 1) * nblocks / nch;
+      TileJob job{static_cast<int64_t>(c0) * ab,
+                  static_cast<int64_t>(n_tile) * BN,
+                  g.W + static_cast<int64_t>(e) * g.N * g.K,
+                  g.sw + static_cast<int64_t>(e) * g.N,
+                  0,
+                  static_cast<int>(g.K / BK),
+                  (c1 - c0) * ab,
+                  -1};
+      __syncthreads();  // the previous tile's LDS staging has been read out
+      tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows>(g, lds, job);
     }
   }
 #endif  // __HIP_DEVICE_COMPILE__

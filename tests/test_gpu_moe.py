@@ -133,7 +133,7 @@ def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
     return logits, W, SW, act
 
 
-NUM_MOE_CFGS = 9  # grouped configurations in csrc/gemm.hip (7, 8: run tiles)
+NUM_MOE_CFGS = 18  # grouped configurations in csrc/gemm.hip (7, 8: run tiles; 9-17: persistent)
 
 
 @pytest.mark.parametrize("shape", ["cfg3", "ragged"])
@@ -199,8 +199,9 @@ def test_grouped_run_tiles(B):
     backward scan for its first block crosses 64 blocks and its runs split
     into several tiles), others own 1-3 blocks (short runs), some none;
     N and the pair count are not tile multiples.  Bit-exact int32 and bf16
-    for every grouped configuration, gate_up-style (A row = pair // top_k)
-    and down-style (top_k 1, routed weight)."""
+    for the run-tile and persistent configurations (whose item lists cut
+    the long runs into chunks and skip padding fragments), gate_up-style
+    (A row = pair // top_k) and down-style (top_k 1, routed weight)."""
     from minisgl_amd.kernel import lib as mw8lib
 
     announce(f"grouped run tiles B={B}")
@@ -231,7 +232,7 @@ def test_grouped_run_tiles(B):
                 q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
                 routed=routed, return_acc=True,
             )
-            for cfg in (-1, 0, 7, 8):
+            for cfg in (-1, 0, 7, 8, *range(9, 18)):
                 announce(f"run tiles B={B} gemm{which} cfg={cfg}")
                 lib.mw8_set_tuning(-1, -1, cfg)
                 out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
