@@ -524,6 +524,63 @@ void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hi
   else launch_grouped_epi<kEpiI32>(g, blocks, bm, st);
 }
 
+void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
+
+// 16-row alignment blocks on the LDS DMA ring (decode3 core, gathered rows).
+template <int WAVES, int D, int EPI>
+void launch_grouped_ring(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  constexpr int kLds = DecodeRing<1, WAVES, D>::kLds;
+  auto kern = decode3_gemm_kernel<1, WAVES, D, EPI, SortedRows>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((g.N + 15) / 16), blocks), dim3(64 * WAVES), kLds,
+                     st, g);
+}
+
+template <int EPI>
+void launch_grouped_ring_cfg(int cfg, const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  switch (cfg) {
+    case 1: launch_grouped_ring<1, 4, EPI>(g, blocks, st); break;
+    case 2: launch_grouped_ring<1, 3, EPI>(g, blocks, st); break;
+    case 3: launch_grouped_ring<2, 4, EPI>(g, blocks, st); break;
+    case 4: launch_grouped_ring<2, 3, EPI>(g, blocks, st); break;
+    case 5: launch_grouped_ring<4, 3, EPI>(g, blocks, st); break;
+    default: launch_grouped_ring<1, 6, EPI>(g, blocks, st); break;
+  }
+}
+
+// 16-row alignment blocks (decode MoE): moe_cfg 0 the register-streaming
+// core with the block's tokens gathered in LDS (K <= 4080), 1-6 the LDS DMA
+// ring with (waves, ring depth) = (1,4), (1,3), (2,4), (2,3), (4,3), (1,6).
+// Measured on MI355X at config 3 (whole layer): 16 tokens 120 us (cfg 0)
+// -> 107 us (cfg 2), 64 tokens 156 -> 145 us; at 256 tokens the 64-row
+// tiles win (167 us against 210 for cfg 2 over 16-row blocks).
+int default_stream_cfg(const GemmArgs& g) {
+  (void)g;
+  return 2;
+}
+
+bool grouped_stream_fits(int64_t K) {
+  const int64_t ldl = ((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
+  return 16 * ldl <= 65536;
+}
+
+void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {
+  int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  if (cfg < 0 || cfg > 6) cfg = default_stream_cfg(g);
+  if (cfg == 0 && grouped_stream_fits(g.K)) {
+    launch_grouped_stream(g, blocks, epi, st);
+    return;
+  }
+  if (cfg == 0) cfg = 1;
+  if (epi == kEpiBf16) launch_grouped_ring_cfg<kEpiBf16>(cfg, g, blocks, st);
+  else launch_grouped_ring_cfg<kEpiI32>(cfg, g, blocks, st);
+}
+
 void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {
   const int ldl = static_cast<int>(((g.K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16);
   const size_t lds = static_cast<size_t>(16) * ldl;

@@ -1265,16 +1265,32 @@ struct RingDrain<D, OPS, D> {
   __device__ __forceinline__ static void run(F&) {}
 };
 
-template <int TG, int WAVES, int D, int EPI>
+// Grouped use (SortedRows, 16-row alignment blocks, TG = 1): grid y is the
+// alignment block; its expert's weights stream through the ring, the
+// token rows are gathered through sorted_ids (padding rows read zeros), and
+// the epilogue scatters to pair rows with the routed weight.
+template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kAcc = TG * 4;
   constexpr int kOps = 4 + 4 * TG;  // vector memory ops per stage (DMA + token loads)
   static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
+  static_assert(!Rows::kGrouped || (TG == 1 && !Rows::kRuns), "grouped rows: one 16-row block");
   extern __shared__ __align__(16) unsigned char ring[];
   __shared__ int32_t red[kAcc][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int8_t* W = g.W;
+  const float* sw = g.sw;
+  int64_t m0 = 0;  // grouped: first sorted position of the alignment block
+  if constexpr (Rows::kGrouped) {
+    m0 = static_cast<int64_t>(blockIdx.y) * 16;
+    if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
+    const int e = g.expert_ids[blockIdx.y];
+    if (e < 0 || e >= g.num_experts) return;
+    W += static_cast<int64_t>(e) * g.N * g.K;
+    sw += static_cast<int64_t>(e) * g.N;
+  }
   for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
@@ -1286,7 +1302,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   // weight DMA: instruction j of a stage fills LDS rows 4j .. 4j+3; lane l
   // fills row 4j + l/16, chunk l%16 from global chunk (l%16) ^ row
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      scalar_ptr(const_cast<int8_t*>(g.W + n0 * g.K)), 0,
+      scalar_ptr(const_cast<int8_t*>(W + n0 * g.K)), 0,
       static_cast<int>(rows * g.K), kBufferFlags);
   uint32_t w_off[4];
 #pragma unroll
@@ -1303,8 +1319,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   bool mok[TG];
 #pragma unroll
   for (int tg = 0; tg < TG; ++tg) {
-    const int64_t m = 16 * tg + r16;
-    mok[tg] = m < g.M;
+    int64_t m;
+    if constexpr (Rows::kGrouped) {
+      const int32_t p = g.sorted_ids[m0 + r16];
+      mok[tg] = p < g.num_valid;
+      m = p / g.top_k;
+    } else {
+      m = 16 * tg + r16;
+      mok[tg] = m < g.M;
+    }
     xrow[tg] = reinterpret_cast<uint64_t>(g.A + (mok[tg] ? m : 0) * g.lda);
   }
   v4i xr[D][4][TG];  // token chunks of the stages in flight, per ring slot
@@ -1372,13 +1395,27 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     const int j = e >> 6, l = e & 63;
     const int tg = j / 4, v = j & 3;
     const int64_t n = n0 + 4 * (l >> 4) + v;
-    const int64_t m = 16 * tg + (l & 15);
-    if (n >= g.N || m >= g.M) continue;
+    if (n >= g.N) continue;
+    int64_t orow, arow;
+    float routed = 1.0f;
+    if constexpr (Rows::kGrouped) {
+      const int32_t p = g.sorted_ids[m0 + (l & 15)];
+      if (p >= g.num_valid) continue;
+      orow = p;
+      arow = p / g.top_k;
+      if (g.topk_w) routed = g.topk_w[p];
+    } else {
+      orow = 16 * tg + (l & 15);
+      arow = orow;
+      if (orow >= g.M) continue;
+    }
     const int32_t a = red[j][l];
     if constexpr (EPI == kEpiBf16)
-      static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
+      static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
+          epi_bf16(a, g.sa[arow], sw[n], Rows::kGrouped ? nullptr : g.bias, n, routed,
+                   Rows::kGrouped && g.topk_w != nullptr);
     else
-      static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
+      static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }

@@ -6,7 +6,7 @@
 namespace mw8 {
 
 void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
-void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
+void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
 
 namespace {
 
@@ -357,10 +357,7 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   g.align_bsz = bsz;
   if (bsz == 16) {
-    const int64_t ldl = ((K + kStreamStep - 1) / kStreamStep) * kStreamStep + 16;
-    MW8_REQUIRE(16 * ldl <= 65536, kErrShape, "moe_gemm: K=%lld too large for the 16-row path",
-                (long long)K);
-    launch_grouped_stream(g, static_cast<unsigned>(blocks), epi, st);
+    launch_grouped_small(g, static_cast<unsigned>(blocks), epi, st);
   } else {
     launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);
   }

@@ -192,6 +192,64 @@ def test_grouped_every_tile_config(shape):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
+NUM_SMALL_CFGS = 7  # 16-row block configurations in csrc/gemm.hip (0: register streaming, 1-6: DMA ring)
+
+
+@pytest.mark.parametrize("shape", ["cfg3", "ragged", "longk"])
+def test_grouped_small_blocks_every_config(shape):
+    """16-row alignment blocks (the decode regime) through every small-block
+    configuration: the register-streaming core (cfg 0, K <= 4080) and the
+    LDS DMA ring with gathered token rows (1-6), gate_up-style and
+    down-style, bit-exact against the oracle.  The ragged case has K and N
+    off the 256 / 16 grids; the long-K case (K = 4160) exceeds the
+    streaming core's LDS panel, so cfg 0 runs the ring as well."""
+    from minisgl_amd.kernel import lib as mw8lib
+
+    lib = mw8lib.load()
+    if shape == "cfg3":
+        c = moe_case(16, seed=16)
+        M, k = 16, 8
+        logits = c["logits"]
+        gen = torch.Generator().manual_seed(98)
+        act2 = torch.randn(M * k, c["w2"].shape[2], generator=gen).to(torch.bfloat16)
+        cases = [(1, c["hidden"], c["w1"], c["s_w1"]), (2, act2, c["w2"], c["s_w2"])]
+    elif shape == "ragged":
+        M, k = 50, 2
+        logits, W, SW, act = _ragged_expert_case(11, M=M, k=k, E=8, N=200, K=336)
+        cases = [(1, act[:M], W, SW), (2, act, W, SW)]
+    else:
+        M, k = 12, 2
+        logits, W, SW, act = _ragged_expert_case(12, M=M, k=k, E=6, N=96, K=4160)
+        cases = [(1, act[:M], W, SW), (2, act, W, SW)]
+    E = cases[0][2].shape[0]
+    w_ref, ids_ref = orc.topk_softmax(f32(logits), k, True)
+    ids = torch.from_numpy(ids_ref).to(DEV)
+    tw = torch.from_numpy(w_ref).to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, 16, E)
+    try:
+        for which, act, W, SW in cases:
+            q, s = quant_per_token(act.to(DEV))
+            top_k, routed = (k, None) if which == 1 else (1, tw)
+            Wd, SWd = W.to(DEV), SW.to(DEV)
+            N = W.shape[1]
+            y_ref, acc_ref = orc.grouped_gemm_w8a8(
+                q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
+                routed=None if routed is None else w_ref, return_acc=True,
+            )
+            for cfg in range(-1, NUM_SMALL_CFGS):
+                announce(f"grouped small {shape} gemm{which} cfg={cfg}")
+                lib.mw8_set_tuning(-1, -1, cfg)
+                out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
+                fused_moe_kernel_w8a8(q, s, Wd, SWd, out, tw, sorted_ids, expert_ids, npp,
+                                      routed is not None, top_k, 16, M * k)
+                acc = fused_moe_kernel_w8a8_i32(q, Wd, sorted_ids, expert_ids, npp, top_k, 16, M * k)
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
+                assert bf16_bits_equal(out, y_ref).all(), f"cfg {cfg}"
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+
+
 @pytest.mark.parametrize("B", [64, 128])
 def test_grouped_run_tiles(B):
     """Run tiles (one tile over up to 256 / B consecutive alignment blocks
