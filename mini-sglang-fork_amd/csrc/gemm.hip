@@ -176,6 +176,7 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 256, true, 64, 2},   // 23: 8 waves (2x4), 3 stages
     {64, 256, true, 128, 1},   // 24: 4 waves (1x4), 4 stages
     {64, 128, true, 128, 1},   // 25: 4 waves (1x4), 4 stages
+    {256, 256, true, 64, 1},   // 26: 8 waves (4x2), 4 stages
 };
 constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
@@ -327,6 +328,7 @@ void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     case 23: launch_tile3<128, 256, 64, 2, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 24: launch_tile3<64, 256, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 25: launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 26: launch_tile3<256, 256, 64, 4, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
   if (split) {
@@ -444,7 +446,8 @@ void launch_grouped_persist(const GemmArgs& g, hipStream_t st) {
 // 128 rows on the 8-wave 256-wide ring (K % 128 == 0), 9-12 the persistent
 // item walk with 256x256, 128x256, 256x128 and 128x128 tiles (K % 128 == 0),
 // 13 as 9 with chunk items, 14-17 4-wave 128x256 / 256x128 tiles on
-// 64-byte K stages, two blocks per CU (expert items, chunk items).
+// 64-byte K stages, two blocks per CU (expert items, chunk items), 18-19
+// 4-wave 128x128 tiles with chunk items, three / four blocks per CU.
 //
 // Automatic choice, measured on MI355X at config 3 (E 128, top-8, H 2048,
 // I 768; whole layer): with at least 32 pairs per expert on average the
@@ -483,7 +486,9 @@ void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t 
       case 14: launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, false, 2>(g, st); break;
       case 15: launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, true, 2>(g, st); break;
       case 16: launch_grouped_persist<256, 128, 64, 2, 2, 3, EPI, false, 2>(g, st); break;
-      default: launch_grouped_persist<256, 128, 64, 2, 2, 3, EPI, true, 2>(g, st); break;
+      case 17: launch_grouped_persist<256, 128, 64, 2, 2, 3, EPI, true, 2>(g, st); break;
+      case 18: launch_grouped_persist<128, 128, 64, 2, 2, 3, EPI, true, 3>(g, st); break;
+      default: launch_grouped_persist<128, 128, 64, 2, 2, 2, EPI, true, 4>(g, st); break;
     }
     return;
   }

@@ -356,12 +356,20 @@ bool dispatch_rows(int64_t nvec, int64_t rows, hipStream_t st, Args... args) {
   };
   using I64 = std::integral_constant<int, 64>;
   using I256 = std::integral_constant<int, 256>;
+  // few lanes idle on the last vector (K = 5120: 640 of 768 slots, K =
+  // 17408: 2176 of 2304).  Rows past 512 vectors use 256-thread rows: one
+  // wave per 5120-wide row measured slower for the fused RMSNorm.
   if (nvec <= 64 * 1) return go(I64{}, std::integral_constant<int, 1>{});
   if (nvec <= 64 * 2) return go(I64{}, std::integral_constant<int, 2>{});
+  if (nvec <= 64 * 3) return go(I64{}, std::integral_constant<int, 3>{});
   if (nvec <= 64 * 4) return go(I64{}, std::integral_constant<int, 4>{});
+  if (nvec <= 64 * 6) return go(I64{}, std::integral_constant<int, 6>{});
   if (nvec <= 64 * 8) return go(I64{}, std::integral_constant<int, 8>{});
+  if (nvec <= 256 * 3) return go(I256{}, std::integral_constant<int, 3>{});
   if (nvec <= 256 * 4) return go(I256{}, std::integral_constant<int, 4>{});
+  if (nvec <= 256 * 6) return go(I256{}, std::integral_constant<int, 6>{});
   if (nvec <= 256 * 8) return go(I256{}, std::integral_constant<int, 8>{});
+  if (nvec <= 256 * 9) return go(I256{}, std::integral_constant<int, 9>{});
   if (nvec <= 256 * 12) return go(I256{}, std::integral_constant<int, 12>{});
   if (nvec <= 256 * 16) return go(I256{}, std::integral_constant<int, 16>{});
   return false;

@@ -133,7 +133,7 @@ def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
     return logits, W, SW, act
 
 
-NUM_MOE_CFGS = 18  # grouped configurations in csrc/gemm.hip (7, 8: run tiles; 9-17: persistent)
+NUM_MOE_CFGS = 20  # grouped configurations in csrc/gemm.hip (7, 8: run tiles; 9-19: persistent)
 
 
 @pytest.mark.parametrize("shape", ["cfg3", "ragged"])
@@ -290,7 +290,7 @@ def test_grouped_run_tiles(B):
                 q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
                 routed=routed, return_acc=True,
             )
-            for cfg in (-1, 0, 7, 8, *range(9, 18)):
+            for cfg in (-1, 0, 7, 8, *range(9, 20)):
                 announce(f"run tiles B={B} gemm{which} cfg={cfg}")
                 lib.mw8_set_tuning(-1, -1, cfg)
                 out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)

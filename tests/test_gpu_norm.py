@@ -26,7 +26,8 @@ def _case(M, H, seed, outliers=True):
     return x.to(torch.bfloat16), res, w
 
 
-@pytest.mark.parametrize("M,H", [(1, 5120), (7, 5120), (300, 2048), (2080, 5120), (33, 1032), (5, 40), (3, 17408)])
+@pytest.mark.parametrize("M,H", [(1, 5120), (7, 5120), (300, 2048), (2080, 5120), (33, 1032), (5, 40), (3, 17408),
+                                 (4, 1280), (2, 6144)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_rmsnorm_quant_bit_exact(M, H, with_res):
     announce(f"rmsnorm_quant M={M} H={H} res={with_res}")
