@@ -186,7 +186,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
-    ap.add_argument("--mode", choices=["bench", "gemm", "copy"], default="bench")
+    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "vendor"], default="bench",
+                    help="bench: the contract line; gemm / copy: one workload for rocprofv3 passes; "
+                         "vendor: this library against hipBLASLt int8 (torch._int_mm) at the config-1 "
+                         "shapes with M >= 512")
     ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
     ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
@@ -197,6 +200,8 @@ def main() -> int:
 
     import torch
 
+    if args.mode == "vendor":
+        return vendor_mode(args)
     if args.mode != "bench":
         return profile_mode(args)
 
@@ -396,6 +401,64 @@ def profile_mode(args) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"mode": "gemm", "M": M, "N": N, "K": K, "reps": args.reps,
                       "algorithmic_bytes": gemm_bytes(M, N, K)}))
+    return 0
+
+
+def vendor_mode(args) -> int:
+    """The platform's own int8 GEMM (hipBLASLt through torch._int_mm: int8 x
+    int8 -> int32, no epilogue) beside this library's int32 and bf16-epilogue
+    GEMMs, same shapes, same rotating weight copies, graph-timed."""
+    import torch
+
+    from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES, SWEEP_M
+    from minisgl_amd.kernel import gemm_w8a8, gemm_w8a8_i32, gemm_workspace, quant_per_token
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    stream = torch.cuda.Stream()
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            fn(0)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(n):
+                    fn(i)
+            g.replay()
+            torch.cuda.synchronize()
+            best = float("inf")
+            for _ in range(3):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+                e1.synchronize()
+                best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+        del g
+        return best
+
+    for M in [m for m in SWEEP_M if m >= 512]:
+        for name, K, N in QWEN3_14B_SHAPES:
+            ncopy = max(args.reps, -(-args.copy_mb * 10**6 // (N * K)))
+            ws = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev) for _ in range(ncopy)]
+            sw = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
+            q, s = quant_per_token(torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16))
+            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            gemm_workspace(M, N, K, dev)  # reserve before capture
+            ops = 2.0 * M * N * K
+            rec = {"mode": "vendor", "shape": name, "M": M, "N": N, "K": K}
+            for key, fn in (
+                ("hipblaslt_int_mm_i32", lambda i: torch._int_mm(q, ws[i % ncopy].t())),
+                ("mw8_i32", lambda i: gemm_w8a8_i32(q, ws[i % ncopy])),
+                ("mw8_bf16", lambda i: gemm_w8a8(q, s, ws[i % ncopy], sw, out=y)),
+            ):
+                us = timed(fn, args.reps)
+                rec[key] = {"us": round(us, 1), "tops": round(ops / us / 1e6, 1)}
+            print(json.dumps(rec), flush=True)
+            del ws
+            torch.cuda.empty_cache()
     return 0
 
 
