@@ -388,6 +388,10 @@ __device__ __forceinline__ T* scalar_ptr(T* p) {
 
 // Buffer-resource word 3 for raw byte-addressed buffers on gfx9-family parts.
 constexpr int kBufferFlags = 0x00020000;
+// Cache policy of a streamed weight DMA: non-temporal (decode GEMM weights
+// are read once).  Measured on MI355X against the default policy: gate_up
+// M=1 32.5 -> 30.0 us, qkv / o_proj / down M=1 4-8% faster.
+constexpr int kStreamAux = 2;
 
 // Workgroup barrier without the release/acquire fence of __syncthreads()
 // (which would force vmcnt(0) and drain the prefetch ring).  The empty asm
@@ -1338,7 +1342,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     const int soff = st < s_end ? st * 256 : 0x7fff0000;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0,
+                                               kStreamAux);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
