@@ -665,7 +665,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         const int64_t n = n0 + ch * 8;
         if (orow >= 0 && n < g.N) {
           const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
-          *reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n) = d;
+          // non-temporal: the output is written once (gate_up M=8192 1405 -> 1377 us)
+          __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n));
         }
       }
       return;

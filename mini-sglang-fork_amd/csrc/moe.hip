@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void moe_sum_reduce_kernel(const uint16_t* __r
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
   for (int i = 0; i < k; ++i) {
-    const v4i raw = *reinterpret_cast<const v4i*>(in + (t * k + i) * H + h);
+    const v4i raw = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(in + (t * k + i) * H + h));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t u = static_cast<uint32_t>(raw[j]);
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void moe_sum_reduce_kernel(const uint16_t* __r
   for (int j = 0; j < 4; ++j)
     o[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[2 * j])) |
                             (static_cast<uint32_t>(f32_to_bf16(acc[2 * j + 1])) << 16));
-  *reinterpret_cast<v4i*>(out + t * H + h) = o;
+  __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(out + t * H + h));
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
