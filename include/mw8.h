@@ -95,9 +95,11 @@ int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, fl
 
 /*
  * Tile-configuration override, process-wide: decode_cfg indexes the dense
- * small-M (M <= 64) configurations, tile_cfg the dense large-M ones, moe_cfg
- * the grouped (fused-MoE) tile configurations for block sizes 64 and 128;
- * -1 restores the automatic choice.  Results do not depend on the
+ * decode-core configurations (forcing one keeps M <= 64 on the decode
+ * core), tile_cfg the dense tile-core ones (forcing one takes M > 32 to the
+ * tile core), moe_cfg the grouped (fused-MoE) configurations (tile or
+ * persistent configurations for block sizes 64 and 128, small-block ones
+ * for block size 16); -1 restores the automatic choice.  Results do not depend on the
  * configuration (exact integer accumulation).  Tuning hook; no reference
  * counterpart.
  */
@@ -105,11 +107,12 @@ void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 
 /*
  * Bytes of workspace mw8_gemm_w8a8_* uses for (M, N, K): the int32 partial
- * tiles of the tail-wave K split (M > 64, K % 128 == 0, 256 x 256 tiles:
- * the r = T mod 256 tiles of the last partial wave, all T when T < 256, are
- * cut into sp = min(256 / r, K / 128, 16) K ranges when sp >= 2; each range
- * writes one 256 x 256 int32 tile, summed in range order by a second
- * kernel on the same stream).  0 when no split applies.  A NULL or smaller
+ * tiles of the tile core's K split (for the tiling the call will choose,
+ * including a mw8_set_tuning override: with T tiles and S = 256 x resident
+ * blocks per CU, the r = T mod S tiles of the last partial wave, all T when
+ * T < S, are cut into sp = min(S / r, K / BK, 16) K ranges when sp >= 2;
+ * each range writes one BM x BN int32 tile, summed in range order by a
+ * second kernel on the same stream).  0 when no split applies.  A NULL or smaller
  * workspace is not an error: the GEMM then runs every tile whole (same
  * result, slower).  The workspace holds no state between calls; calls that
  * share one must be ordered (one stream).  No reference counterpart.
@@ -167,7 +170,7 @@ int mw8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int32_t slo
  *   out[p, :] = epilogue(A[p / top_k] . W[e]^T, sa[p / top_k], sw[e], routed = topk_w[p])
  * where e = expert_ids[r / block_size]; topk_w may be NULL (no routed
  * multiply).  A int8 [*, K], W int8 [E, N, K], sw fp32 [E, N], out bf16
- * [num_valid, N].  block_size in {16, 64, 128}.
+ * [num_valid, N].  block_size in {16, 32, 64, 128}.
  * Replaces fused_moe_kernel_triton / fused_moe_kernel
  * (python/minisgl/kernel/moe_impl.py:6-62, python/minisgl/kernel/triton/fused_moe.py:50-193).
  */

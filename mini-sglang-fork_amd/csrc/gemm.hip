@@ -531,11 +531,12 @@ void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hi
 
 void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
 
-// 16-row alignment blocks on the LDS DMA ring (decode3 core, gathered rows).
-template <int WAVES, int D, int EPI>
+// 16- or 32-row alignment blocks on the LDS DMA ring (decode3 core,
+// gathered rows; TG token groups of 16).
+template <int WAVES, int D, int EPI, int TG = 1>
 void launch_grouped_ring(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  constexpr int kLds = DecodeRing<1, WAVES, D>::kLds;
-  auto kern = decode3_gemm_kernel<1, WAVES, D, EPI, SortedRows>;
+  constexpr int kLds = DecodeRing<TG, WAVES, D>::kLds;
+  auto kern = decode3_gemm_kernel<TG, WAVES, D, EPI, SortedRows>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -575,6 +576,11 @@ bool grouped_stream_fits(int64_t K) {
 }
 
 void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {
+  if (g.align_bsz == 32) {  // two token groups per block (ring depth 3)
+    if (epi == kEpiBf16) launch_grouped_ring<1, 3, kEpiBf16, 2>(g, blocks, st);
+    else launch_grouped_ring<1, 3, kEpiI32, 2>(g, blocks, st);
+    return;
+  }
   int cfg = g_moe_cfg.load(std::memory_order_relaxed);
   if (cfg < 0 || cfg > 6) cfg = default_stream_cfg(g);
   if (cfg == 0 && grouped_stream_fits(g.K)) {

@@ -1270,8 +1270,8 @@ struct RingDrain<D, OPS, D> {
   __device__ __forceinline__ static void run(F&) {}
 };
 
-// Grouped use (SortedRows, 16-row alignment blocks, TG = 1): grid y is the
-// alignment block; its expert's weights stream through the ring, the
+// Grouped use (SortedRows, alignment blocks of 16 * TG rows): grid y is
+// the alignment block; its expert's weights stream through the ring, the
 // token rows are gathered through sorted_ids (padding rows read zeros), and
 // the epilogue scatters to pair rows with the routed weight.
 template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows>
@@ -1280,7 +1280,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   constexpr int kAcc = TG * 4;
   constexpr int kOps = 4 + 4 * TG;  // vector memory ops per stage (DMA + token loads)
   static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
-  static_assert(!Rows::kGrouped || (TG == 1 && !Rows::kRuns), "grouped rows: one 16-row block");
+  static_assert(!Rows::kRuns, "grouped rows: one alignment block per block");
   extern __shared__ __align__(16) unsigned char ring[];
   __shared__ int32_t red[kAcc][64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1289,7 +1289,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   const float* sw = g.sw;
   int64_t m0 = 0;  // grouped: first sorted position of the alignment block
   if constexpr (Rows::kGrouped) {
-    m0 = static_cast<int64_t>(blockIdx.y) * 16;
+    m0 = static_cast<int64_t>(blockIdx.y) * (16 * TG);
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
     const int e = g.expert_ids[blockIdx.y];
     if (e < 0 || e >= g.num_experts) return;
@@ -1326,7 +1326,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   for (int tg = 0; tg < TG; ++tg) {
     int64_t m;
     if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + r16];
+      const int32_t p = g.sorted_ids[m0 + 16 * tg + r16];
       mok[tg] = p < g.num_valid;
       m = p / g.top_k;
     } else {
@@ -1405,7 +1405,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     int64_t orow, arow;
     float routed = 1.0f;
     if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + (l & 15)];
+      const int32_t p = g.sorted_ids[m0 + 16 * tg + (l & 15)];
       if (p >= g.num_valid) continue;
       orow = p;
       arow = p / g.top_k;

@@ -337,8 +337,8 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   MW8_REQUIRE(N > 0 && K > 0 && K % 16 == 0 && K <= (1ll << 17), kErrShape,
               "moe_gemm: need K %% 16 == 0 and K <= 131072 (N=%lld K=%lld)", (long long)N,
               (long long)K);
-  MW8_REQUIRE(bsz == 16 || bsz == 64 || bsz == 128, kErrShape,
-              "moe_gemm: block size must be 16, 64 or 128 (got %d)", bsz);
+  MW8_REQUIRE(bsz == 16 || bsz == 32 || bsz == 64 || bsz == 128, kErrShape,
+              "moe_gemm: block size must be 16, 32, 64 or 128 (got %d)", bsz);
   MW8_REQUIRE(top_k >= 1 && E >= 1 && num_valid >= 0 && max_sorted >= 0, kErrShape,
               "moe_gemm: bad routing sizes");
   MW8_REQUIRE(aligned16(A) && aligned16(W), kErrAlign, "moe_gemm: A and W need 16-byte alignment");
@@ -356,7 +356,7 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   g.align_bsz = bsz;
-  if (bsz == 16) {
+  if (bsz <= 32) {
     launch_grouped_small(g, static_cast<unsigned>(blocks), epi, st);
   } else {
     launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);

@@ -118,10 +118,18 @@ def test_grouped_gemm(M, which):
     _grouped(moe_case(M, seed=M), M, 8, B, which)
 
 
-@pytest.mark.parametrize("B", [16, 128])
+@pytest.mark.parametrize("B", [16, 32, 128])
 def test_grouped_gemm_other_blocks(B):
     announce(f"grouped gemm B={B}")
     _grouped(moe_case(40, seed=40), 40, 8, B, 1)
+
+
+@pytest.mark.parametrize("which", [1, 2])
+def test_grouped_gemm_32_row_blocks(which):
+    """32-row alignment blocks (two token groups per ring block) at 256
+    tokens: ~16 pairs per expert, experts past 32 pairs span two blocks."""
+    announce(f"grouped gemm{which} B=32 M=256")
+    _grouped(moe_case(256, seed=7), 256, 8, 32, which)
 
 
 def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
