@@ -188,6 +188,25 @@ int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorte
                           mw8_stream_t stream);
 
 /*
+ * Small-batch MoE preparation in one launch: the router of
+ * mw8_topk_softmax (logits [M, E] -> topk_w fp32 / topk_ids int32 [M, topk]),
+ * the per-token quantization of the hidden rows of mw8_quant_per_token_bf16
+ * (hidden bf16 [M, H] -> q int8 [M, H], s fp32 [M]) and the alignment of
+ * mw8_moe_align_block_size over the selected ids (same outputs and buffer
+ * sizes), each bit-identical to its own entry point.  M * topk <= 1024,
+ * topk <= min(E, 64), E <= 1024, E <= slots <= 512, H % 8 == 0, hidden
+ * 16-byte and q 8-byte aligned.  Replaces, for decode batches, the
+ * sequence fused_topk (python/minisgl/moe/fused.py:9-28) ->
+ * moe_align_block_size (:31-89) of fused_experts_impl (:157-227) plus the
+ * activation quantization of the W8A8 grouped GEMM.
+ */
+int mw8_moe_prepare_small(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,
+                          int32_t renorm, const void* hidden, int64_t H, float* topk_w,
+                          int32_t* topk_ids, int8_t* q, float* s, int32_t slots, int32_t block_size,
+                          int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_pad,
+                          mw8_stream_t stream);
+
+/*
  * Slot sum: in bf16 [M, k, H] -> out bf16 [M, H], fp32 sum in slot order.
  * H % 8 == 0.  Replaces moe_sum_reduce_triton
  * (python/minisgl/kernel/moe_impl.py:65-98, python/minisgl/kernel/triton/fused_moe.py:5-47).

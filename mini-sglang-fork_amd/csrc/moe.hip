@@ -1,6 +1,8 @@
 // Fused-MoE building blocks (gfx950): router top-k softmax, expert
 // alignment (stable counting sort with block padding), grouped W8A8 GEMM
 // over expert segments, and the top-k slot sum.
+#include <type_traits>
+
 #include "gemm_kernels.h"
 
 namespace mw8 {
@@ -46,14 +48,13 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 // wins ties: a max over values, then a min over the indices holding it),
 // then the two renormalisations of the reference
 // (python/minisgl/moe/fused.py:22-24).
+// Token t on the calling wave; the selected ids also go to ids_copy[t * topk
+// + i] when ids_copy is given (the fused small-batch preparation).
 template <int VPL>
-__global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, int is_bf16,
-                                                           int64_t M, int E, int topk,
-                                                           int renorm, float* __restrict__ tw,
-                                                           int32_t* __restrict__ tid_out) {
+__device__ __forceinline__ void topk_token(const void* logits, int is_bf16, int64_t t, int E,
+                                           int topk, int renorm, float* __restrict__ tw,
+                                           int32_t* __restrict__ tid_out, int32_t* ids_copy) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= M) return;
   float v[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
@@ -103,7 +104,18 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, i
   if (lane < topk) {
     tw[t * topk + lane] = w_sel;
     tid_out[t * topk + lane] = id_sel;
+    if (ids_copy) ids_copy[t * topk + lane] = id_sel;
   }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const void* logits, int is_bf16,
+                                                           int64_t M, int E, int topk,
+                                                           int renorm, float* __restrict__ tw,
+                                                           int32_t* __restrict__ tid_out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;
+  topk_token<VPL>(logits, is_bf16, t, E, topk, renorm, tw, tid_out, nullptr);
 }
 
 // ------------------------------------------------------------ alignment
@@ -125,10 +137,11 @@ constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignMaxSlots = 512;
 
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+// Block `bid` of `nblk` (ids may live in global memory or in LDS).
+__device__ __forceinline__ void align_body(
     const int32_t* __restrict__ ids, int64_t numel, int slots, int bsz, int unroll,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks, int nbits) {
+    int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks, int nbits, int bid, int nblk) {
   __shared__ int wpos[kAlignWaves][kAlignMaxSlots];  // counts, then start positions
   __shared__ int before[kAlignMaxSlots];
   __shared__ int after[kAlignMaxSlots];
@@ -137,7 +150,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   __shared__ int wave_tot[kAlignWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t wave_span = 64 * static_cast<int64_t>(unroll);
-  const int64_t lo = static_cast<int64_t>(blockIdx.x) * kAlignWaves * wave_span;
+  const int64_t lo = static_cast<int64_t>(bid) * kAlignWaves * wave_span;
   const int64_t hi = lo + kAlignWaves * wave_span < numel ? lo + kAlignWaves * wave_span : numel;
 
   for (int j = tid; j < kAlignWaves * kAlignMaxSlots; j += kAlignThreads) (&wpos[0][0])[j] = 0;
@@ -183,8 +196,8 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     if (w < wave) base += wave_tot[w];
     total += wave_tot[w];
   }
-  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kAlignThreads;
-  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kAlignThreads + tid;
+  const int64_t gstride = static_cast<int64_t>(nblk) * kAlignThreads;
+  const int64_t gtid = static_cast<int64_t>(bid) * kAlignThreads + tid;
   if (tid < slots) {
     const int start = base + x - padded;
     off[tid] = start;
@@ -230,6 +243,73 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     if (valid && rank == 0) wpos[wave][ev] = pos + __popcll(m);
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int slots, int bsz, int unroll,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks, int nbits) {
+  align_body(ids, numel, slots, bsz, unroll, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits,
+             blockIdx.x, gridDim.x);
+}
+
+// ------------------------------------------------ small-batch preparation
+// One block does the router, the per-token quantization of the hidden rows
+// and the alignment (pairs <= 1024, one block of the alignment kernel's
+// own code with the ids in LDS): three launches of the decode MoE layer in
+// one.  Each part is the code of its own kernel, so the outputs are those
+// of topk_softmax, quant_per_token and moe_align_block_size bit for bit.
+constexpr int kPrepMaxPairs = kAlignThreads;
+
+// Row r of the hidden states quantized by the calling wave (two passes over
+// the L2-resident row: integer absmax of sign-cleared bf16 bits, then the
+// quantizer's own closed form per element).
+__device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ x, int64_t K,
+                                               int8_t* __restrict__ q, float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nvec = K >> 3;
+  uint32_t m = 0;
+  for (int64_t v = lane; v < nvec; v += 64) {
+    const v4i w = *reinterpret_cast<const v4i*>(x + 8 * v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = static_cast<uint32_t>(w[j]);
+      const uint32_t lo = u & 0x7FFFu, hi = (u >> 16) & 0x7FFFu;
+      m = lo > m ? lo : m;
+      m = hi > m ? hi : m;
+    }
+  }
+  m = wave_reduce_u32(m, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
+  for (int64_t v = lane; v < nvec; v += 64) {
+    const v4i w = *reinterpret_cast<const v4i*>(x + 8 * v);
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = static_cast<uint32_t>(w[j]);
+      const int a = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(u & 0xFFFFu)), rs));
+      const int b = static_cast<int>(quant_div_rne(bf16_to_f32(static_cast<uint16_t>(u >> 16)), rs));
+      packed[j >> 1] |= ((static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8)) << (16 * (j & 1));
+    }
+    *reinterpret_cast<uint2*>(q + 8 * v) = make_uint2(packed[0], packed[1]);
+  }
+  if (lane == 0) *s = rs.s;
+}
+
+template <int VPL>
+__global__ __launch_bounds__(kAlignThreads) void moe_prepare_kernel(
+    const void* logits, int is_bf16, int64_t M, int E, int topk, int renorm,
+    const uint16_t* __restrict__ hidden, int64_t H, float* __restrict__ tw, int32_t* __restrict__ tid_out,
+    int8_t* __restrict__ q, float* __restrict__ s, int slots, int bsz, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ npp, int64_t max_padded, int64_t max_blocks,
+    int nbits) {
+  __shared__ int32_t ids[kPrepMaxPairs];
+  const int wave = threadIdx.x >> 6;
+  for (int64_t t = wave; t < M; t += kAlignWaves)
+    topk_token<VPL>(logits, is_bf16, t, E, topk, renorm, tw, tid_out, ids);
+  for (int64_t r = wave; r < M; r += kAlignWaves) quant_row_wave(hidden + r * H, H, q + r * H, s + r);
+  __syncthreads();  // the ids of every token are in LDS
+  align_body(ids, M * topk, slots, bsz, 1, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits, 0, 1);
 }
 
 // ------------------------------------------------------------ slot sum
@@ -314,6 +394,42 @@ int moe_align_block_size(const int32_t* topk_ids, int64_t numel, int slots, int 
   hipLaunchKernelGGL(moe_align_kernel, dim3(grid), dim3(kAlignThreads), 0, st, topk_ids, numel,
                      slots, bsz, unroll, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits);
   return check_launch("moe_align");
+}
+
+int moe_prepare_small(const void* logits, int is_bf16, int64_t M, int E, int topk, int renorm,
+                      const void* hidden, int64_t H, float* topk_w, int32_t* topk_ids, int8_t* q,
+                      float* s, int slots, int bsz, int32_t* sorted_ids, int32_t* expert_ids,
+                      int32_t* npp, hipStream_t st) {
+  MW8_REQUIRE(logits && hidden && topk_w && topk_ids && q && s && sorted_ids && expert_ids && npp, kErrArg,
+              "moe_prepare_small: null pointer");
+  MW8_REQUIRE(M > 0 && E > 0 && E <= 1024 && topk > 0 && topk <= E && topk <= 64 &&
+                  M * topk <= kPrepMaxPairs,
+              kErrShape, "moe_prepare_small: need 0 < M * topk <= %d, topk <= min(E, 64), E <= 1024 "
+              "(M=%lld E=%d topk=%d)", kPrepMaxPairs, (long long)M, E, topk);
+  MW8_REQUIRE(slots >= E && slots <= kAlignMaxSlots && bsz > 0 && bsz <= 4096, kErrShape,
+              "moe_prepare_small: need E <= slots <= 512 and 0 < block <= 4096 (slots=%d block=%d)",
+              slots, bsz);
+  MW8_REQUIRE(H > 0 && H % 8 == 0, kErrShape, "moe_prepare_small: need H %% 8 == 0 (H=%lld)", (long long)H);
+  MW8_REQUIRE(aligned16(hidden) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0, kErrAlign,
+              "moe_prepare_small: hidden needs 16-byte and q 8-byte alignment");
+  const int64_t numel = M * topk;
+  const int64_t max_padded = moe_align_max_padded(numel, slots, bsz);
+  const int64_t max_blocks = (max_padded + bsz - 1) / bsz;
+  int nbits = 1;
+  while ((1 << nbits) < slots) ++nbits;
+  const int vpl = (E + 63) / 64;
+  auto go = [&](auto vpl_c) {
+    constexpr int V = decltype(vpl_c)::value;
+    hipLaunchKernelGGL((moe_prepare_kernel<V>), dim3(1), dim3(kAlignThreads), 0, st, logits, is_bf16, M, E,
+                       topk, renorm, static_cast<const uint16_t*>(hidden), H, topk_w, topk_ids, q, s, slots,
+                       bsz, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits);
+  };
+  if (vpl <= 1) go(std::integral_constant<int, 1>{});
+  else if (vpl <= 2) go(std::integral_constant<int, 2>{});
+  else if (vpl <= 4) go(std::integral_constant<int, 4>{});
+  else if (vpl <= 8) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 16>{});
+  return check_launch("moe_prepare_small");
 }
 
 int moe_sum_reduce_bf16(const void* in, int64_t M, int k, int64_t H, void* out, hipStream_t st) {

@@ -7,6 +7,7 @@ from .ops import (
     gemm_w8a8_i32,
     gemm_workspace,
     moe_align_block_size,
+    moe_prepare_small,
     moe_sum_reduce,
     quant_per_token,
     rmsnorm_quant,
@@ -23,6 +24,7 @@ __all__ = [
     "gemm_w8a8_i32",
     "gemm_workspace",
     "moe_align_block_size",
+    "moe_prepare_small",
     "moe_sum_reduce",
     "quant_per_token",
     "rmsnorm_quant",

@@ -250,6 +250,53 @@ def moe_align_block_size(
     return sorted_ids, expert_ids, num_tokens_post_pad
 
 
+PREPARE_MAX_PAIRS = 1024  # M * topk bound of the one-block preparation
+
+
+def moe_prepare_small(
+    gating_output: torch.Tensor,
+    hidden_states: torch.Tensor,
+    topk: int,
+    renormalize: bool,
+    block_size: int,
+    num_experts: int,
+) -> Tuple[torch.Tensor, ...]:
+    """Router + alignment + hidden-state quantization in one launch (decode
+    batches, M * topk <= 1024).  Returns (topk_weights, topk_ids, sorted_ids,
+    expert_ids, num_tokens_post_pad, q, s), each bit-identical to
+    topk_softmax, moe_align_block_size and quant_per_token."""
+    _on_gpu(gating_output, hidden_states)
+    g, h = gating_output, hidden_states
+    _need(g.dim() == 2 and g.is_contiguous(), "gating_output: [M, E] contiguous")
+    _need(g.dtype in (torch.bfloat16, torch.float32), "gating_output: bf16 or fp32")
+    _need(h.dtype == torch.bfloat16 and h.dim() == 2 and h.is_contiguous(), "hidden_states: bf16 [M, H] contiguous")
+    M, E = g.shape
+    _need(h.shape[0] == M, "hidden_states / gating_output token counts differ")
+    _need(E == num_experts, "gating_output width != num_experts")
+    H = h.shape[1]
+    lib = load()
+    dev = g.device
+    slots = num_experts + 1
+    numel = M * topk
+    max_padded = int(lib.mw8_moe_align_max_padded(numel, slots, block_size))
+    max_blocks = -(-max_padded // block_size)
+    w = torch.empty((M, topk), dtype=torch.float32, device=dev)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=dev)
+    q = torch.empty((M, H), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    sorted_ids = torch.empty((max_padded,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((max_blocks,), dtype=torch.int32, device=dev)
+    npp = torch.empty((1,), dtype=torch.int32, device=dev)
+    check(
+        lib.mw8_moe_prepare_small(
+            _ptr(g), int(g.dtype == torch.bfloat16), M, E, topk, int(renormalize), _ptr(h), H,
+            _ptr(w), _ptr(ids), _ptr(q), _ptr(s), slots, block_size, _ptr(sorted_ids),
+            _ptr(expert_ids), _ptr(npp), _stream(g),
+        )
+    )
+    return w, ids, sorted_ids, expert_ids, npp, q, s
+
+
 def fused_moe_kernel_w8a8(
     A: torch.Tensor,
     A_scale: torch.Tensor,

@@ -93,9 +93,19 @@ def test_argument_errors_return_codes(lib):
     assert lib.mw8_act_and_mul_quant_bf16(FAKE_A, 4, 32, 7, FAKE_B, FAKE_C, None, None) == E["MW8_ERR_ARG"]
     assert lib.mw8_topk_softmax(FAKE_A, 1, 4, 8, 9, 1, FAKE_B, FAKE_C, None) == E["MW8_ERR_SHAPE"]
     assert lib.mw8_moe_align_block_size(FAKE_A, 16, 600, 16, FAKE_B, FAKE_C, FAKE_A, None) == E["MW8_ERR_SHAPE"]
-    rc = lib.mw8_moe_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 64, 1, 16, 64, 64, 4, 32,
+    rc = lib.mw8_moe_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 64, 1, 16, 64, 64, 4, 48,
                                    FAKE_A, None)
-    assert rc == E["MW8_ERR_SHAPE"]  # block size 32 unsupported
+    assert rc == E["MW8_ERR_SHAPE"]  # block size 48 unsupported
+    # small-batch preparation: M * topk > 1024, H % 8 != 0, slots < E, a null output
+    prep = lib.mw8_moe_prepare_small
+    assert prep(FAKE_A, 1, 129, 16, 8, 1, FAKE_B, 64, FAKE_C, FAKE_C, FAKE_C, FAKE_C, 17, 16,
+                FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    assert prep(FAKE_A, 1, 4, 16, 8, 1, FAKE_B, 60, FAKE_C, FAKE_C, FAKE_C, FAKE_C, 17, 16,
+                FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    assert prep(FAKE_A, 1, 4, 16, 8, 1, FAKE_B, 64, FAKE_C, FAKE_C, FAKE_C, FAKE_C, 15, 16,
+                FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    assert prep(FAKE_A, 1, 4, 16, 8, 1, FAKE_B, 64, None, FAKE_C, FAKE_C, FAKE_C, 17, 16,
+                FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_ARG"]
     assert lib.mw8_moe_sum_reduce_bf16(FAKE_A, 4, 8, 12, FAKE_B, None) == E["MW8_ERR_SHAPE"]
     # empty problems are no-ops
     assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0

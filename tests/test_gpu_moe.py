@@ -16,6 +16,7 @@ from minisgl_amd.kernel import (
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
+    moe_prepare_small,
     moe_sum_reduce,
     quant_per_token,
     topk_softmax,
@@ -79,6 +80,45 @@ def test_topk_softmax(M, E, k, renorm):
     w_ref, ids_ref = orc.topk_softmax(f32(logits), k, renorm)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize(
+    "M,E,k,renorm,H",
+    [(1, 128, 8, True, 2048), (16, 128, 8, True, 2048), (64, 128, 8, True, 2048), (5, 64, 2, False, 40),
+     (33, 300, 6, True, 1032), (128, 8, 8, True, 16), (3, 511, 1, False, 5120)],
+)
+def test_moe_prepare_small_equals_the_separate_kernels(M, E, k, renorm, H):
+    """The one-launch decode preparation (router + hidden quantization +
+    alignment) against topk_softmax, quant_per_token and
+    moe_align_block_size run separately: every output bit-identical (the
+    whole sorted_ids / expert_ids buffers included), at the pair bound
+    (128 x 8 = 1024), E up to 511 and odd hidden widths."""
+    announce(f"moe prepare M={M} E={E} k={k} H={H}")
+    gen = torch.Generator().manual_seed(M * 7 + E + k)
+    logits = torch.randn(M, E, generator=gen).to(torch.bfloat16).to(DEV)
+    hidden = (torch.randn(M, H, generator=gen) * 3).to(torch.bfloat16).to(DEV)
+    tw, ids, sorted_ids, expert_ids, npp, q, s = moe_prepare_small(logits, hidden, k, renorm, 16, E)
+    tw2, ids2 = topk_softmax(logits, k, renorm)
+    q2, s2 = quant_per_token(hidden)
+    sorted2, expert2, npp2 = moe_align_block_size(ids2, 16, E)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2)
+    assert torch.equal(tw.view(torch.int32), tw2.view(torch.int32))
+    assert torch.equal(q, q2) and torch.equal(s.view(torch.int32), s2.view(torch.int32))
+    assert int(npp.item()) == int(npp2.item())
+    assert torch.equal(sorted_ids, sorted2) and torch.equal(expert_ids, expert2)
+    s_ref, e_ref, n_ref = orc.moe_align_block_size(ids.cpu().numpy(), 16, E)
+    assert int(npp.item()) == n_ref
+    np.testing.assert_array_equal(sorted_ids.cpu().numpy(), s_ref)
+
+
+def test_moe_prepare_small_rejects_too_many_pairs():
+    from minisgl_amd.kernel import MW8Error
+
+    logits = torch.zeros(129, 16, dtype=torch.bfloat16, device=DEV)
+    hidden = torch.zeros(129, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(MW8Error):
+        moe_prepare_small(logits, hidden, 8, True, 16, 16)
 
 
 def _grouped(c, M, k, B, which):
@@ -326,7 +366,7 @@ def test_sum_reduce():
     assert o2.float().abs().max().item() == 0.0
 
 
-@pytest.mark.parametrize("M", [16, 256, 4096])
+@pytest.mark.parametrize("M", [4, 16, 256, 4096])
 def test_moe_layer_stagewise(M):
     """Whole W8A8 MoE layer through MoELayer -> ctx.moe_backend ("fused_w8a8"),
     checked stage by stage on the GPU's own intermediate values."""
