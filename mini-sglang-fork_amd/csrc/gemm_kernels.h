@@ -443,6 +443,18 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // scalar offset): the A view starts at the tile's first row (row 0 for
   // gathered rows), the W view at the tile's first weight row.  The host
   // keeps every offset below 2^31 (gemm_common / moe_gemm_w8a8 checks).
+  // Grouped bf16 epilogue: the tile's row metadata (pair index, activation
+  // scale, routed weight) is fetched at the start and kept in LDS, so the
+  // dependent loads overlap the main loop instead of stalling the epilogue.
+  constexpr bool kMeta = Rows::kGrouped && EPI == kEpiBf16;
+  static_assert(!kMeta || BM <= 64 * kWaves, "one metadata row per thread");
+  __shared__ int32_t meta_p[kMeta ? BM : 1];
+  __shared__ float meta_sa[kMeta ? BM : 1], meta_rt[kMeta ? BM : 1];
+  int32_t meta_pv = 0;
+  float meta_sav = 0.0f, meta_rtv = 1.0f;
+  if constexpr (kMeta) {
+    if (tid < BM) meta_pv = tid < rows_valid ? g.sorted_ids[m0 + tid] : static_cast<int32_t>(g.num_valid);
+  }
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
@@ -463,6 +475,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       arow = m0 + row < g.M ? m0 + row : g.M - 1;
     }
     a_doff[j] = a_live ? static_cast<uint32_t>((arow - a_base_row) * g.lda + 16 * c) : 0x80000000u;
+  }
+  if constexpr (kMeta) {
+    if (tid < BM && meta_pv < g.num_valid) {
+      meta_sav = g.sa[meta_pv / g.top_k];
+      if (g.topk_w) meta_rtv = g.topk_w[meta_pv];
+    }
   }
 #pragma unroll
   for (int j = 0; j < kLB; ++j) {
@@ -538,6 +556,14 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 #pragma unroll
   for (int s = 0; s < NSTAGE; ++s)
     if (s < nk) issue(s);
+  if constexpr (kMeta) {
+    if (tid < BM) {  // visible to every wave after the barriers of the main loop
+      const bool ok = meta_pv < g.num_valid;
+      meta_p[tid] = ok ? meta_pv : -1;
+      meta_sa[tid] = ok ? meta_sav : 0.0f;
+      meta_rt[tid] = ok ? meta_rtv : 0.0f;
+    }
+  }
   wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
   raw_barrier();
   read_frags(0, 0);
@@ -608,14 +634,10 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
           const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
           float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
           if constexpr (Rows::kGrouped) {
-            const int32_t p0 = r0 < rows_valid ? g.sorted_ids[m0 + r0] : static_cast<int32_t>(g.num_valid);
-            const int32_t p1 = r0 + 1 < rows_valid ? g.sorted_ids[m0 + r0 + 1] : static_cast<int32_t>(g.num_valid);
-            sa0 = p0 < g.num_valid ? g.sa[p0 / g.top_k] : 0.0f;
-            sa1 = p1 < g.num_valid ? g.sa[p1 / g.top_k] : 0.0f;
-            if (g.topk_w) {
-              rt0 = p0 < g.num_valid ? g.topk_w[p0] : 0.0f;
-              rt1 = p1 < g.num_valid ? g.topk_w[p1] : 0.0f;
-            }
+            sa0 = meta_sa[r0];
+            sa1 = meta_sa[r0 + 1];
+            rt0 = meta_rt[r0];
+            rt1 = meta_rt[r0 + 1];
           } else {
             const int64_t ma = m0 + r0 < g.M ? m0 + r0 : g.M - 1;
             const int64_t mb = m0 + r0 + 1 < g.M ? m0 + r0 + 1 : g.M - 1;
@@ -657,8 +679,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
         int64_t orow;
         if constexpr (Rows::kGrouped) {
-          const int32_t p = r < rows_valid ? g.sorted_ids[m0 + r] : static_cast<int32_t>(g.num_valid);
-          orow = p < g.num_valid ? p : -1;
+          orow = meta_p[r];
         } else {
           orow = m0 + r < g.M ? m0 + r : -1;
         }
