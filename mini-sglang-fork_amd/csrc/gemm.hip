@@ -174,7 +174,7 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 128, true, 128, 2},  // 21: 4 waves (2x2), 2 stages
     {64, 256, true, 64, 2},    // 22: 4 waves (1x4), 3 stages
     {128, 256, true, 64, 2},   // 23: 8 waves (2x4), 3 stages
-    {64, 256, true, 128, 1},   // 24: 4 waves (1x4), 4 stages
+    {64, 256, true, 64, 1},    // 24: 4 waves (1x4), 4 stages
     {64, 128, true, 128, 1},   // 25: 4 waves (1x4), 4 stages
     {256, 256, true, 64, 1},   // 26: 8 waves (4x2), 4 stages
 };
@@ -326,7 +326,7 @@ void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     case 21: launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 22: launch_tile3<64, 256, 64, 1, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 23: launch_tile3<128, 256, 64, 2, 4, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 24: launch_tile3<64, 256, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 24: launch_tile3<64, 256, 64, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 25: launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 26: launch_tile3<256, 256, 64, 4, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;

@@ -386,6 +386,8 @@ __device__ __forceinline__ T* scalar_ptr(T* p) {
   return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+constexpr int kPersistMaxSlots = 512;  // expert slots of the persistent grouped walk (E < this)
+
 // Buffer-resource word 3 for raw byte-addressed buffers on gfx9-family parts.
 constexpr int kBufferFlags = 0x00020000;
 // Cache policy of a streamed weight DMA: non-temporal (decode GEMM weights
@@ -446,14 +448,23 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // Grouped bf16 epilogue: the tile's row metadata (pair index, activation
   // scale, routed weight) is fetched at the start and kept in LDS, so the
   // dependent loads overlap the main loop instead of stalling the epilogue.
+  // The dense bf16 epilogue keeps its row scales in the same table, and
+  // both keep the tile's column scales (and bias) in LDS.
   constexpr bool kMeta = Rows::kGrouped && EPI == kEpiBf16;
-  static_assert(!kMeta || BM <= 64 * kWaves, "one metadata row per thread");
+  constexpr bool kMetaSa = EPI == kEpiBf16;
+  static_assert(!kMetaSa || (BM <= 64 * kWaves && BN <= 64 * kWaves), "one metadata row per thread");
   __shared__ int32_t meta_p[kMeta ? BM : 1];
-  __shared__ float meta_sa[kMeta ? BM : 1], meta_rt[kMeta ? BM : 1];
+  __shared__ float meta_sa[kMetaSa ? BM : 1], meta_rt[kMeta ? BM : 1];
+  __shared__ float meta_sw[kMetaSa ? BN : 1], meta_bias[kMetaSa && !Rows::kGrouped ? BN : 1];
+  // ring + these tables + the persistent walk's run tables fit in the CU's 160 KB
+  static_assert(NSTAGE * kStage + 4 * (3 * BM + 2 * BN) + 4 * (2 * kPersistMaxSlots + 2 + 16) <= 163840,
+                "LDS budget");
   int32_t meta_pv = 0;
-  float meta_sav = 0.0f, meta_rtv = 1.0f;
+  float meta_sav = 0.0f, meta_rtv = 1.0f, meta_swv = 0.0f, meta_bv = 0.0f;
   if constexpr (kMeta) {
     if (tid < BM) meta_pv = tid < rows_valid ? g.sorted_ids[m0 + tid] : static_cast<int32_t>(g.num_valid);
+  } else if constexpr (kMetaSa) {
+    if (tid < BM) meta_sav = g.sa[m0 + tid < g.M ? m0 + tid : g.M - 1];
   }
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -480,6 +491,13 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
     if (tid < BM && meta_pv < g.num_valid) {
       meta_sav = g.sa[meta_pv / g.top_k];
       if (g.topk_w) meta_rtv = g.topk_w[meta_pv];
+    }
+  }
+  if constexpr (kMetaSa) {
+    if (tid < BN) {
+      const int64_t nc = n0 + tid < g.N ? n0 + tid : g.N - 1;
+      meta_swv = sw[nc];
+      if (!Rows::kGrouped && g.bias) meta_bv = bf16_to_f32(g.bias[nc]);
     }
   }
 #pragma unroll
@@ -563,6 +581,14 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       meta_sa[tid] = ok ? meta_sav : 0.0f;
       meta_rt[tid] = ok ? meta_rtv : 0.0f;
     }
+  } else if constexpr (kMetaSa) {
+    if (tid < BM) meta_sa[tid] = meta_sav;
+  }
+  if constexpr (kMetaSa) {
+    if (tid < BN) {
+      meta_sw[tid] = meta_swv;
+      if constexpr (!Rows::kGrouped) meta_bias[tid] = meta_bv;
+    }
   }
   wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
   raw_barrier();
@@ -639,22 +665,20 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
             rt0 = meta_rt[r0];
             rt1 = meta_rt[r0 + 1];
           } else {
-            const int64_t ma = m0 + r0 < g.M ? m0 + r0 : g.M - 1;
-            const int64_t mb = m0 + r0 + 1 < g.M ? m0 + r0 + 1 : g.M - 1;
-            sa0 = g.sa[ma];
-            sa1 = g.sa[mb];
+            sa0 = meta_sa[r0];
+            sa1 = meta_sa[r0 + 1];
           }
 #pragma unroll
           for (int j = 0; j < kFN; ++j) {
             const int c = wn * kWaveN + 32 * j + frow;
-            const int64_t n = n0 + c < g.N ? n0 + c : g.N - 1;
-            const float swv = sw[n];
+            const float swv = meta_sw[c];
             float t0 = epi_scale(acc[i][j][v0], sa0, swv);
             float t1 = epi_scale(acc[i][j][v0 + 1], sa1, swv);
-            if (!Rows::kGrouped && g.bias) {
-              const float b = bf16_to_f32(g.bias[n]);
-              t0 = t0 + b;
-              t1 = t1 + b;
+            if constexpr (!Rows::kGrouped) {
+              if (g.bias) {
+                t0 = t0 + meta_bias[c];
+                t1 = t1 + meta_bias[c];
+              }
             }
             if (Rows::kGrouped && g.topk_w) {
               t0 = t0 * rt0;
@@ -829,7 +853,6 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
 // (block b runs on XCD b % 8) deal one contiguous range of them, so all
 // column tiles of an expert share its gathered rows in one L2.  Each block
 // walks its items with a static stride: no queue, no inter-block waiting.
-constexpr int kPersistMaxSlots = 512;  // expert slots (moe_gemm checks E < this)
 
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & 63;
