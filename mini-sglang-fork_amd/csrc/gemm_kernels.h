@@ -1400,6 +1400,47 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       }
     }
   };
+  // epilogue operands of this thread's output elements, fetched before the
+  // stream so that the loads (dependent ones for gathered rows) overlap it
+  // (output row, or -1; activation scale; column scale; routed weight or
+  // bias).  Gathered rows only: their loads depend on sorted_ids (measured on
+  // MI355X: 16-token MoE layer 96.8 -> 93.9 us); for dense rows the extra
+  // registers cost 1-2% at 8-32 tokens and the epilogue loads directly.
+  constexpr bool kPre = Rows::kGrouped;
+  constexpr int kEpiPerThread = (kAcc * 64 + 64 * WAVES - 1) / (64 * WAVES);
+  int32_t e_orow[kPre ? kEpiPerThread : 1];
+  float e_sa[kPre ? kEpiPerThread : 1], e_sw[kPre ? kEpiPerThread : 1], e_x[kPre ? kEpiPerThread : 1];
+#pragma unroll
+  for (int u = 0; u < (kPre ? kEpiPerThread : 0); ++u) {
+    const int e = tid + u * 64 * WAVES;
+    const int j = e >> 6, l = e & 63;
+    const int tg = j / 4, v = j & 3;
+    const int64_t n = n0 + 4 * (l >> 4) + v;
+    e_orow[u] = -1;
+    e_sa[u] = 0.0f;
+    e_sw[u] = 0.0f;
+    e_x[u] = 0.0f;
+    if (e >= kAcc * 64 || n >= g.N) continue;
+    int32_t arow;
+    if constexpr (Rows::kGrouped) {
+      const int32_t p = g.sorted_ids[m0 + 16 * tg + (l & 15)];
+      if (p >= g.num_valid) continue;
+      e_orow[u] = p;
+      arow = p / g.top_k;
+      if (g.topk_w) e_x[u] = g.topk_w[p];
+    } else {
+      const int32_t m = 16 * tg + (l & 15);
+      if (m >= g.M) continue;
+      e_orow[u] = m;
+      arow = m;
+      if (g.bias) e_x[u] = bf16_to_f32(g.bias[n]);
+    }
+    if constexpr (EPI == kEpiBf16) {
+      e_sa[u] = g.sa[arow];
+      e_sw[u] = sw[n];
+    }
+  }
+
   v4i acc[TG];
 #pragma unroll
   for (int tg = 0; tg < TG; ++tg) acc[tg] = v4i{0};
@@ -1441,31 +1482,37 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) atomicAdd(&red[tg * 4 + v][lane], acc[tg][v]);
   __syncthreads();
-  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) {
+#pragma unroll
+  for (int u = 0; u < kEpiPerThread; ++u) {
+    const int e = tid + u * 64 * WAVES;
+    if (e >= kAcc * 64) continue;
     const int j = e >> 6, l = e & 63;
-    const int tg = j / 4, v = j & 3;
+    const int v = j & 3;
     const int64_t n = n0 + 4 * (l >> 4) + v;
-    if (n >= g.N) continue;
-    int64_t orow, arow;
-    float routed = 1.0f;
-    if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + 16 * tg + (l & 15)];
-      if (p >= g.num_valid) continue;
-      orow = p;
-      arow = p / g.top_k;
-      if (g.topk_w) routed = g.topk_w[p];
-    } else {
-      orow = 16 * tg + (l & 15);
-      arow = orow;
-      if (orow >= g.M) continue;
+    if constexpr (!kPre) {  // dense rows: operands loaded here
+      const int32_t m = 16 * (j / 4) + (l & 15);
+      if (n >= g.N || m >= g.M) continue;
+      e_orow[0] = m;
+      if constexpr (EPI == kEpiBf16) {
+        e_sa[0] = g.sa[m];
+        e_sw[0] = sw[n];
+        e_x[0] = g.bias ? bf16_to_f32(g.bias[n]) : 0.0f;
+      }
     }
+    const int ui = kPre ? u : 0;
+    if (e_orow[ui] < 0) continue;
     const int32_t a = red[j][l];
-    if constexpr (EPI == kEpiBf16)
-      static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
-          epi_bf16(a, g.sa[arow], sw[n], Rows::kGrouped ? nullptr : g.bias, n, routed,
-                   Rows::kGrouped && g.topk_w != nullptr);
-    else
-      static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
+    if constexpr (EPI == kEpiBf16) {
+      float t = epi_scale(a, e_sa[ui], e_sw[ui]);
+      if constexpr (Rows::kGrouped) {
+        if (g.topk_w) t = t * e_x[ui];
+      } else {
+        if (g.bias) t = t + e_x[ui];
+      }
+      static_cast<uint16_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = f32_to_bf16(t);
+    } else {
+      static_cast<int32_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = a;
+    }
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
