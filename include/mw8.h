@@ -180,6 +180,24 @@ int mw8_moe_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, co
                            int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
                            int32_t block_size, void* out, mw8_stream_t stream);
 
+/*
+ * Gate|up grouped GEMM with the gated activation fused into its epilogue:
+ * W int8 [E, N = 2I, K] holds the gate rows then the up rows of each expert;
+ * out bf16 [num_valid, I] receives act(g) * u with g, u the bf16 outputs the
+ * grouped GEMM above would write for columns i and I + i (act 0: silu with
+ * the hardware reciprocal, 1: erf-gelu), rounded to bf16 -- bit-identical to
+ * mw8_moe_gemm_w8a8_bf16 followed by mw8_act_and_mul_quant_bf16's
+ * activation output.  block_size 64 or 128, N % 16 == 0, K % 64 == 0,
+ * E < 512, out 16-byte aligned.  Replaces fused_moe_kernel (GEMM1) +
+ * silu_and_mul (python/minisgl/moe/fused.py:195-210,
+ * python/minisgl/layers/activation.py:9-12) for prefill batches.
+ */
+int mw8_moe_gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const int32_t* sorted_ids, const int32_t* expert_ids,
+                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
+                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
+                               int32_t block_size, int32_t act, void* out, mw8_stream_t stream);
+
 /* Same, raw int32 accumulators out [num_valid, N] (parity hook; no reference counterpart). */
 int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorted_ids,
                           const int32_t* expert_ids, const int32_t* num_post_pad,

@@ -428,10 +428,11 @@ void launch_grouped_runs(const GemmArgs& g, unsigned blocks, hipStream_t st) {
 
 // Persistent grouped GEMM: 256 x per_cu blocks walk the (expert chunk,
 // column tile) items.
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems = false, int kPerCu = 1>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems = false, int kPerCu = 1,
+          int kAct = -1>
 void launch_grouped_persist(const GemmArgs& g, hipStream_t st) {
   constexpr int kLds = NSTAGE * (BM + BN) * BK;
-  auto kern = grouped_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, kChunkItems, kPerCu>;
+  auto kern = grouped_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, kChunkItems, kPerCu, kAct>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -522,6 +523,13 @@ void launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t 
       default: launch_grouped3<128, 128, 64, 2, 2, 4, EPI>(g, blocks, st); break;
     }
   }
+}
+
+// Gate|up GEMM with the gated activation fused (persistent chunk walk, the
+// cfg-15 tiling): out [rows, N/2] = act(gate) * up, bf16.
+void launch_grouped_act(const GemmArgs& g, int act, hipStream_t st) {
+  if (act == 0) launch_grouped_persist<128, 256, 64, 2, 2, 3, kEpiBf16, true, 2, 0>(g, st);
+  else launch_grouped_persist<128, 256, 64, 2, 2, 3, kEpiBf16, true, 2, 1>(g, st);
 }
 
 void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st) {

@@ -414,7 +414,12 @@ struct TileJob {
   int64_t split_unit; // >= 0: write the int32 partial tile part[split_unit]
 };
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
+// kAct >= 0 (grouped bf16, staged epilogue): the tile's B rows are the gate
+// rows [n0, n0 + BN/2) and the up rows N/2 + [n0, n0 + BN/2) of a gate|up
+// weight [N = 2I, K]; the epilogue writes act = bf16(act_fn(g) * u) for act
+// columns [n0, n0 + BN/2) of an [rows, I] output (g.ldo = I), g and u the
+// bf16-rounded GEMM outputs, as the separate activation kernel computes it.
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1>
 __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds, const TileJob& job) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kWaves = WM * WN;
@@ -469,8 +474,23 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
+  static_assert(kAct < 0 || (Rows::kGrouped && EPI == kEpiBf16 && BM * BN * 2 <= NSTAGE * kStage && BN >= 128),
+                "fused activation: grouped bf16 with the staged epilogue (the host sets staged_out)");
+  constexpr int kHalfN = BN / 2;
+  const int64_t half = g.N / 2;  // kAct: rows of each of the gate and up halves
+  // weight row of tile row r (kAct: gate rows then the matching up rows)
+  auto w_row_of = [&](int r) -> int64_t {
+    if constexpr (kAct >= 0) {
+      const int64_t a = n0 + (r < kHalfN ? r : r - kHalfN);
+      const int64_t ac = a < half ? a : half - 1;
+      return r < kHalfN ? ac : half + ac;
+    } else {
+      return n0 + r < g.N ? n0 + r : g.N - 1;
+    }
+  };
+  const int64_t w_base_row = kAct >= 0 ? 0 : n0;
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      scalar_ptr(const_cast<int8_t*>(W + n0 * g.K)), 0, 0x7fffffff, kBufferFlags);
+      scalar_ptr(const_cast<int8_t*>(W + w_base_row * g.K)), 0, 0x7fffffff, kBufferFlags);
   uint32_t a_doff[kLA], w_doff[kLB];
 #pragma unroll
   for (int j = 0; j < kLA; ++j) {
@@ -495,7 +515,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   }
   if constexpr (kMetaSa) {
     if (tid < BN) {
-      const int64_t nc = n0 + tid < g.N ? n0 + tid : g.N - 1;
+      const int64_t nc = w_row_of(tid);
       meta_swv = sw[nc];
       if (!Rows::kGrouped && g.bias) meta_bv = bf16_to_f32(g.bias[nc]);
     }
@@ -504,8 +524,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   for (int j = 0; j < kLB; ++j) {
     const int unit = (j * kWaves + wave) * 64 + lane, row = unit / kChunks;
     const int c = (unit % kChunks) ^ swz_f<BK>(row);
-    const int64_t wrow = n0 + row < g.N ? n0 + row : g.N - 1;
-    w_doff[j] = static_cast<uint32_t>((wrow - n0) * g.K + 16 * c);
+    const int64_t wrow = w_row_of(row);
+    w_doff[j] = static_cast<uint32_t>((wrow - w_base_row) * g.K + 16 * c);
   }
   const int nk = kt_end - kt_begin;
   auto issue = [&](int kt) {
@@ -696,8 +716,34 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         }
       }
       __syncthreads();
-      constexpr int kChunksRow = BN / 8;
       constexpr int kThreads = 64 * kWaves;
+      if constexpr (kAct >= 0) {  // act chunk ch of row r: gate chunk ch, up chunk ch + BN/16
+        constexpr int kActChunks = BN / 16;
+#pragma unroll
+        for (int q0 = 0; q0 < BM * kActChunks; q0 += kThreads) {
+          const int q = q0 + tid, r = q / kActChunks, ch = q % kActChunks;
+          const int64_t orow = meta_p[r];
+          const int64_t n = n0 + ch * 8;
+          if (orow >= 0 && n < half) {
+            const v4i gv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
+            const v4i uv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (((ch + kActChunks) ^ sf(r)) << 4));
+            v4i o;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const uint32_t gw = static_cast<uint32_t>(gv[w]), uw = static_cast<uint32_t>(uv[w]);
+              const float a0 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw & 0xFFFFu))) *
+                               bf16_to_f32(static_cast<uint16_t>(uw & 0xFFFFu));
+              const float a1 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw >> 16))) *
+                               bf16_to_f32(static_cast<uint16_t>(uw >> 16));
+              o[w] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(a0)) |
+                                      (static_cast<uint32_t>(f32_to_bf16(a1)) << 16));
+            }
+            __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n));
+          }
+        }
+        return;
+      }
+      constexpr int kChunksRow = BN / 8;
 #pragma unroll
       for (int q0 = 0; q0 < BM * kChunksRow; q0 += kThreads) {
         const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
@@ -864,7 +910,8 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems, int kPerCu>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems, int kPerCu,
+          int kAct = -1>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(kPerCu * WM * WN / 4)))
 void grouped_persist_kernel(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -905,7 +952,10 @@ void grouped_persist_kernel(GemmArgs g) {
   }
   if (tid == 0) act_base[E] = carry;
   __syncthreads();
-  const int tn = static_cast<int>((g.N + BN - 1) / BN);
+  // column tiles: BN output columns, or BN / 2 activation columns (kAct)
+  constexpr int kTileCols = kAct >= 0 ? BN / 2 : BN;
+  const int64_t out_cols = kAct >= 0 ? g.N / 2 : g.N;
+  const int tn = static_cast<int>((out_cols + kTileCols - 1) / kTileCols);
   const int total = carry * tn;
 
   // this block's share: XCD x deals items [begin, begin + count)
@@ -939,7 +989,7 @@ void grouped_persist_kernel(GemmArgs g) {
     for (int c = c_lo; c < c_hi; ++c) {
       const int c0 = b_first + c * nblocks / nch, c1 = b_first + (c + 1) * nblocks / nch;
       TileJob job{static_cast<int64_t>(c0) * ab,
-                  static_cast<int64_t>(n_tile) * BN,
+                  static_cast<int64_t>(n_tile) * kTileCols,
                   g.W + static_cast<int64_t>(e) * g.N * g.K,
                   g.sw + static_cast<int64_t>(e) * g.N,
                   0,
@@ -947,7 +997,7 @@ void grouped_persist_kernel(GemmArgs g) {
                   (c1 - c0) * ab,
                   -1};
       __syncthreads();  // the previous tile's LDS staging has been read out
-      tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows>(g, lds, job);
+      tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows, kAct>(g, lds, job);
     }
   }
 #endif  // __HIP_DEVICE_COMPILE__

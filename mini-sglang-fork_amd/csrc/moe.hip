@@ -9,6 +9,7 @@ namespace mw8 {
 
 void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
 void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
+void launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
 
 namespace {
 
@@ -478,6 +479,35 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
     launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);
   }
   return check_launch("moe_gemm");
+}
+
+int moe_gemm_act_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* npp,
+                      int64_t max_sorted, const float* topk_w, int top_k, int64_t num_valid,
+                      int64_t N, int64_t K, int E, int bsz, int act, void* out, hipStream_t st) {
+  MW8_REQUIRE(A && sa && W && sw && sorted_ids && expert_ids && npp && out, kErrArg,
+              "moe_gemm_act: null pointer");
+  MW8_REQUIRE(act == 0 || act == 1, kErrArg, "moe_gemm_act: act must be 0 (silu) or 1 (gelu)");
+  MW8_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0 && K <= (1ll << 17), kErrShape,
+              "moe_gemm_act: need N %% 16 == 0, K %% 64 == 0 and K <= 131072 (N=%lld K=%lld)",
+              (long long)N, (long long)K);
+  MW8_REQUIRE(bsz == 64 || bsz == 128, kErrShape, "moe_gemm_act: block size must be 64 or 128 (got %d)", bsz);
+  MW8_REQUIRE(top_k >= 1 && E >= 1 && E < kPersistMaxSlots && num_valid >= 0 && max_sorted >= 0, kErrShape,
+              "moe_gemm_act: bad routing sizes (E=%d)", E);
+  MW8_REQUIRE(aligned16(A) && aligned16(W) && aligned16(out), kErrAlign,
+              "moe_gemm_act: A, W and out need 16-byte alignment");
+  MW8_REQUIRE((num_valid / top_k + 1) * K < (1ll << 31) && N * K < (1ll << 31), kErrShape,
+              "moe_gemm_act: operands exceed 32-bit buffer offsets");
+  if (max_sorted / bsz == 0) return kOk;
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
+  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N / 2;
+  g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
+  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.staged_out = 1;
+  g.align_bsz = bsz;
+  launch_grouped_act(g, act, st);
+  return check_launch("moe_gemm_act");
 }
 
 }  // namespace mw8

@@ -112,6 +112,15 @@ enum Status : int {
 };
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Gated activation of the MoE / MLP intermediate (shared by the activation
+// kernel and the GEMM epilogue that fuses it): silu with the hardware
+// reciprocal, or erf-gelu.
+template <int ACT>
+__device__ __forceinline__ float act_fn(float g) {
+  if constexpr (ACT == 0) return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));  // silu
+  else return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f));  // gelu (erf)
+}
+
 }  // namespace mw8
 
 #define MW8_REQUIRE(cond, code, ...)                     \

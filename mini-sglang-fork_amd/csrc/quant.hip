@@ -173,11 +173,6 @@ __global__ __launch_bounds__(kBlock) void quant_rows_generic_kernel(
 // silu(g) = g * 1 / (1 + e^-g) with the hardware reciprocal (1 ulp) in place
 // of an IEEE division: the activation is rounded to bf16 next and is held
 // to a tolerance, while the requant that follows is exact on its bf16 value.
-template <int ACT>
-__device__ __forceinline__ float act_fn(float g) {
-  if constexpr (ACT == 0) return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));  // silu
-  else return 0.5f * g * (1.0f + erff(g * 0.70710678118654752440f));  // gelu (erf)
-}
 
 template <int TPR, int VPT, int ACT>
 __global__ __launch_bounds__(kBlock) void act_rows_kernel(

@@ -1,6 +1,7 @@
 from .lib import MW8Error, load
 from .ops import (
     act_and_mul_quant,
+    fused_moe_kernel_act_w8a8,
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     gemm_w8a8,
@@ -18,6 +19,7 @@ __all__ = [
     "MW8Error",
     "load",
     "act_and_mul_quant",
+    "fused_moe_kernel_act_w8a8",
     "fused_moe_kernel_w8a8",
     "fused_moe_kernel_w8a8_i32",
     "gemm_w8a8",

@@ -337,6 +337,44 @@ def fused_moe_kernel_w8a8(
     )
 
 
+def fused_moe_kernel_act_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    C: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    top_k: int,
+    block_size: int,
+    num_valid_tokens: int,
+    activation: str = "silu",
+    topk_weights: Optional[torch.Tensor] = None,
+) -> None:
+    """Gate|up grouped GEMM with the gated activation in its epilogue
+    (``topk_weights`` given: the routed weight multiplies g and u first):
+    C bf16 [M*k, N/2] = act(gate) * up, bit-identical to
+    fused_moe_kernel_w8a8 into [M*k, N] followed by act_and_mul_quant's
+    activation (64/128-row blocks, persistent walk)."""
+    _on_gpu(A, A_scale, B, B_scale, C)
+    _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [T, K]")
+    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
+    E, N, K = B.shape
+    _need(A.shape[1] == K, "A/B K mismatch")
+    _need(A_scale.dtype == torch.float32 and A_scale.shape == (A.shape[0],), "A_scale: fp32 [T]")
+    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
+    _need(C.dtype == torch.bfloat16 and C.is_contiguous() and C.numel() == num_valid_tokens * (N // 2), "C: bf16 [M*k, N/2]")
+    _need(activation in ("silu", "gelu"), "activation: silu or gelu")
+    check(
+        load().mw8_moe_gemm_act_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids), _ptr(expert_ids),
+            _ptr(num_tokens_post_padded), sorted_token_ids.shape[0], _ptr(topk_weights), top_k,
+            num_valid_tokens, N, K, E, block_size, 0 if activation == "silu" else 1, _ptr(C), _stream(A),
+        )
+    )
+
+
 def fused_moe_kernel_w8a8_i32(
     A: torch.Tensor,
     B: torch.Tensor,

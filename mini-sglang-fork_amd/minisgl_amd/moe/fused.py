@@ -10,7 +10,8 @@ w2 int8 [E, H, I]:
    ``pair // top_k``)
 4. GEMM1 -> bf16 cache [M*k, N]; routed weight only if
    ``apply_router_weight_on_input`` (reference :201)
-5. activation + requant -> int8 [M*k, I] + fp32 scales
+5. activation + requant -> int8 [M*k, I] + fp32 scales (prefill batches:
+   the activation runs in GEMM1's epilogue, then the plain quantizer)
 6. GEMM2 (top_k = 1) -> bf16 cache [M*k, H], routed weight otherwise (:217)
 7. slot sum, written into ``hidden_states`` in place (:175, :223-226)
 
@@ -29,6 +30,7 @@ import torch
 
 from ..kernel import (
     act_and_mul_quant,
+    fused_moe_kernel_act_w8a8,
     fused_moe_kernel_w8a8,
     moe_align_block_size,
     moe_prepare_small,
@@ -109,17 +111,28 @@ def _experts_from_routing(
     hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, sorted_ids, expert_ids,
     num_post_pad, k, bsz, activation, apply_router_weight_on_input,
 ) -> torch.Tensor:
-    """Steps 4-7: GEMM1, activation + requant, GEMM2, slot sum in place."""
+    """Steps 4-7: GEMM1, activation + requant, GEMM2, slot sum in place.
+    Prefill batches (>= 32 pairs per expert, 64/128-row blocks) run the
+    activation in GEMM1's epilogue, writing [M*k, I] instead of [M*k, 2I];
+    the values are the same bit for bit."""
     M, H = hidden_states.shape
-    N = w1.shape[1]
+    E, N, K = w1.shape
     # one buffer backs both bf16 caches, as in the reference (:157-172)
     cache = torch.empty(M * k * max(N, H), dtype=torch.bfloat16, device=hidden_states.device)
-    cache1 = cache[: M * k * N].view(M * k, N)
-    fused_moe_kernel_w8a8(
-        q_h, s_h, w1, w1_scale, cache1, topk_weights, sorted_ids, expert_ids, num_post_pad,
-        apply_router_weight_on_input, k, bsz, M * k,
-    )
-    q_a, s_a = act_and_mul_quant(cache1, activation)
+    if bsz in (64, 128) and M * k >= 32 * E and N % 16 == 0 and K % 64 == 0 and E < 512:
+        act = cache[: M * k * (N // 2)].view(M * k, N // 2)
+        fused_moe_kernel_act_w8a8(
+            q_h, s_h, w1, w1_scale, act, sorted_ids, expert_ids, num_post_pad, k, bsz, M * k,
+            activation, topk_weights if apply_router_weight_on_input else None,
+        )
+        q_a, s_a = quant_per_token(act)
+    else:
+        cache1 = cache[: M * k * N].view(M * k, N)
+        fused_moe_kernel_w8a8(
+            q_h, s_h, w1, w1_scale, cache1, topk_weights, sorted_ids, expert_ids, num_post_pad,
+            apply_router_weight_on_input, k, bsz, M * k,
+        )
+        q_a, s_a = act_and_mul_quant(cache1, activation)
     cache3 = cache[: M * k * H].view(M * k, H)
     fused_moe_kernel_w8a8(
         q_a, s_a, w2, w2_scale, cache3, topk_weights, sorted_ids, expert_ids, num_post_pad,

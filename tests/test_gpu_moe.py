@@ -13,6 +13,7 @@ from minisgl_amd.benchmark import moe_case
 from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
 from minisgl_amd.kernel import (
     act_and_mul_quant,
+    fused_moe_kernel_act_w8a8,
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
@@ -238,6 +239,41 @@ def test_grouped_every_tile_config(shape):
                     assert bf16_bits_equal(out, y_ref).all()
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
+
+
+@pytest.mark.parametrize("shape", ["cfg3", "ragged"])
+@pytest.mark.parametrize("B", [64, 128])
+def test_fused_activation_gemm_equals_gemm_then_activation(shape, B):
+    """GEMM1 with the gated activation in its epilogue against GEMM1 into the
+    [pairs, 2I] cache followed by the activation kernel: the [pairs, I]
+    activation bit-identical, for silu and gelu, with and without the routed
+    weight on the input side.  The ragged case has I = 168 (act tiles of
+    128 columns, the second one partial), skewed experts and K = 512."""
+    announce(f"fused act gemm {shape} B={B}")
+    if shape == "cfg3":
+        c = moe_case(512, seed=5)
+        M, k, W, SW, hidden, logits = 512, 8, c["w1"], c["s_w1"], c["hidden"], c["logits"]
+    else:
+        M, k = 700, 2
+        logits, W, SW, act_in = _ragged_expert_case(21, M=M, k=k, E=6, N=336, K=512)
+        hidden = act_in[:M]
+    E, N, K = W.shape
+    w_ref, ids_ref = orc.topk_softmax(f32(logits), k, True)
+    ids = torch.from_numpy(ids_ref).to(DEV)
+    tw = torch.from_numpy(w_ref).to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, E)
+    q, s = quant_per_token(hidden.to(DEV))
+    Wd, SWd = W.to(DEV), SW.to(DEV)
+    for act_name in ("silu", "gelu"):
+        for routed in (False, True):
+            c1 = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
+            fused_moe_kernel_w8a8(q, s, Wd, SWd, c1, tw, sorted_ids, expert_ids, npp, routed, k, B, M * k)
+            _, _, a_ref = act_and_mul_quant(c1, act_name, return_act=True)
+            a = torch.empty(M * k, N // 2, dtype=torch.bfloat16, device=DEV)
+            fused_moe_kernel_act_w8a8(q, s, Wd, SWd, a, sorted_ids, expert_ids, npp, k, B, M * k, act_name,
+                                      tw if routed else None)
+            torch.cuda.synchronize()
+            assert torch.equal(a.view(torch.int16), a_ref.view(torch.int16)), f"{act_name} routed={routed}"
 
 
 NUM_SMALL_CFGS = 7  # 16-row block configurations in csrc/gemm.hip (0: register streaming, 1-6: DMA ring)
