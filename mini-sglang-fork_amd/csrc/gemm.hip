@@ -27,6 +27,10 @@ constexpr DecodeCfg kDecodeCfgs[] = {
     {1, 16, 4}, {1, 8, 4}, {2, 16, 2}, {1, 16, 2}, {2, 8, 4}, {4, 16, 1},
     // 13-21: decode3_gemm_kernel (16 rows, LDS DMA ring; u = ring depth)
     {1, 4, 4}, {1, 4, 3}, {1, 2, 4}, {1, 8, 2}, {1, 4, 2}, {1, 2, 3}, {1, 2, 2}, {1, 1, 4}, {1, 8, 3},
+    // 22-31: decode3_gemm_kernel over a CU-balanced grid (a multiple of the
+    // CU count, each block up to 16 rg rows)
+    {1, 1, 4}, {1, 2, 2}, {1, 4, 3}, {1, 8, 2}, {2, 1, 4}, {2, 2, 3}, {2, 2, 4}, {2, 4, 2},
+    {2, 4, 3}, {2, 8, 2},
 };
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
@@ -44,20 +48,40 @@ void launch_decode2(const GemmArgs& g, hipStream_t st) {
                      st, g);
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // Ring depth is capped by the token-register ring (D x 4 x TG x 4 VGPRs).
-template <int TG, int WAVES, int D, int EPI>
+// kBal: a grid of c x CUs blocks of at most 16 RG rows each (every CU
+// streams the same bytes); otherwise one block per 16 rows.
+template <int TG, int WAVES, int D, int EPI, int RG = 1, bool kBal = false>
 void launch_decode3(const GemmArgs& g, hipStream_t st) {
   constexpr int kD = TG == 1 ? D : (TG == 2 ? (D < 3 ? D : 3) : 2);
-  constexpr int kLds = DecodeRing<TG, WAVES, kD>::kLds;
-  auto kern = decode3_gemm_kernel<TG, WAVES, kD, EPI>;
+  constexpr int kLds = RG * DecodeRing<TG, WAVES, kD>::kLds;
+  auto kern = decode3_gemm_kernel<TG, WAVES, kD, EPI, DenseRows, RG>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     attr_set = true;
   }
-  const unsigned blocks = static_cast<unsigned>((g.N + 15) / 16);
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WAVES), kLds, st, g);
+  int64_t blocks = (g.N + 15) / 16;
+  if (kBal) {
+    const int64_t cus = device_cus();
+    blocks = cus * ((g.N + cus * 16 * RG - 1) / (cus * 16 * RG));
+  }
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), kLds, st, g);
 }
 
 template <int TG, int EPI>
@@ -84,24 +108,44 @@ void decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
     case 18: launch_decode3<TG, 2, 3, EPI>(g, st); break;
     case 19: launch_decode3<TG, 2, 2, EPI>(g, st); break;
     case 20: launch_decode3<TG, 1, 4, EPI>(g, st); break;
-    default: launch_decode3<TG, 8, 3, EPI>(g, st); break;
+    case 21: launch_decode3<TG, 8, 3, EPI>(g, st); break;
+    case 22: launch_decode3<TG, 1, 4, EPI, 1, true>(g, st); break;
+    case 23: launch_decode3<TG, 2, 2, EPI, 1, true>(g, st); break;
+    case 24: launch_decode3<TG, 4, 3, EPI, 1, true>(g, st); break;
+    case 25: launch_decode3<TG, 8, 2, EPI, 1, true>(g, st); break;
+    case 26: launch_decode3<TG, 1, 4, EPI, 2, true>(g, st); break;
+    case 27: launch_decode3<TG, 2, 3, EPI, 2, true>(g, st); break;
+    case 28: launch_decode3<TG, 2, 4, EPI, 2, true>(g, st); break;
+    case 29: launch_decode3<TG, 4, 2, EPI, 2, true>(g, st); break;
+    case 30: launch_decode3<TG, 4, 3, EPI, 2, true>(g, st); break;
+    default: launch_decode3<TG, 8, 2, EPI, 2, true>(g, st); break;
   }
 }
 
 // Measured on MI355X at the Qwen3-14B shapes (K 5120 / 17408, N 5120 -
-// 34816).  Up to 32 tokens the LDS DMA ring (decode3) streams fastest:
-// at M = 1, 4 waves x 3 slots per block for wide N (gate_up: 32.6 us,
-// 5.5 TB/s) and 2 waves x 2 slots otherwise (o_proj: 7.9 us); for 2-32
-// tokens one wave x 4 slots per block (more resident blocks per CU).
+// 34816), weights streamed from HBM.  Up to 32 tokens the LDS DMA ring
+// (decode3) over a CU-balanced grid streams fastest.  With one block per
+// 16 rows, N = 5120 gives 320 blocks: a quarter of the CUs stream twice
+// the bytes of the others (down at M = 1: 22.3 us, against 13.5 us for
+// N = 4096).  The balanced grid (256 blocks of 20 rows, two MFMA row
+// groups sharing the token fragments) takes 18.1 us, and 21.6 us instead
+// of 28.8 us at 16 tokens.  Narrow N (<= 16384): 4 waves x 3 slots of 32
+// rows at one token, 8 waves x 2 slots up to 8 and from 17 tokens, 4
+// waves x 2 slots at 9-16.  Wide N (gate_up, 2176 row groups): 16-row
+// blocks, 2 waves x 2 slots at one token (30.6 us, 5.8 TB/s), one wave x
+// 4 slots up to 8, 32-row blocks of one wave x 4 slots at 17-32 tokens.
 // From 33 tokens on the token operand, read per wave through the texture
 // path, costs more than the weight stream: the register-streaming core
 // with 32 rows over 8 waves (cfg 3) wins, or 64 rows per block for very
 // wide N (cfg 4), which keeps fewer blocks re-reading the token panel.
 int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
   (void)K;
-  if (M == 1) return N >= 16384 ? 14 : 19;
-  if (M <= 32) return 20;
-  if (M > 48 && N >= 16384) return 4;
+  const bool wide = N >= 16384;
+  if (M == 1) return wide ? 23 : 30;
+  if (M <= 8) return wide ? 22 : 31;
+  if (M <= 16) return 29;
+  if (M <= 32) return wide ? 26 : 31;
+  if (M > 48 && wide) return 4;
   return 3;
 }
 

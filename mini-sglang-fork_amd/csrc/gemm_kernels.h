@@ -1364,17 +1364,25 @@ struct RingDrain<D, OPS, D> {
   __device__ __forceinline__ static void run(F&) {}
 };
 
-// Grouped use (SortedRows, alignment blocks of 16 * TG rows): grid y is
-// the alignment block; its expert's weights stream through the ring, the
-// token rows are gathered through sorted_ids (padding rows read zeros), and
-// the epilogue scatters to pair rows with the routed weight.
-template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows>
+// Dense use: the N weight rows are cut into gridDim.x equal ranges
+// (block b owns rows [N b / G, N (b+1) / G), at most 16 RG of them), so a
+// grid of a multiple of 256 blocks gives every CU the same bytes to stream
+// whatever N is; RG 16-row MFMA groups per block share the token fragments,
+// and rows past the block's range read zeros through the buffer range check
+// (no traffic) and are not stored.
+// Grouped use (SortedRows, RG = 1, alignment blocks of 16 * TG rows): grid y
+// is the alignment block; its expert's weights stream through the ring (16
+// rows per block), the token rows are gathered through sorted_ids (padding
+// rows read zeros), and the epilogue scatters to pair rows with the routed
+// weight.
+template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int kAcc = TG * 4;
-  constexpr int kOps = 4 + 4 * TG;  // vector memory ops per stage (DMA + token loads)
+  constexpr int kAcc = RG * TG * 4;
+  constexpr int kOps = 4 * RG + 4 * TG;  // vector memory ops per stage (DMA + token loads)
   static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
   static_assert(!Rows::kRuns, "grouped rows: one alignment block per block");
+  static_assert(RG == 1 || !Rows::kGrouped, "grouped rows: 16 weight rows per block");
   extern __shared__ __align__(16) unsigned char ring[];
   __shared__ int32_t red[kAcc][64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1390,24 +1398,32 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
   }
+  int64_t n0, rows;
+  if constexpr (Rows::kGrouped) {
+    n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    rows = g.N - n0 < 16 ? g.N - n0 : 16;
+  } else {
+    n0 = g.N * blockIdx.x / gridDim.x;
+    rows = g.N * (blockIdx.x + 1) / gridDim.x - n0;
+    if (rows <= 0) return;  // more blocks than rows (uniform per block)
+  }
   for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
   const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-  const int64_t rows = g.N - n0 < 16 ? g.N - n0 : 16;
   const int steps = static_cast<int>((g.K + 255) / 256);
   const int s_begin = steps * wave / WAVES, s_end = steps * (wave + 1) / WAVES;
-  unsigned char* my_ring = ring + wave * (D * kRingStage);
+  constexpr int kStage = RG * kRingStage;
+  unsigned char* my_ring = ring + wave * (D * kStage);
 
   // weight DMA: instruction j of a stage fills LDS rows 4j .. 4j+3; lane l
-  // fills row 4j + l/16, chunk l%16 from global chunk (l%16) ^ row
+  // fills row 4j + l/16, chunk l%16 from global chunk (l%16) ^ (row & 15)
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(W + n0 * g.K)), 0,
       static_cast<int>(rows * g.K), kBufferFlags);
-  uint32_t w_off[4];
+  uint32_t w_off[4 * RG];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 4 * RG; ++j) {
     const int row = 4 * j + (lane >> 4);
-    w_off[j] = static_cast<uint32_t>(row * g.K + 16 * ((lane & 15) ^ row));
+    w_off[j] = static_cast<uint32_t>(row * g.K + 16 * ((lane & 15) ^ (row & 15)));
   }
   // token operand: lane (token r16 of group tg, 16-byte group grp).  The
   // address is chosen by an integer select (no branch) and read through a
@@ -1432,11 +1448,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   v4i xr[D][4][TG];  // token chunks of the stages in flight, per ring slot
 
   auto issue = [&](int d, int st) {
-    unsigned char* slot = my_ring + d * kRingStage;
+    unsigned char* slot = my_ring + d * kStage;
     // a padding stage (st >= s_end) reads past the buffer range: zeros, no traffic
     const int soff = st < s_end ? st * 256 : 0x7fff0000;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4 * RG; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0,
                                                kStreamAux);
 #pragma unroll
@@ -1491,17 +1507,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     }
   }
 
-  v4i acc[TG];
+  v4i acc[RG][TG];
 #pragma unroll
-  for (int tg = 0; tg < TG; ++tg) acc[tg] = v4i{0};
+  for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) acc[rg][tg] = v4i{0};
   auto consume = [&](int d) {
-    const unsigned char* slot = my_ring + d * kRingStage;
+    const unsigned char* slot = my_ring + d * kStage;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const v4i w = *reinterpret_cast<const v4i*>(slot + r16 * 256 + 16 * ((4 * kb + grp) ^ r16));
 #pragma unroll
-      for (int tg = 0; tg < TG; ++tg)
-        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, xr[d][kb][tg], acc[tg], 0, 0, 0);
+      for (int rg = 0; rg < RG; ++rg) {
+        const v4i w = *reinterpret_cast<const v4i*>(slot + (16 * rg + r16) * 256 + 16 * ((4 * kb + grp) ^ r16));
+#pragma unroll
+        for (int tg = 0; tg < TG; ++tg)
+          acc[rg][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, xr[d][kb][tg], acc[rg][tg], 0, 0, 0);
+      }
     }
   };
 
@@ -1528,9 +1549,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 
   __syncthreads();  // red[] zeroed by every thread before any wave adds into it
 #pragma unroll
-  for (int tg = 0; tg < TG; ++tg)
+  for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) atomicAdd(&red[tg * 4 + v][lane], acc[tg][v]);
+    for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) atomicAdd(&red[(rg * TG + tg) * 4 + v][lane], acc[rg][tg][v]);
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kEpiPerThread; ++u) {
@@ -1538,10 +1561,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     if (e >= kAcc * 64) continue;
     const int j = e >> 6, l = e & 63;
     const int v = j & 3;
-    const int64_t n = n0 + 4 * (l >> 4) + v;
+    const int nl = 16 * (j / (4 * TG)) + 4 * (l >> 4) + v;  // row within the block's range
+    const int64_t n = n0 + nl;
     if constexpr (!kPre) {  // dense rows: operands loaded here
-      const int32_t m = 16 * (j / 4) + (l & 15);
-      if (n >= g.N || m >= g.M) continue;
+      const int32_t m = 16 * ((j / 4) % TG) + (l & 15);
+      if (nl >= rows || m >= g.M) continue;
       e_orow[0] = m;
       if constexpr (EPI == kEpiBf16) {
         e_sa[0] = g.sa[m];

@@ -225,14 +225,16 @@ def test_gemm_every_tile_config(M, K, N):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
-NUM_DECODE_CFGS = 22  # kDecodeCfgs in csrc/gemm.hip
+NUM_DECODE_CFGS = 32  # kDecodeCfgs in csrc/gemm.hip
 
 
 @pytest.mark.parametrize(
     "M,K,N",
     [(1, 1344, 336), (5, 1344, 336), (16, 1344, 336), (17, 1344, 336), (33, 1344, 336), (64, 1344, 336),
      (1, 1328, 200), (8, 1328, 200), (40, 1328, 200),  # K % 64 == 48: partial last step
-     (3, 4160, 72), (16, 4160, 72)],  # 65 steps: several pipelined batches per wave
+     (3, 4160, 72), (16, 4160, 72),  # 65 steps: several pipelined batches per wave
+     # CU-balanced grids: uneven row ranges of 1-32 rows per block
+     (1, 1344, 5000), (16, 1344, 8200), (32, 2048, 4100), (7, 1024, 16400)],
 )
 def test_gemm_every_decode_config(M, K, N):
     from minisgl_amd.kernel.lib import load
