@@ -181,6 +181,33 @@ int mw8_moe_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, co
                            int32_t block_size, void* out, mw8_stream_t stream);
 
 /*
+ * The MoE layer's down-projection GEMM with the slot sum fused in.  For
+ * every sorted position r below *num_post_pad with p = sorted_ids[r] <
+ * num_valid (p = token * top_k + slot):
+ *   cache[p, :] = epilogue(A[p] . W[e]^T, sa[p], sw[e], routed = topk_w[p])
+ * as mw8_moe_gemm_w8a8_bf16 with top_k = 1, and then
+ *   out[t, :] = bf16(sum over slots i = 0 .. top_k-1, in order, in fp32 of cache[t * top_k + i, :])
+ * as mw8_moe_sum_reduce_bf16 -- the same bits.  The block that writes the
+ * last of a token's top_k slots for a 16-column group sums that group, so
+ * no second launch runs.  counters int32 [num_valid / top_k, ceil(N/16)]
+ * carry the count between blocks: zero-fill them once before their first
+ * use; every call leaves them zero (calls that share them must be ordered
+ * on one stream).  Every pair's expert must lie in [0, E) (a block of an
+ * expert outside it writes nothing, and its tokens get no sum).  A int8
+ * [num_valid, K], W int8 [E, N, K], sw fp32 [E, N], cache bf16 [num_valid,
+ * N], out bf16 [num_valid / top_k, N]; N % 8 == 0, K % 64 == 0,
+ * block_size in {16, 32, 64, 128}, 16-byte aligned A, W, cache and out.
+ * Replaces fused_moe_kernel (GEMM2, MUL_ROUTED_WEIGHT) + moe_sum_reduce
+ * (python/minisgl/moe/fused.py:212-226, python/minisgl/kernel/moe_impl.py:65-98).
+ */
+int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const int32_t* sorted_ids, const int32_t* expert_ids,
+                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
+                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
+                               int32_t block_size, void* cache, void* out, int32_t* counters,
+                               mw8_stream_t stream);
+
+/*
  * Gate|up grouped GEMM with the gated activation fused into its epilogue:
  * W int8 [E, N = 2I, K] holds the gate rows then the up rows of each expert;
  * out bf16 [num_valid, I] receives act(g) * u with g, u the bf16 outputs the

@@ -189,6 +189,22 @@ void launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), kLds, st, g);
 }
 
+// Persistent form: min(units, CUs x per_cu) resident blocks walk the units.
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI>
+void launch_tile3_persist(const GemmArgs& g, unsigned units, int per_cu, hipStream_t st) {
+  constexpr int kLds = NSTAGE * (BM + BN) * BK;
+  auto kern = tile3_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    attr_set = true;
+  }
+  const int64_t slots = static_cast<int64_t>(device_cus()) * per_cu;
+  const unsigned grid = static_cast<unsigned>(units < slots ? units : slots);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * WM * WN), kLds, st, g);
+}
+
 // 0-4: register-staged tile core (any K % 16 == 0); 5 and up: direct-to-LDS
 // ring (K % bk == 0).  per_cu: resident blocks per CU (LDS-bound).
 struct TileCfg {
@@ -221,6 +237,7 @@ constexpr TileCfg kTileCfgs[] = {
     {64, 256, true, 64, 1},    // 24: 4 waves (1x4), 4 stages
     {64, 128, true, 128, 1},   // 25: 4 waves (1x4), 4 stages
     {256, 256, true, 64, 1},   // 26: 8 waves (4x2), 4 stages
+    {256, 256, true, 128, 1},  // 27: 14 as a persistent walk
 };
 constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
@@ -373,6 +390,7 @@ void dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     case 24: launch_tile3<64, 256, 64, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 25: launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 26: launch_tile3<256, 256, 64, 4, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 27: launch_tile3_persist<256, 256, 128, 4, 2, 2, EPI>(g, tiles, c.per_cu, st); break;
     default: launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
   if (split) {
@@ -635,7 +653,7 @@ void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream
   }
   int cfg = g_moe_cfg.load(std::memory_order_relaxed);
   if (cfg < 0 || cfg > 6) cfg = default_stream_cfg(g);
-  if (cfg == 0 && grouped_stream_fits(g.K)) {
+  if (cfg == 0 && grouped_stream_fits(g.K) && !g.sum_out) {  // no fused slot sum in the stream core
     launch_grouped_stream(g, blocks, epi, st);
     return;
   }

@@ -70,6 +70,12 @@ struct GemmArgs {
   // blocks behind expert_ids / num_post_pad (the tile height BM is a
   // multiple of it)
   int32_t align_bsz;
+  // fused slot sum (grouped bf16 only, slot_sum_step): sum_out bf16
+  // [num_valid / sum_k][N], sum_cnt int32 [num_valid / sum_k][ceil(N/16)]
+  // (zero on entry, left zero); null sum_out: no sum
+  uint16_t* sum_out;
+  int32_t* sum_cnt;
+  int32_t sum_k;
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -78,6 +84,28 @@ __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, co
   if (bias) t = t + bf16_to_f32(bias[n]);
   if (has_routed) t = t * routed;
   return f32_to_bf16(t);
+}
+
+// Output stores of a grouped bf16 epilogue.  With the fused slot sum the
+// rows are read back by other blocks in the same launch, so they are
+// written as device-scope (agent) atomic stores, which the compiler emits
+// as stores coherent across the XCDs' L2 caches; otherwise non-temporal.
+__device__ __forceinline__ void store_out16(uint16_t* dst, v4i d, bool coherent) {
+  if (coherent) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(dst);
+    __hip_atomic_store(q, static_cast<uint64_t>(static_cast<uint32_t>(d[0])) |
+                              (static_cast<uint64_t>(static_cast<uint32_t>(d[1])) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, static_cast<uint64_t>(static_cast<uint32_t>(d[2])) |
+                                  (static_cast<uint64_t>(static_cast<uint32_t>(d[3])) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(dst));
+  }
+}
+__device__ __forceinline__ void store_out1(uint16_t* dst, uint16_t v, bool coherent) {
+  if (coherent) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *dst = v;
 }
 
 // ------------------------------------------------------------------------
@@ -314,8 +342,9 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
         if constexpr (EPI == kEpiBf16) {
-          static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
-              epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr);
+          store_out1(static_cast<uint16_t*>(g.out) + orow * g.ldo + n,
+                     epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr),
+                     Rows::kGrouped && g.sum_out != nullptr);
         } else {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
@@ -402,6 +431,76 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// Fused slot sum (the MoE layer's GEMM2, routed weight applied): after a
+// block has stored its output rows -- row r of the block holds pair
+// row_p(r) (-1: none) for columns [n0, n0 + ncols) -- it counts, per
+// (token p / sum_k, 16-column group), the slots it completed.  The block
+// whose count completes a group's sum_k slots sums the token's sum_k rows
+// of out in slot order in fp32 (moe_sum_reduce_kernel's arithmetic) into
+// sum_out and resets the counter to zero for the next call.  The rows are
+// exchanged through device-coherent accesses only (store_out* with the
+// slot sum, agent-scope atomic loads here): every wave waits until its
+// stores have completed before the block counts, and the completing thread
+// issues its loads after its count has returned.  No cache write-back or
+// invalidation is needed (a device-scope fence per block, which writes back
+// the XCD's L2, made the launch several times slower than the separate sum
+// kernel), and no block waits for another.  Needs N % 8 == 0 and 16-byte
+// aligned out / sum_out.
+template <class RowP>
+__device__ __forceinline__ void slot_sum_step(const GemmArgs& g, int nrows, int64_t n0, int ncols, RowP row_p) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores have completed
+  __syncthreads();
+  const int groups = ncols / 16;
+  const int64_t G = (g.N + 15) / 16;
+  const int k = g.sum_k;
+  for (int it = threadIdx.x; it < nrows * groups; it += blockDim.x) {
+    const int r = it / groups;
+    const int64_t n = n0 + 16 * (it % groups);
+    const int32_t p = row_p(r);
+    if (p < 0 || n >= g.N) continue;
+    const int64_t t = p / k;
+    int32_t* cnt = g.sum_cnt + t * G + n / 16;
+    if (atomicAdd(cnt, 1) != k - 1) continue;
+    *cnt = 0;
+    const bool two = n + 8 < g.N;  // N % 8 == 0: the group holds 8 or 16 columns
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(static_cast<const uint16_t*>(g.out) + t * k * g.ldo + n);
+    const int64_t ld64 = g.ldo / 4;
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    for (int i = 0; i < k; ++i) {
+      uint64_t w[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        w[h] = (h < 2 || two) ? __hip_atomic_load(src + i * ld64 + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : uint64_t{0};
+      const v4i lo = v4i{static_cast<int>(w[0]), static_cast<int>(w[0] >> 32), static_cast<int>(w[1]),
+                         static_cast<int>(w[1] >> 32)};
+      const v4i hi = v4i{static_cast<int>(w[2]), static_cast<int>(w[2] >> 32), static_cast<int>(w[3]),
+                         static_cast<int>(w[3] >> 32)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a = static_cast<uint32_t>(lo[j]), b = static_cast<uint32_t>(hi[j]);
+        acc[2 * j] = acc[2 * j] + bf16_to_f32(static_cast<uint16_t>(a & 0xFFFFu));
+        acc[2 * j + 1] = acc[2 * j + 1] + bf16_to_f32(static_cast<uint16_t>(a >> 16));
+        acc[8 + 2 * j] = acc[8 + 2 * j] + bf16_to_f32(static_cast<uint16_t>(b & 0xFFFFu));
+        acc[8 + 2 * j + 1] = acc[8 + 2 * j + 1] + bf16_to_f32(static_cast<uint16_t>(b >> 16));
+      }
+    }
+    v4i o0, o1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o0[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[2 * j])) |
+                               (static_cast<uint32_t>(f32_to_bf16(acc[2 * j + 1])) << 16));
+      o1[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[8 + 2 * j])) |
+                               (static_cast<uint32_t>(f32_to_bf16(acc[8 + 2 * j + 1])) << 16));
+    }
+    uint16_t* dst = g.sum_out + t * g.N + n;
+    *reinterpret_cast<v4i*>(dst) = o0;
+    if (two) *reinterpret_cast<v4i*>(dst + 8) = o1;
+  }
 }
 
 // One BM x BN output tile over K stages [kt_begin, kt_end) of the ring core.
@@ -757,8 +856,11 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         if (orow >= 0 && n < g.N) {
           const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
           // non-temporal: the output is written once (gate_up M=8192 1405 -> 1377 us)
-          __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n));
+          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d, kMeta && g.sum_out != nullptr);
         }
+      }
+      if constexpr (kMeta) {
+        if (g.sum_out) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
       }
       return;
     }
@@ -792,15 +894,44 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
         if constexpr (EPI == kEpiBf16) {
-          static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
-              epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr);
+          store_out1(static_cast<uint16_t*>(g.out) + orow * g.ldo + n,
+                     epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr),
+                     Rows::kGrouped && g.sum_out != nullptr);
         } else {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
       }
     }
   }
+  if constexpr (kMeta) {
+    if (g.sum_out) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
+  }
 #endif  // __HIP_DEVICE_COMPILE__
+}
+
+// Work unit b of a dense ring grid: blocks [0, full_tiles) own whole tiles
+// (XCD-contiguous), block full_tiles + u the K range u % tail_split of
+// tail tile u / tail_split (an int32 partial tile); without a split, block
+// b owns tile tile_of_block(b).
+template <int BM, int BN, int BK>
+__device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, int64_t b) {
+  const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  int64_t pm, pn, split_unit = -1;
+  int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
+  if (g.tail_split > 1) {
+    if (b < g.full_tiles) {
+      tile_of_index(xcd_tile_index(b, g.full_tiles), tm, tn, pm, pn);
+    } else {
+      split_unit = b - g.full_tiles;
+      tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
+      const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
+      kt_begin = static_cast<int>(nkt * sp / g.tail_split);
+      kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
+    }
+  } else {
+    tile_of_block(b, tm, tn, pm, pn);
+  }
+  return TileJob{pm * BM, pn * BN, g.W, g.sw, kt_begin, kt_end, BM, split_unit};
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
@@ -859,27 +990,34 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     W += static_cast<int64_t>(e) * g.N * g.K;
     sw += static_cast<int64_t>(e) * g.N;
   } else {
-    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-    int64_t pm, pn;
-    if (g.tail_split > 1) {
-      if (blockIdx.x < g.full_tiles) {
-        tile_of_index(xcd_tile_index(blockIdx.x, g.full_tiles), tm, tn, pm, pn);
-      } else {
-        split_unit = static_cast<int64_t>(blockIdx.x) - g.full_tiles;
-        tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
-        const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
-        kt_begin = static_cast<int>(nkt * sp / g.tail_split);
-        kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
-      }
-    } else {
-      tile_of_block(blockIdx.x, tm, tn, pm, pn);
-    }
-    m0 = pm * BM;
-    n0 = pn * BN;
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, dense_tile_job<BM, BN, BK>(g, blockIdx.x));
+    return;
   }
 
   TileJob job{m0, n0, W, sw, kt_begin, kt_end, rows_valid, split_unit};
   tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// Persistent dense ring GEMM: gridDim.x resident blocks (a multiple of the
+// XCD count) walk the units of tile3_gemm_kernel's grid -- unit u runs on
+// block u % gridDim.x, so on the same XCD as in the one-block-per-unit
+// launch -- with one barrier between units (the staged epilogue's LDS reads
+// and metadata tables are done before the next unit's DMA refills the
+// ring).  The previous unit's output stores drain while the next unit's
+// first stages load: the stage waits count loads, which complete in issue
+// order among themselves, so stores still in flight only make them wait
+// longer, never shorter.
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI>
+__global__ __launch_bounds__(64 * WM * WN) void tile3_persist_kernel(GemmArgs g) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  const int64_t units = g.tail_split > 1 ? g.full_tiles + (tiles - g.full_tiles) * g.tail_split : tiles;
+  for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, DenseRows>(g, lds, dense_tile_job<BM, BN, BK>(g, u));
+    __syncthreads();
+  }
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -1583,10 +1721,18 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       } else {
         if (g.bias) t = t + e_x[ui];
       }
-      static_cast<uint16_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = f32_to_bf16(t);
+      store_out1(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(e_orow[ui]) * g.ldo + n, f32_to_bf16(t),
+                 Rows::kGrouped && g.sum_out != nullptr);
     } else {
       static_cast<int32_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = a;
     }
+  }
+  if constexpr (Rows::kGrouped && EPI == kEpiBf16) {
+    if (g.sum_out)
+      slot_sum_step(g, 16 * TG, n0, 16, [&](int r) {
+        const int32_t p = g.sorted_ids[m0 + r];
+        return p < g.num_valid ? p : -1;
+      });
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }

@@ -53,6 +53,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P],
     ),
+    "mw8_moe_gemm_sum_w8a8_bf16": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P],
+    ),
     "mw8_moe_prepare_small": (
         ctypes.c_int,
         [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],

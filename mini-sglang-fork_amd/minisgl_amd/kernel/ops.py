@@ -375,6 +375,70 @@ def fused_moe_kernel_act_w8a8(
     )
 
 
+_SLOT_COUNTERS: Dict[torch.device, torch.Tensor] = {}
+
+
+def slot_sum_counters(tokens: int, N: int, device: torch.device) -> torch.Tensor:
+    """Counters of the fused slot sum for ``tokens`` x ``N`` outputs: int32
+    [tokens * ceil(N / 16)], zero-filled once, cached per device and grown on
+    demand.  Every call of fused_moe_kernel_sum_w8a8 leaves them zero, so any
+    calls ordered on one stream share them.  Reserve the largest size before
+    capturing a graph (growing it allocates)."""
+    need = tokens * ((N + 15) // 16)
+    dev = torch.device(device)
+    buf = _SLOT_COUNTERS.get(dev)
+    if buf is None or buf.numel() < need:
+        buf = torch.zeros(max(need, 1 << 16), dtype=torch.int32, device=dev)
+        _SLOT_COUNTERS[dev] = buf
+    return buf
+
+
+def fused_moe_kernel_sum_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    C: torch.Tensor,
+    out: torch.Tensor,
+    topk_weights: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    top_k: int,
+    block_size: int,
+    num_valid_tokens: int,
+    counters: Optional[torch.Tensor] = None,
+) -> None:
+    """GEMM2 of the MoE layer with the slot sum fused in: C bf16 [M*k, N]
+    receives the routed-weighted expert outputs of every pair (as
+    fused_moe_kernel_w8a8 with MUL_ROUTED_WEIGHT and top_k = 1) and out bf16
+    [M, N] their sum over the k slots (as moe_sum_reduce, the same bits),
+    from one launch.  Every pair's expert must lie in [0, E)."""
+    _on_gpu(A, A_scale, B, B_scale, C, out, topk_weights)
+    _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [M*k, K]")
+    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
+    E, N, K = B.shape
+    _need(A.shape == (num_valid_tokens, K), "A: [M*k, K]")
+    _need(A_scale.dtype == torch.float32 and A_scale.shape == (num_valid_tokens,), "A_scale: fp32 [M*k]")
+    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
+    _need(num_valid_tokens % top_k == 0, "num_valid_tokens: a multiple of top_k")
+    M = num_valid_tokens // top_k
+    _need(C.dtype == torch.bfloat16 and C.is_contiguous() and C.numel() == num_valid_tokens * N, "C: bf16 [M*k, N]")
+    _need(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == M * N, "out: bf16 [M, N]")
+    _need(topk_weights.dtype == torch.float32 and topk_weights.is_contiguous() and topk_weights.numel() == num_valid_tokens,
+          "topk_weights: fp32 [M, k]")
+    if counters is None:
+        counters = slot_sum_counters(M, N, A.device)
+    _need(counters.dtype == torch.int32 and counters.numel() >= M * ((N + 15) // 16), "counters: int32 [M * ceil(N/16)]")
+    check(
+        load().mw8_moe_gemm_sum_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids), _ptr(expert_ids),
+            _ptr(num_tokens_post_padded), sorted_token_ids.shape[0], _ptr(topk_weights), top_k,
+            num_valid_tokens, N, K, E, block_size, _ptr(C), _ptr(out), _ptr(counters), _stream(A),
+        )
+    )
+
+
 def fused_moe_kernel_w8a8_i32(
     A: torch.Tensor,
     B: torch.Tensor,
@@ -424,5 +488,9 @@ __all__ = [
     "moe_align_block_size",
     "fused_moe_kernel_w8a8",
     "fused_moe_kernel_w8a8_i32",
+    "fused_moe_kernel_act_w8a8",
+    "fused_moe_kernel_sum_w8a8",
+    "slot_sum_counters",
+    "moe_prepare_small",
     "moe_sum_reduce",
 ]

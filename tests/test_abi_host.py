@@ -107,6 +107,19 @@ def test_argument_errors_return_codes(lib):
     assert prep(FAKE_A, 1, 4, 16, 8, 1, FAKE_B, 64, None, FAKE_C, FAKE_C, FAKE_C, 17, 16,
                 FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_ARG"]
     assert lib.mw8_moe_sum_reduce_bf16(FAKE_A, 4, 8, 12, FAKE_B, None) == E["MW8_ERR_SHAPE"]
+    # GEMM2 with the fused slot sum: null counters, N % 8 != 0, K % 64 != 0,
+    # num_valid not a multiple of top_k
+    gsum = lib.mw8_moe_gemm_sum_w8a8_bf16
+    args = [FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 64, FAKE_B, 8, 64, 64, 128, 4, 16,
+            FAKE_A, FAKE_B, FAKE_C, None]
+    bad = list(args); bad[17] = None
+    assert gsum(*bad) == E["MW8_ERR_ARG"]
+    bad = list(args); bad[11] = 60
+    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
+    bad = list(args); bad[12] = 96
+    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
+    bad = list(args); bad[10] = 60
+    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
     # empty problems are no-ops
     assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0
 
