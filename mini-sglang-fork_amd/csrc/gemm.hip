@@ -653,13 +653,29 @@ void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream
   }
   int cfg = g_moe_cfg.load(std::memory_order_relaxed);
   if (cfg < 0 || cfg > 6) cfg = default_stream_cfg(g);
-  if (cfg == 0 && grouped_stream_fits(g.K) && !g.sum_out) {  // no fused slot sum in the stream core
+  if (cfg == 0 && grouped_stream_fits(g.K)) {
     launch_grouped_stream(g, blocks, epi, st);
     return;
   }
   if (cfg == 0) cfg = 1;
   if (epi == kEpiBf16) launch_grouped_ring_cfg<kEpiBf16>(cfg, g, blocks, st);
   else launch_grouped_ring_cfg<kEpiI32>(cfg, g, blocks, st);
+}
+
+// GEMM2 with the fused slot sum (kEpiBf16Sum): the automatic choice of the
+// plain GEMM2 for the block size (the tuning override does not apply).
+void launch_grouped_sum(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st) {
+  if (bm == 32) {
+    launch_grouped_ring<1, 3, kEpiBf16Sum, 2>(g, blocks, st);
+  } else if (bm == 16) {
+    launch_grouped_ring<1, 3, kEpiBf16Sum>(g, blocks, st);
+  } else if (default_moe_cfg(g, bm) == 15) {
+    launch_grouped_persist<128, 256, 64, 2, 2, 3, kEpiBf16Sum, true, 2>(g, st);
+  } else if (bm == 64) {
+    launch_grouped3<64, 128, 64, 2, 2, 4, kEpiBf16Sum>(g, blocks, st);
+  } else {
+    launch_grouped3<128, 128, 64, 2, 2, 4, kEpiBf16Sum>(g, blocks, st);
+  }
 }
 
 void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {

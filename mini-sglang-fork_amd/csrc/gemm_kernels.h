@@ -34,7 +34,10 @@
 
 namespace mw8 {
 
-enum EpiKind : int { kEpiBf16 = 0, kEpiI32 = 1 };
+// kEpiBf16Sum: the bf16 epilogue of the MoE layer's GEMM2 followed by the
+// fused slot sum (slot_sum_step); instantiated only for that entry point.
+enum EpiKind : int { kEpiBf16 = 0, kEpiI32 = 1, kEpiBf16Sum = 2 };
+constexpr bool epi_bf16_out(int e) { return e != kEpiI32; }
 
 // Everything a core needs to know about rows, experts and the epilogue.
 struct GemmArgs {
@@ -70,9 +73,9 @@ struct GemmArgs {
   // blocks behind expert_ids / num_post_pad (the tile height BM is a
   // multiple of it)
   int32_t align_bsz;
-  // fused slot sum (grouped bf16 only, slot_sum_step): sum_out bf16
+  // fused slot sum (EPI kEpiBf16Sum, slot_sum_step): sum_out bf16
   // [num_valid / sum_k][N], sum_cnt int32 [num_valid / sum_k][ceil(N/16)]
-  // (zero on entry, left zero); null sum_out: no sum
+  // (zero on entry, left zero)
   uint16_t* sum_out;
   int32_t* sum_cnt;
   int32_t sum_k;
@@ -86,10 +89,11 @@ __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, co
   return f32_to_bf16(t);
 }
 
-// Output stores of a grouped bf16 epilogue.  With the fused slot sum the
-// rows are read back by other blocks in the same launch, so they are
-// written as device-scope (agent) atomic stores, which the compiler emits
-// as stores coherent across the XCDs' L2 caches; otherwise non-temporal.
+// Output stores of a grouped bf16 epilogue.  With the fused slot sum
+// (kEpiBf16Sum) the rows are read back by other blocks in the same launch,
+// so they are written as device-scope (agent) atomic stores, which the
+// compiler emits as stores coherent across the XCDs' L2 caches; otherwise
+// non-temporal.
 __device__ __forceinline__ void store_out16(uint16_t* dst, v4i d, bool coherent) {
   if (coherent) {
     uint64_t* q = reinterpret_cast<uint64_t*>(dst);
@@ -342,9 +346,8 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
         if constexpr (EPI == kEpiBf16) {
-          store_out1(static_cast<uint16_t*>(g.out) + orow * g.ldo + n,
-                     epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr),
-                     Rows::kGrouped && g.sum_out != nullptr);
+          static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
+              epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr);
         } else {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
@@ -554,8 +557,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // dependent loads overlap the main loop instead of stalling the epilogue.
   // The dense bf16 epilogue keeps its row scales in the same table, and
   // both keep the tile's column scales (and bias) in LDS.
-  constexpr bool kMeta = Rows::kGrouped && EPI == kEpiBf16;
-  constexpr bool kMetaSa = EPI == kEpiBf16;
+  constexpr bool kMeta = Rows::kGrouped && epi_bf16_out(EPI);
+  constexpr bool kMetaSa = epi_bf16_out(EPI);
   static_assert(!kMetaSa || (BM <= 64 * kWaves && BN <= 64 * kWaves), "one metadata row per thread");
   __shared__ int32_t meta_p[kMeta ? BM : 1];
   __shared__ float meta_sa[kMetaSa ? BM : 1], meta_rt[kMeta ? BM : 1];
@@ -573,7 +576,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
-  static_assert(kAct < 0 || (Rows::kGrouped && EPI == kEpiBf16 && BM * BN * 2 <= NSTAGE * kStage && BN >= 128),
+  static_assert(kAct < 0 || (Rows::kGrouped && epi_bf16_out(EPI) && BM * BN * 2 <= NSTAGE * kStage && BN >= 128),
                 "fused activation: grouped bf16 with the staged epilogue (the host sets staged_out)");
   constexpr int kHalfN = BN / 2;
   const int64_t half = g.N / 2;  // kAct: rows of each of the gate and up halves
@@ -765,7 +768,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // word; the staging layout XORs the 16-byte chunk index of row r with
   // sf(r), which keeps both the word writes (rows R, R+1, R+4, R+5 per
   // instruction) and the 16-byte row reads on distinct LDS banks.
-  if constexpr (EPI == kEpiBf16 && BM * BN * 2 <= NSTAGE * kStage && BN >= 128) {
+  if constexpr (epi_bf16_out(EPI) && BM * BN * 2 <= NSTAGE * kStage && BN >= 128) {
     if (g.staged_out) {
       constexpr int kRowBytes = BN * 2;
       auto sf = [](int r) { return 4 * ((r & 1) | (((r >> 2) & 1) << 1)); };
@@ -856,12 +859,10 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         if (orow >= 0 && n < g.N) {
           const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
           // non-temporal: the output is written once (gate_up M=8192 1405 -> 1377 us)
-          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d, kMeta && g.sum_out != nullptr);
+          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d, EPI == kEpiBf16Sum);
         }
       }
-      if constexpr (kMeta) {
-        if (g.sum_out) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
-      }
+      if constexpr (EPI == kEpiBf16Sum) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
       return;
     }
   }
@@ -887,25 +888,23 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         rvalid = orow < g.M;
       }
       if (!rvalid) continue;
-      const float sa = EPI == kEpiBf16 ? g.sa[arow] : 0.0f;
+      const float sa = epi_bf16_out(EPI) ? g.sa[arow] : 0.0f;
 #pragma unroll
       for (int j = 0; j < kFN; ++j) {
         const int64_t n = n0 + wn * kWaveN + 32 * j + frow;
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
-        if constexpr (EPI == kEpiBf16) {
+        if constexpr (epi_bf16_out(EPI)) {
           store_out1(static_cast<uint16_t*>(g.out) + orow * g.ldo + n,
                      epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr),
-                     Rows::kGrouped && g.sum_out != nullptr);
+                     EPI == kEpiBf16Sum);
         } else {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
       }
     }
   }
-  if constexpr (kMeta) {
-    if (g.sum_out) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
-  }
+  if constexpr (EPI == kEpiBf16Sum) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -1639,7 +1638,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       arow = m;
       if (g.bias) e_x[u] = bf16_to_f32(g.bias[n]);
     }
-    if constexpr (EPI == kEpiBf16) {
+    if constexpr (epi_bf16_out(EPI)) {
       e_sa[u] = g.sa[arow];
       e_sw[u] = sw[n];
     }
@@ -1705,7 +1704,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       const int32_t m = 16 * ((j / 4) % TG) + (l & 15);
       if (nl >= rows || m >= g.M) continue;
       e_orow[0] = m;
-      if constexpr (EPI == kEpiBf16) {
+      if constexpr (epi_bf16_out(EPI)) {
         e_sa[0] = g.sa[m];
         e_sw[0] = sw[n];
         e_x[0] = g.bias ? bf16_to_f32(g.bias[n]) : 0.0f;
@@ -1714,7 +1713,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     const int ui = kPre ? u : 0;
     if (e_orow[ui] < 0) continue;
     const int32_t a = red[j][l];
-    if constexpr (EPI == kEpiBf16) {
+    if constexpr (epi_bf16_out(EPI)) {
       float t = epi_scale(a, e_sa[ui], e_sw[ui]);
       if constexpr (Rows::kGrouped) {
         if (g.topk_w) t = t * e_x[ui];
@@ -1722,17 +1721,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
         if (g.bias) t = t + e_x[ui];
       }
       store_out1(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(e_orow[ui]) * g.ldo + n, f32_to_bf16(t),
-                 Rows::kGrouped && g.sum_out != nullptr);
+                 EPI == kEpiBf16Sum);
     } else {
       static_cast<int32_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = a;
     }
   }
-  if constexpr (Rows::kGrouped && EPI == kEpiBf16) {
-    if (g.sum_out)
-      slot_sum_step(g, 16 * TG, n0, 16, [&](int r) {
-        const int32_t p = g.sorted_ids[m0 + r];
-        return p < g.num_valid ? p : -1;
-      });
+  if constexpr (Rows::kGrouped && EPI == kEpiBf16Sum) {
+    slot_sum_step(g, 16 * TG, n0, 16, [&](int r) {
+      const int32_t p = g.sorted_ids[m0 + r];
+      return p < g.num_valid ? p : -1;
+    });
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }

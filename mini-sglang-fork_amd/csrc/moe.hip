@@ -9,6 +9,7 @@ namespace mw8 {
 
 void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
 void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
+void launch_grouped_sum(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
 void launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
 
 namespace {
@@ -514,11 +515,7 @@ int moe_gemm_sum_w8a8(const int8_t* A, const float* sa, const int8_t* W, const f
   g.sum_out = static_cast<uint16_t*>(out);
   g.sum_cnt = counters;
   g.sum_k = top_k;
-  if (bsz <= 32) {
-    launch_grouped_small(g, static_cast<unsigned>(blocks), kEpiBf16, st);
-  } else {
-    launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, kEpiBf16, st);
-  }
+  launch_grouped_sum(g, static_cast<unsigned>(blocks), bsz, st);
   return check_launch("moe_gemm_sum");
 }
 

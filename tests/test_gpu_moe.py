@@ -389,56 +389,47 @@ def test_grouped_run_tiles(B):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
-@pytest.mark.parametrize("shape", ["cfg3", "ragged"])
+@pytest.mark.parametrize("shape", ["cfg3", "ragged", "ragged_big"])
 @pytest.mark.parametrize("B", [16, 32, 64, 128])
 def test_fused_slot_sum_equals_gemm_then_sum(shape, B):
     """GEMM2 with the slot sum fused in (one launch): the pair rows equal
     fused_moe_kernel_w8a8 (routed weight, top_k 1) and the token rows equal
-    moe_sum_reduce of them, bit for bit, against the oracle, through every
-    grouped configuration of the block size.  Each configuration runs twice
-    on one counter buffer, the second time on fewer tokens, and the counters
-    must be back to zero after each call."""
-    from minisgl_amd.kernel import lib as mw8lib
-
-    lib = mw8lib.load()
+    moe_sum_reduce of them, bit for bit, against the oracle, on the DMA ring
+    (16- and 32-row blocks), the one-tile-per-block grid and the persistent
+    walk (ragged_big: at least 32 pairs per expert).  Each case runs twice
+    on one counter buffer, the second time on fewer tokens, and the
+    counters must be back to zero after each call."""
     if shape == "cfg3":
         c = moe_case(96, seed=97)
         M, k = 96, 8
         logits, W, SW = c["logits"], c["w2"], c["s_w2"]
         gen = torch.Generator().manual_seed(97)
         act = torch.randn(M * k, W.shape[2], generator=gen).to(torch.bfloat16)
-    else:
+    elif shape == "ragged":
         M, k = 50, 2
         logits, W, SW, act = _ragged_expert_case(13, M=M, k=k, E=8, N=208, K=384)
+    else:
+        M, k = 400, 2
+        logits, W, SW, act = _ragged_expert_case(14, M=M, k=k, E=8, N=208, K=384)
     E, N, K = W.shape
     Wd, SWd = W.to(DEV), SW.to(DEV)
-    cfgs = range(-1, NUM_SMALL_CFGS) if B == 16 else ([-1] if B == 32 else range(-1, NUM_MOE_CFGS))
     counters = torch.zeros(M * ((N + 15) // 16), dtype=torch.int32, device=DEV)
-    runs = []
     for m in (M, M // 3):  # second call: fewer tokens on the same counters
+        announce(f"fused slot sum {shape} B={B} M={m}")
         w_ref, ids_ref = orc.topk_softmax(f32(logits[:m]), k, True)
         q, s = quant_per_token(act[: m * k].to(DEV))
         y_ref = orc.grouped_gemm_w8a8(q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, 1,
                                       routed=w_ref)
         o_ref = orc.moe_sum_reduce(y_ref.reshape(m, k, N))
-        ids = torch.from_numpy(ids_ref).to(DEV)
-        sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, E)
-        runs.append((m, q, s, torch.from_numpy(w_ref).to(DEV), sorted_ids, expert_ids, npp, y_ref, o_ref))
-    try:
-        for cfg in cfgs:
-            lib.mw8_set_tuning(-1, -1, cfg)
-            for m, q, s, tw, sorted_ids, expert_ids, npp, y_ref, o_ref in runs:
-                announce(f"fused slot sum {shape} B={B} cfg={cfg} M={m}")
-                cache = torch.empty(m * k, N, dtype=torch.bfloat16, device=DEV)
-                out = torch.empty(m, N, dtype=torch.bfloat16, device=DEV)
-                fused_moe_kernel_sum_w8a8(q, s, Wd, SWd, cache, out, tw, sorted_ids, expert_ids, npp, k, B,
-                                          m * k, counters=counters)
-                torch.cuda.synchronize()
-                assert bf16_bits_equal(cache, y_ref).all(), f"cfg {cfg} M={m}: pair rows"
-                assert bf16_bits_equal(out, o_ref).all(), f"cfg {cfg} M={m}: slot sums"
-                assert int(counters.abs().sum().item()) == 0, f"cfg {cfg} M={m}: counters not reset"
-    finally:
-        lib.mw8_set_tuning(-1, -1, -1)
+        sorted_ids, expert_ids, npp = moe_align_block_size(torch.from_numpy(ids_ref).to(DEV), B, E)
+        cache = torch.empty(m * k, N, dtype=torch.bfloat16, device=DEV)
+        out = torch.empty(m, N, dtype=torch.bfloat16, device=DEV)
+        fused_moe_kernel_sum_w8a8(q, s, Wd, SWd, cache, out, torch.from_numpy(w_ref).to(DEV), sorted_ids,
+                                  expert_ids, npp, k, B, m * k, counters=counters)
+        torch.cuda.synchronize()
+        assert bf16_bits_equal(cache, y_ref).all(), f"M={m}: pair rows"
+        assert bf16_bits_equal(out, o_ref).all(), f"M={m}: slot sums"
+        assert int(counters.abs().sum().item()) == 0, f"M={m}: counters not reset"
 
 
 def test_sum_reduce():
