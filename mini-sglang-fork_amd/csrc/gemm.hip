@@ -292,6 +292,7 @@ constexpr ModelCfg kModelCfgs[] = {
     {21, 3.0, 3.7, 6.1},  // 128x128 BK 128, 2 stages, two per CU
     {7, 3.0, 4.6, 5.9},   // 128x128 BK 64, 4 stages, two per CU
     {25, 3.0, 3.36, 3.36},  // 64x128, 4 stages
+    {17, 6.0, 8.0, 8.0},    // 256x128, 8 waves, 3 stages (no K split): grids of 129-256 tiles
 };
 
 double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
