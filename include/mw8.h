@@ -233,6 +233,18 @@ int mw8_moe_gemm_w8a8_i32(const int8_t* A, const int8_t* W, const int32_t* sorte
                           mw8_stream_t stream);
 
 /*
+ * Router and hidden-state quantizer in one launch (one wave per token):
+ * topk_w / topk_ids as mw8_topk_softmax and q / s as
+ * mw8_quant_per_token_bf16 on hidden bf16 [M, H] (row stride H), bit for
+ * bit.  H % 8 == 0, hidden 16-byte and q 8-byte aligned; E and topk as
+ * mw8_topk_softmax.  Replaces fused_topk (python/minisgl/moe/fused.py:9-28)
+ * plus the quantization of hidden_states before GEMM1 (:192).
+ */
+int mw8_moe_route_quant(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,
+                        int32_t renorm, const void* hidden, int64_t H, float* topk_w, int32_t* topk_ids,
+                        int8_t* q, float* s, mw8_stream_t stream);
+
+/*
  * Small-batch MoE preparation in one launch: the router of
  * mw8_topk_softmax (logits [M, E] -> topk_w fp32 / topk_ids int32 [M, topk]),
  * the per-token quantization of the hidden rows of mw8_quant_per_token_bf16

@@ -41,6 +41,8 @@ int moe_sum_reduce_bf16(const void*, int64_t, int, int64_t, void*, hipStream_t);
 int moe_gemm_act_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
                       const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                       int64_t, int, int, int, void*, hipStream_t);
+int moe_route_quant(const void*, int, int64_t, int, int, int, const void*, int64_t, float*, int32_t*, int8_t*,
+                    float*, hipStream_t);
 int moe_gemm_sum_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
                       const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                       int64_t, int, int, void*, void*, int32_t*, hipStream_t);
@@ -163,6 +165,13 @@ int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W
                                mw8_stream_t stream) {
   MW8_ENTRY(mw8::moe_gemm_sum_w8a8(A, sa, W, sw, sorted_ids, expert_ids, num_post_pad, max_sorted, topk_w,
                                    top_k, num_valid, N, K, E, block_size, cache, out, counters, S(stream)));
+}
+
+int mw8_moe_route_quant(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,
+                        int32_t renorm, const void* hidden, int64_t H, float* topk_w, int32_t* topk_ids,
+                        int8_t* q, float* s, mw8_stream_t stream) {
+  MW8_ENTRY(mw8::moe_route_quant(logits, is_bf16, M, E, topk, renorm, hidden, H, topk_w, topk_ids, q, s,
+                                 S(stream)));
 }
 
 int mw8_moe_prepare_small(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,

@@ -314,6 +314,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_prepare_kernel(
   align_body(ids, M * topk, slots, bsz, 1, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits, 0, 1);
 }
 
+// Router and hidden-state quantizer of one token per wave (both read only
+// their own token): the outputs of topk_softmax_kernel and quant_rows_kernel
+// bit for bit, from one launch.
+template <int VPL>
+__global__ __launch_bounds__(256) void route_quant_kernel(const void* logits, int is_bf16, int64_t M, int E,
+                                                          int topk, int renorm, const uint16_t* __restrict__ hidden,
+                                                          int64_t H, float* __restrict__ tw,
+                                                          int32_t* __restrict__ tid_out, int8_t* __restrict__ q,
+                                                          float* __restrict__ s) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;  // whole waves
+  topk_token<VPL>(logits, is_bf16, t, E, topk, renorm, tw, tid_out, nullptr);
+  quant_row_wave(hidden + t * H, H, q + t * H, s + t);
+}
+
 // ------------------------------------------------------------ slot sum
 // out[t, h] = bf16(sum_i in[t, i, h]) in fp32, slot order i = 0..k-1
 // (python/minisgl/kernel/triton/fused_moe.py:36-47); 8 columns per thread.
@@ -369,6 +384,30 @@ int topk_softmax(const void* logits, int is_bf16, int64_t M, int E, int topk, in
   else if (vpl <= 8) launch_topk<8>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
   else launch_topk<16>(logits, is_bf16, M, E, topk, renorm, topk_w, topk_ids, st);
   return check_launch("topk_softmax");
+}
+
+int moe_route_quant(const void* logits, int is_bf16, int64_t M, int E, int topk, int renorm, const void* hidden,
+                    int64_t H, float* topk_w, int32_t* topk_ids, int8_t* q, float* s, hipStream_t st) {
+  MW8_REQUIRE(logits && hidden && topk_w && topk_ids && q && s, kErrArg, "moe_route_quant: null pointer");
+  MW8_REQUIRE(E > 0 && E <= 1024 && topk > 0 && topk <= E && topk <= 64, kErrShape,
+              "moe_route_quant: need 0 < topk <= min(E, 64), E <= 1024 (E=%d topk=%d)", E, topk);
+  MW8_REQUIRE(H > 0 && H % 8 == 0, kErrShape, "moe_route_quant: need H %% 8 == 0 (H=%lld)", (long long)H);
+  MW8_REQUIRE(aligned16(hidden) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0, kErrAlign,
+              "moe_route_quant: hidden needs 16-byte and q 8-byte alignment");
+  if (M <= 0) return kOk;
+  MW8_REQUIRE(M < (1ll << 32), kErrShape, "moe_route_quant: too many tokens");
+  const int vpl = (E + 63) / 64;
+  auto go = [&](auto vpl_c) {
+    constexpr int V = decltype(vpl_c)::value;
+    hipLaunchKernelGGL((route_quant_kernel<V>), dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, st, logits,
+                       is_bf16, M, E, topk, renorm, static_cast<const uint16_t*>(hidden), H, topk_w, topk_ids, q, s);
+  };
+  if (vpl <= 1) go(std::integral_constant<int, 1>{});
+  else if (vpl <= 2) go(std::integral_constant<int, 2>{});
+  else if (vpl <= 4) go(std::integral_constant<int, 4>{});
+  else if (vpl <= 8) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 16>{});
+  return check_launch("moe_route_quant");
 }
 
 int64_t moe_align_max_padded(int64_t numel, int slots, int bsz) {

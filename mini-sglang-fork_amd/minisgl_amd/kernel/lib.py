@@ -57,6 +57,9 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P],
     ),
+    "mw8_moe_route_quant": (
+        ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P]
+    ),
     "mw8_moe_prepare_small": (
         ctypes.c_int,
         [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],

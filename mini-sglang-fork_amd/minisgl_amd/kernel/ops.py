@@ -253,6 +253,38 @@ def moe_align_block_size(
 PREPARE_MAX_PAIRS = 1024  # M * topk bound of the one-block preparation
 
 
+def moe_route_quant(
+    gating_output: torch.Tensor,
+    hidden_states: torch.Tensor,
+    topk: int,
+    renormalize: bool,
+) -> Tuple[torch.Tensor, ...]:
+    """Router + hidden-state quantization in one launch (one wave per
+    token).  Returns (topk_weights fp32 [M, k], topk_ids int32 [M, k], q
+    int8 [M, H], s fp32 [M]), bit-identical to topk_softmax and
+    quant_per_token."""
+    _on_gpu(gating_output, hidden_states)
+    g, h = gating_output, hidden_states
+    _need(g.dim() == 2 and g.is_contiguous(), "gating_output: [M, E] contiguous")
+    _need(g.dtype in (torch.bfloat16, torch.float32), "gating_output: bf16 or fp32")
+    _need(h.dtype == torch.bfloat16 and h.dim() == 2 and h.is_contiguous(), "hidden_states: bf16 [M, H] contiguous")
+    M, E = g.shape
+    _need(h.shape[0] == M, "hidden_states / gating_output token counts differ")
+    H = h.shape[1]
+    dev = g.device
+    w = torch.empty((M, topk), dtype=torch.float32, device=dev)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=dev)
+    q = torch.empty((M, H), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    check(
+        load().mw8_moe_route_quant(
+            _ptr(g), int(g.dtype == torch.bfloat16), M, E, topk, int(renormalize), _ptr(h), H,
+            _ptr(w), _ptr(ids), _ptr(q), _ptr(s), _stream(g),
+        )
+    )
+    return w, ids, q, s
+
+
 def moe_prepare_small(
     gating_output: torch.Tensor,
     hidden_states: torch.Tensor,
@@ -492,5 +524,6 @@ __all__ = [
     "fused_moe_kernel_sum_w8a8",
     "slot_sum_counters",
     "moe_prepare_small",
+    "moe_route_quant",
     "moe_sum_reduce",
 ]

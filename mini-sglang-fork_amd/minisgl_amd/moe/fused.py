@@ -17,8 +17,8 @@ w2 int8 [E, H, I]:
 
 All counts stay on the device (no host sync), so the call can be captured
 in a HIP graph.  For the smallest decode batches (M * k <= 32) the backend
-runs steps 1-3 as one launch (``moe_prepare_small``), with the same
-outputs bit for bit.
+runs steps 1-3 as one launch (``moe_prepare_small``), otherwise steps 1 and
+3 as one launch (``moe_route_quant``), with the same outputs bit for bit.
 """
 
 from __future__ import annotations
@@ -34,6 +34,7 @@ from ..kernel import (
     fused_moe_kernel_w8a8,
     moe_align_block_size,
     moe_prepare_small,
+    moe_route_quant,
     moe_sum_reduce,
     quant_per_token,
     topk_softmax,
@@ -161,6 +162,11 @@ class FusedMoeW8A8(BaseMoeBackend):
             raise ValueError("the W8A8 MoE backend needs w1_scale and w2_scale")
         M, H = hidden_states.shape
         E = w1.shape[0]
+        # the contract fused_experts_impl_w8a8 asserts, for the fast paths too
+        assert H == w1.shape[2], "Hidden size mismatch"
+        assert hidden_states.dtype == torch.bfloat16, "W8A8 MoE takes bf16 activations"
+        assert w1.dtype == torch.int8 and w2.dtype == torch.int8, "W8A8 MoE takes int8 weights"
+        assert w1.is_contiguous() and w2.is_contiguous(), "Expert weights must be contiguous"
         bsz = try_get_optimal_moe_config(w1.shape, w2.shape, topk, M)["BLOCK_SIZE_M"]
         if (
             bsz == 16
@@ -177,6 +183,14 @@ class FusedMoeW8A8(BaseMoeBackend):
             return _experts_from_routing(
                 hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, sorted_ids,
                 expert_ids, npp, topk, bsz, activation, apply_router_weight_on_input,
+            )
+        if H % 8 == 0 and hidden_states.is_contiguous() and gating_output.is_contiguous():
+            # router and hidden quantization in one launch (one wave per token)
+            topk_weights, topk_ids, q_h, s_h = moe_route_quant(gating_output, hidden_states, topk, renormalize)
+            sorted_ids, expert_ids, npp = moe_align_block_size(topk_ids, bsz, E)
+            return _experts_from_routing(
+                hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, sorted_ids, expert_ids,
+                npp, topk, bsz, activation, apply_router_weight_on_input,
             )
         topk_weights, topk_ids = fused_topk(hidden_states, gating_output, topk, renormalize)
         return fused_experts_impl_w8a8(

@@ -19,6 +19,7 @@ from minisgl_amd.kernel import (
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
     moe_prepare_small,
+    moe_route_quant,
     moe_sum_reduce,
     quant_per_token,
     topk_softmax,
@@ -112,6 +113,26 @@ def test_moe_prepare_small_equals_the_separate_kernels(M, E, k, renorm, H):
     s_ref, e_ref, n_ref = orc.moe_align_block_size(ids.cpu().numpy(), 16, E)
     assert int(npp.item()) == n_ref
     np.testing.assert_array_equal(sorted_ids.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("M,E,k,renorm,H", [(1, 128, 8, True, 2048), (16, 128, 8, True, 2048),
+                                            (300, 64, 2, False, 520), (4096, 128, 8, True, 2048),
+                                            (37, 300, 6, True, 1024)])
+def test_moe_route_quant_equals_the_separate_kernels(M, E, k, renorm, H):
+    """Router + hidden quantization in one launch: bit-identical to
+    topk_softmax and quant_per_token (which the oracle pins), bf16 logits
+    and fp32 logits."""
+    announce(f"route+quant M={M} E={E} k={k} H={H}")
+    gen = torch.Generator().manual_seed(M + E)
+    hid = torch.randn(M, H, generator=gen).to(torch.bfloat16).to(DEV)
+    for dt in (torch.bfloat16, torch.float32):
+        lg = torch.randn(M, E, generator=gen).to(dt).to(DEV)
+        w, ids, q, s = moe_route_quant(lg, hid, k, renorm)
+        w_ref, ids_ref = topk_softmax(lg, k, renorm)
+        q_ref, s_ref = quant_per_token(hid)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ids_ref) and torch.equal(w.view(torch.int32), w_ref.view(torch.int32))
+        assert torch.equal(q, q_ref) and torch.equal(s.view(torch.int32), s_ref.view(torch.int32))
 
 
 def test_moe_prepare_small_rejects_too_many_pairs():
