@@ -225,6 +225,33 @@ def test_gemm_every_tile_config(M, K, N):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
+@pytest.mark.parametrize("M,K,N,bias", [(4096, 128, 8192, False), (4000, 384, 8168, True), (4096, 256, 8192, True)])
+def test_gemm_persistent_two_tiles_per_block(M, K, N, bias):
+    """The persistent 256x256 walk (tile cfg 27) with 512 tiles: every
+    block runs two whole tiles back to back on one LDS ring, including a
+    one-stage K, edge tiles and a bias; bit-exact against the oracle."""
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm persistent two tiles M={M} K={K} N={N} bias={bias}")
+    gen = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
+    s_w = torch.rand(N, generator=gen) * 9e-3 + 1e-3
+    b = (torch.randn(N, generator=gen) * 0.1).to(torch.bfloat16) if bias else None
+    q, s = quant_per_token(x.to(DEV))
+    q_ref, s_ref = orc.quant_per_token(f32(x))
+    acc_ref = orc.gemm_i32(q_ref, w.numpy())
+    y_ref = orc.epilogue(acc_ref, s_ref, s_w.numpy(), bias=None if b is None else f32(b))
+    lib = load()
+    try:
+        lib.mw8_set_tuning(-1, 27, -1)
+        y = gemm_w8a8(q, s, w.to(DEV), s_w.to(DEV), None if b is None else b.to(DEV))
+        torch.cuda.synchronize()
+        assert bf16_bits_equal(y, y_ref).all()
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+
+
 NUM_DECODE_CFGS = 32  # kDecodeCfgs in csrc/gemm.hip
 
 
