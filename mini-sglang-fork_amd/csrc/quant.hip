@@ -5,7 +5,7 @@
 // act_rows:     x bf16 [R, 2d] (gate | up) -> a = bf16(act(g) * u) ->
 //               quantized exactly as above; optionally also writes a.
 //
-// One row is owned by TPR threads (64 = one wave, or 256 = four waves).
+// One row is owned by TPR threads (32 = half a wave, 64 = one wave, or 256 = four waves).
 // Each thread keeps VPT 16-byte vectors (8 bf16) of the row in registers,
 // so the row is read from HBM once: 16-byte coalesced loads, an integer
 // max over the sign-cleared bf16 bit patterns (monotone for finite
@@ -46,23 +46,26 @@ __device__ __forceinline__ void st_row8(uint2* p, uint2 v) {
   __builtin_nontemporal_store(u32x2{v.x, v.y}, reinterpret_cast<u32x2*>(p));
 }
 
+// Max over aligned groups of W lanes (W = 32: each half of the wave).
+template <int W = 64>
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
+  for (int off = W / 2; off >= 1; off >>= 1) {
     uint32_t o = __shfl_xor(v, off, 64);
     v = o > v ? o : v;
   }
   return v;
 }
 
-// Max over the TPR threads owning one row.  TPR == 64: pure wave
-// reduction.  TPR == 256: one row per block, cross-wave through LDS.
+// Max over the TPR threads owning one row.  TPR == 32 / 64: lanes of a
+// half wave / the wave.  TPR == 256: one row per block, cross-wave through
+// LDS.
 template <int TPR>
 __device__ __forceinline__ uint32_t row_max(uint32_t v, uint32_t* red) {
-  v = wave_max_u32(v);
-  if constexpr (TPR == 64) {
-    return v;
+  if constexpr (TPR <= 64) {
+    return wave_max_u32<TPR>(v);
   } else {
+    v = wave_max_u32(v);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(kBlock) void quant_rows_kernel(
   constexpr int kRowsPerBlock = kBlock / TPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
   const int t = threadIdx.x % TPR;
-  const bool live = row < M;  // uniform per wave (TPR >= 64)
+  const bool live = row < M;  // uniform per TPR lanes; every lane reaches row_max
   const int64_t nvec = K >> 3;
   const U16x8* xr = reinterpret_cast<const U16x8*>(x + (live ? row : 0) * ldx);
 
@@ -366,8 +369,15 @@ bool dispatch_rows(int64_t nvec, int64_t rows, hipStream_t st, Args... args) {
     Launch<TPR, VPT>::run(dim3(static_cast<unsigned>(blocks)), st, args...);
     return true;
   };
+  using I32 = std::integral_constant<int, 32>;
   using I64 = std::integral_constant<int, 64>;
   using I256 = std::integral_constant<int, 256>;
+  // two rows per wave where that keeps more lanes busy than one (short
+  // rows: the MoE activation at I = 768 is 96 vectors, 75% of 64 x 2)
+  if constexpr (Launch<32, 1>::kHalfWaveRows) {
+    if (nvec <= 32) return go(I32{}, std::integral_constant<int, 1>{});
+    if (nvec > 64 && nvec <= 96) return go(I32{}, std::integral_constant<int, 3>{});
+  }
   // few lanes idle on the last vector (K = 5120: 640 of 768 slots, K =
   // 17408: 2176 of 2304).  Rows past 512 vectors use 256-thread rows: one
   // wave per 5120-wide row measured slower for the fused RMSNorm.
@@ -389,6 +399,7 @@ bool dispatch_rows(int64_t nvec, int64_t rows, hipStream_t st, Args... args) {
 
 template <int TPR, int VPT>
 struct QuantLaunch {
+  static constexpr bool kHalfWaveRows = true;
   static void run(dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, int64_t M,
                   int64_t K, int8_t* q, int64_t ldq, float* s) {
     hipLaunchKernelGGL((quant_rows_kernel<TPR, VPT>), grid, dim3(kBlock), 0, st, x, ldx, M, K,
@@ -398,6 +409,7 @@ struct QuantLaunch {
 
 template <int TPR, int VPT>
 struct ActLaunch {
+  static constexpr bool kHalfWaveRows = true;
   static void run(dim3 grid, hipStream_t st, const uint16_t* x, int64_t R, int64_t d, int act,
                   int8_t* q, float* s, uint16_t* a_out) {
     if (act == 0)
@@ -411,6 +423,7 @@ struct ActLaunch {
 
 template <int TPR, int VPT>
 struct NormLaunch {
+  static constexpr bool kHalfWaveRows = false;
   static void run(dim3 grid, hipStream_t st, const uint16_t* x, uint16_t* res, const uint16_t* w,
                   float eps, int64_t M, int64_t H, int8_t* q, float* s, uint16_t* y) {
     if (res && q)

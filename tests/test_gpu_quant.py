@@ -28,7 +28,9 @@ def _check_quant(x_bf16: torch.Tensor):
     [(1, 1024), (1, 5120), (3, 8), (16, 1024), (64, 1024), (33, 5120), (5, 17408),
      (7, 25600), (2, 32768), (3, 40000), (4, 1004), (129, 2048), (1000, 768),
      # every (threads per row, vectors per thread) class of the row kernels
-     (2, 1280), (3, 3072), (5, 4104), (2, 6144), (2, 12288), (3, 8200)],
+     (2, 1280), (3, 3072), (5, 4104), (2, 6144), (2, 12288), (3, 8200),
+     # two rows per wave (32 threads per row): odd row counts leave half a wave idle
+     (37, 768), (5, 256), (9, 552), (4097, 768)],
 )
 def test_quant_seeded_bitexact(M, K):
     announce(f"quant M={M} K={K}")
@@ -81,7 +83,7 @@ def test_quant_rejects_bad_args():
 
 @pytest.mark.parametrize("act", ["silu", "gelu"])
 @pytest.mark.parametrize("R,two_d", [(1, 1536), (8, 1536), (300, 1536), (4, 34816), (3, 51200), (5, 32),
-                                     (3, 2560), (2, 8208), (2, 12288)])
+                                     (3, 2560), (2, 8208), (2, 12288), (37, 1536), (9, 1104)])
 def test_act_and_mul_quant(act, R, two_d):
     announce(f"act {act} R={R} 2d={two_d}")
     gen = torch.Generator().manual_seed(R + two_d)
