@@ -314,19 +314,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_prepare_kernel(
   align_body(ids, M * topk, slots, bsz, 1, sorted_ids, expert_ids, npp, max_padded, max_blocks, nbits, 0, 1);
 }
 
-// Router and hidden-state quantizer of one token per wave (both read only
-// their own token): the outputs of topk_softmax_kernel and quant_rows_kernel
-// bit for bit, from one launch.
+// Router and hidden-state quantizer of four tokens per block (both read
+// only their own token): waves 0-3 route tokens 4b .. 4b+3 while waves 4-7
+// quantize their rows, so the two latency chains overlap; the outputs of
+// topk_softmax_kernel and quant_rows_kernel bit for bit, from one launch.
 template <int VPL>
-__global__ __launch_bounds__(256) void route_quant_kernel(const void* logits, int is_bf16, int64_t M, int E,
+__global__ __launch_bounds__(512) void route_quant_kernel(const void* logits, int is_bf16, int64_t M, int E,
                                                           int topk, int renorm, const uint16_t* __restrict__ hidden,
                                                           int64_t H, float* __restrict__ tw,
                                                           int32_t* __restrict__ tid_out, int8_t* __restrict__ q,
                                                           float* __restrict__ s) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int w = threadIdx.x >> 6;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (w & 3);
   if (t >= M) return;  // whole waves
-  topk_token<VPL>(logits, is_bf16, t, E, topk, renorm, tw, tid_out, nullptr);
-  quant_row_wave(hidden + t * H, H, q + t * H, s + t);
+  if (w < 4) topk_token<VPL>(logits, is_bf16, t, E, topk, renorm, tw, tid_out, nullptr);
+  else quant_row_wave(hidden + t * H, H, q + t * H, s + t);
 }
 
 // ------------------------------------------------------------ slot sum
@@ -399,7 +401,7 @@ int moe_route_quant(const void* logits, int is_bf16, int64_t M, int E, int topk,
   const int vpl = (E + 63) / 64;
   auto go = [&](auto vpl_c) {
     constexpr int V = decltype(vpl_c)::value;
-    hipLaunchKernelGGL((route_quant_kernel<V>), dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0, st, logits,
+    hipLaunchKernelGGL((route_quant_kernel<V>), dim3(static_cast<unsigned>((M + 3) / 4)), dim3(512), 0, st, logits,
                        is_bf16, M, E, topk, renorm, static_cast<const uint16_t*>(hidden), H, topk_w, topk_ids, q, s);
   };
   if (vpl <= 1) go(std::integral_constant<int, 1>{});
