@@ -604,18 +604,18 @@ void launch_grouped_stream(const GemmArgs& g, unsigned blocks, int epi, hipStrea
 
 // 16- or 32-row alignment blocks on the LDS DMA ring (decode3 core,
 // gathered rows; TG token groups of 16).
-template <int WAVES, int D, int EPI, int TG = 1>
+template <int WAVES, int D, int EPI, int TG = 1, int RG = 1>
 void launch_grouped_ring(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  constexpr int kLds = DecodeRing<TG, WAVES, D>::kLds;
-  auto kern = decode3_gemm_kernel<TG, WAVES, D, EPI, SortedRows>;
+  constexpr int kLds = RG * DecodeRing<TG, WAVES, D>::kLds;
+  auto kern = decode3_gemm_kernel<TG, WAVES, D, EPI, SortedRows, RG>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((g.N + 15) / 16), blocks), dim3(64 * WAVES), kLds,
-                     st, g);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((g.N + 16 * RG - 1) / (16 * RG)), blocks), dim3(64 * WAVES),
+                     kLds, st, g);
 }
 
 template <int EPI>
@@ -626,13 +626,17 @@ void launch_grouped_ring_cfg(int cfg, const GemmArgs& g, unsigned blocks, hipStr
     case 3: launch_grouped_ring<2, 4, EPI>(g, blocks, st); break;
     case 4: launch_grouped_ring<2, 3, EPI>(g, blocks, st); break;
     case 5: launch_grouped_ring<4, 3, EPI>(g, blocks, st); break;
-    default: launch_grouped_ring<1, 6, EPI>(g, blocks, st); break;
+    case 6: launch_grouped_ring<1, 6, EPI>(g, blocks, st); break;
+    case 7: launch_grouped_ring<1, 3, EPI, 1, 2>(g, blocks, st); break;
+    default: launch_grouped_ring<2, 3, EPI, 1, 2>(g, blocks, st); break;
   }
 }
 
 // 16-row alignment blocks (decode MoE): moe_cfg 0 the register-streaming
 // core with the block's tokens gathered in LDS (K <= 4080), 1-6 the LDS DMA
-// ring with (waves, ring depth) = (1,4), (1,3), (2,4), (2,3), (4,3), (1,6).
+// ring with (waves, ring depth) = (1,4), (1,3), (2,4), (2,3), (4,3), (1,6),
+// 7-8 the ring over 32 weight rows per block, (1,3) and (2,3) (16-token
+// layer 102 and 111 us against 93 for cfg 2: fewer, larger blocks lose).
 // Measured on MI355X at config 3 (whole layer): 16 tokens 120 us (cfg 0)
 // -> 107 us (cfg 2), 64 tokens 156 -> 145 us; at 256 tokens the 64-row
 // tiles win (167 us against 210 for cfg 2 over 16-row blocks).
@@ -653,7 +657,7 @@ void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream
     return;
   }
   int cfg = g_moe_cfg.load(std::memory_order_relaxed);
-  if (cfg < 0 || cfg > 6) cfg = default_stream_cfg(g);
+  if (cfg < 0 || cfg > 8) cfg = default_stream_cfg(g);
   if (cfg == 0 && grouped_stream_fits(g.K)) {
     launch_grouped_stream(g, blocks, epi, st);
     return;

@@ -1507,10 +1507,10 @@ struct RingDrain<D, OPS, D> {
 // whatever N is; RG 16-row MFMA groups per block share the token fragments,
 // and rows past the block's range read zeros through the buffer range check
 // (no traffic) and are not stored.
-// Grouped use (SortedRows, RG = 1, alignment blocks of 16 * TG rows): grid y
-// is the alignment block; its expert's weights stream through the ring (16
-// rows per block), the token rows are gathered through sorted_ids (padding
-// rows read zeros), and the epilogue scatters to pair rows with the routed
+// Grouped use (SortedRows, alignment blocks of 16 * TG rows): grid y is the
+// alignment block; its expert's weights stream through the ring (16 RG rows
+// per block), the token rows are gathered through sorted_ids (padding rows
+// read zeros), and the epilogue scatters to pair rows with the routed
 // weight.
 template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
@@ -1519,7 +1519,6 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   constexpr int kOps = 4 * RG + 4 * TG;  // vector memory ops per stage (DMA + token loads)
   static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
   static_assert(!Rows::kRuns, "grouped rows: one alignment block per block");
-  static_assert(RG == 1 || !Rows::kGrouped, "grouped rows: 16 weight rows per block");
   extern __shared__ __align__(16) unsigned char ring[];
   __shared__ int32_t red[kAcc][64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1537,8 +1536,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   }
   int64_t n0, rows;
   if constexpr (Rows::kGrouped) {
-    n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    rows = g.N - n0 < 16 ? g.N - n0 : 16;
+    n0 = static_cast<int64_t>(blockIdx.x) * (16 * RG);
+    rows = g.N - n0 < 16 * RG ? g.N - n0 : 16 * RG;
   } else {
     n0 = g.N * blockIdx.x / gridDim.x;
     rows = g.N * (blockIdx.x + 1) / gridDim.x - n0;
@@ -1617,13 +1616,14 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   for (int u = 0; u < (kPre ? kEpiPerThread : 0); ++u) {
     const int e = tid + u * 64 * WAVES;
     const int j = e >> 6, l = e & 63;
-    const int tg = j / 4, v = j & 3;
-    const int64_t n = n0 + 4 * (l >> 4) + v;
+    const int tg = (j / 4) % TG, v = j & 3;
+    const int nl = 16 * (j / (4 * TG)) + 4 * (l >> 4) + v;  // row within the block's range
+    const int64_t n = n0 + nl;
     e_orow[u] = -1;
     e_sa[u] = 0.0f;
     e_sw[u] = 0.0f;
     e_x[u] = 0.0f;
-    if (e >= kAcc * 64 || n >= g.N) continue;
+    if (e >= kAcc * 64 || nl >= rows) continue;
     int32_t arow;
     if constexpr (Rows::kGrouped) {
       const int32_t p = g.sorted_ids[m0 + 16 * tg + (l & 15)];
@@ -1727,7 +1727,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     }
   }
   if constexpr (Rows::kGrouped && EPI == kEpiBf16Sum) {
-    slot_sum_step(g, 16 * TG, n0, 16, [&](int r) {
+    slot_sum_step(g, 16 * TG, n0, 16 * RG, [&](int r) {
       const int32_t p = g.sorted_ids[m0 + r];
       return p < g.num_valid ? p : -1;
     });

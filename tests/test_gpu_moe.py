@@ -298,7 +298,7 @@ def test_fused_activation_gemm_equals_gemm_then_activation(shape, B):
             assert torch.equal(a.view(torch.int16), a_ref.view(torch.int16)), f"{act_name} routed={routed}"
 
 
-NUM_SMALL_CFGS = 7  # 16-row block configurations in csrc/gemm.hip (0: register streaming, 1-6: DMA ring)
+NUM_SMALL_CFGS = 9  # 16-row block configurations in csrc/gemm.hip (0: register streaming, 1-6: DMA ring, 7-8: ring over 32 weight rows)
 
 
 @pytest.mark.parametrize("shape", ["cfg3", "ragged", "longk"])
