@@ -67,7 +67,8 @@ int mw8_quant_per_token_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, i
  * Fused activation + requant: x bf16 [R, 2d] (gate | up) ->
  * a = bf16(act(gate) * up), then quantized like mw8_quant_per_token_bf16 into
  * q int8 [R, d], s fp32 [R].  act: 0 = silu, 1 = gelu (erf).  act_out
- * (bf16 [R, d]) is optional and receives a.  2d % 16 == 0.
+ * (bf16 [R, d]) is optional and receives a.  q and s may both be NULL when
+ * act_out is given (activation only, no requant).  2d % 16 == 0.
  * Replaces silu_and_mul / gelu_and_mul (python/minisgl/layers/activation.py:9-18)
  * as called at python/minisgl/moe/fused.py:206-207 and
  * python/minisgl/models/utils.py:48, fused with the requant of the next GEMM.
@@ -94,30 +95,61 @@ int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, fl
                            int64_t H, int8_t* q, float* s, void* y, mw8_stream_t stream);
 
 /*
+ * Plain RMSNorm over strided rows: rows are addressed as [G, inner, H] --
+ * row (g, i) of x at x + g * ldx + i * H, of y at y + g * ldy + i * H
+ * (elements; the inner rows contiguous) -- with the numerics of
+ * mw8_rmsnorm_quant_bf16 (no residual, no quantization).  y may equal x
+ * (in place).  H % 8 == 0, H <= 32768, ldx and ldy multiples of 8 and
+ * >= inner * H, x, y and weight 16-byte aligned.
+ * Replaces flashinfer rmsnorm on the per-head views of a qkv row
+ * (RMSNorm.forward_inplace(q.view(-1, heads, head_dim)),
+ * python/minisgl/layers/norm.py:18-19, called at
+ * python/minisgl/layers/attention.py:49-53), which are not contiguous.
+ */
+int mw8_rmsnorm_strided_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, const void* weight,
+                             float eps, int64_t G, int64_t inner, int64_t H, mw8_stream_t stream);
+
+/*
  * Tile-configuration override, process-wide: decode_cfg indexes the dense
  * decode-core configurations (forcing one keeps M <= 64 on the decode
  * core), tile_cfg the dense tile-core ones (forcing one takes M > 32 to the
- * tile core), moe_cfg the grouped (fused-MoE) configurations (tile or
- * persistent configurations for block sizes 64 and 128, small-block ones
- * for block size 16); -1 restores the automatic choice.  Results do not depend on the
+ * tile core), moe_cfg the grouped (fused-MoE) configurations (for block
+ * sizes 64 and 128, and separately numbered for block size 16); -1
+ * restores the automatic choice.  Results do not depend on the
  * configuration (exact integer accumulation).  Tuning hook; no reference
  * counterpart.
  */
 void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 
 /*
+ * Number of configurations mw8_set_tuning accepts: kind 0 decode, 1 tile,
+ * 2 grouped (64/128-row blocks), 3 grouped (16-row blocks); 0 for other
+ * kinds.  Tuning hook; no reference counterpart.
+ */
+int32_t mw8_tuning_count(int32_t kind);
+
+/*
  * Bytes of workspace mw8_gemm_w8a8_* uses for (M, N, K): the int32 partial
  * tiles of the tile core's K split (for the tiling the call will choose,
- * including a mw8_set_tuning override: with T tiles and S = 256 x resident
+ * including a mw8_set_tuning override: with T tiles and S = CUs x resident
  * blocks per CU, the r = T mod S tiles of the last partial wave, all T when
  * T < S, are cut into sp = min(S / r, K / BK, 16) K ranges when sp >= 2;
  * each range writes one BM x BN int32 tile, summed in range order by a
- * second kernel on the same stream).  0 when no split applies.  A NULL or smaller
- * workspace is not an error: the GEMM then runs every tile whole (same
- * result, slower).  The workspace holds no state between calls; calls that
- * share one must be ordered (one stream).  No reference counterpart.
+ * second kernel on the same stream).  0 when no split applies.  A NULL or
+ * smaller workspace is not an error: the GEMM then runs every tile whole
+ * (same result, slower).  The workspace holds no state between calls;
+ * calls that share one must be ordered (one stream).  No reference
+ * counterpart.
  */
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * Upper bound of mw8_gemm_workspace_bytes over every (M, N, K) and tuning
+ * override on the current device (r x sp <= S, so S x the largest split
+ * tile): a caller that reserves this once never has to grow the workspace,
+ * e.g. between HIP graph captures.  No reference counterpart.
+ */
+size_t mw8_gemm_workspace_max_bytes(void);
 
 /*
  * W8A8 linear: y bf16 [M, N] = epilogue(A int8 [M, K] . W int8 [N, K]^T,
@@ -179,33 +211,6 @@ int mw8_moe_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, co
                            const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
                            int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
                            int32_t block_size, void* out, mw8_stream_t stream);
-
-/*
- * The MoE layer's down-projection GEMM with the slot sum fused in.  For
- * every sorted position r below *num_post_pad with p = sorted_ids[r] <
- * num_valid (p = token * top_k + slot):
- *   cache[p, :] = epilogue(A[p] . W[e]^T, sa[p], sw[e], routed = topk_w[p])
- * as mw8_moe_gemm_w8a8_bf16 with top_k = 1, and then
- *   out[t, :] = bf16(sum over slots i = 0 .. top_k-1, in order, in fp32 of cache[t * top_k + i, :])
- * as mw8_moe_sum_reduce_bf16 -- the same bits.  The block that writes the
- * last of a token's top_k slots for a 16-column group sums that group, so
- * no second launch runs.  counters int32 [num_valid / top_k, ceil(N/16)]
- * carry the count between blocks: zero-fill them once before their first
- * use; every call leaves them zero (calls that share them must be ordered
- * on one stream).  Every pair's expert must lie in [0, E) (a block of an
- * expert outside it writes nothing, and its tokens get no sum).  A int8
- * [num_valid, K], W int8 [E, N, K], sw fp32 [E, N], cache bf16 [num_valid,
- * N], out bf16 [num_valid / top_k, N]; N % 8 == 0, K % 64 == 0,
- * block_size in {16, 32, 64, 128}, 16-byte aligned A, W, cache and out.
- * Replaces fused_moe_kernel (GEMM2, MUL_ROUTED_WEIGHT) + moe_sum_reduce
- * (python/minisgl/moe/fused.py:212-226, python/minisgl/kernel/moe_impl.py:65-98).
- */
-int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                               const int32_t* sorted_ids, const int32_t* expert_ids,
-                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
-                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
-                               int32_t block_size, void* cache, void* out, int32_t* counters,
-                               mw8_stream_t stream);
 
 /*
  * Gate|up grouped GEMM with the gated activation fused into its epilogue:

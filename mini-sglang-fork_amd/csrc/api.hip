@@ -29,7 +29,9 @@ int check_launch(const char* what) {
 int quant_per_token_bf16(const void*, int64_t, int64_t, int64_t, int8_t*, int64_t, float*, hipStream_t);
 int act_and_mul_quant_bf16(const void*, int64_t, int64_t, int, int8_t*, float*, void*, hipStream_t);
 size_t gemm_workspace_bytes(int64_t, int64_t, int64_t);
+size_t gemm_workspace_max_bytes();
 void set_tuning(int, int, int);
+int tuning_count(int);
 int gemm_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, const void*, void*,
                    int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 int gemm_w8a8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, void*, size_t,
@@ -43,9 +45,6 @@ int moe_gemm_act_w8a8(const int8_t*, const float*, const int8_t*, const float*, 
                       int64_t, int, int, int, void*, hipStream_t);
 int moe_route_quant(const void*, int, int64_t, int, int, int, const void*, int64_t, float*, int32_t*, int8_t*,
                     float*, hipStream_t);
-int moe_gemm_sum_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
-                      const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
-                      int64_t, int, int, void*, void*, int32_t*, hipStream_t);
 int moe_prepare_small(const void*, int, int64_t, int, int, int, const void*, int64_t, float*, int32_t*,
                       int8_t*, float*, int, int, int32_t*, int32_t*, int32_t*, hipStream_t);
 int moe_gemm_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
@@ -53,6 +52,8 @@ int moe_gemm_w8a8(const int8_t*, const float*, const int8_t*, const float*, cons
                   int64_t, int, int, void*, int, hipStream_t);
 int rmsnorm_quant_bf16(const void*, void*, const void*, float, int64_t, int64_t, int8_t*, float*, void*,
                        hipStream_t);
+int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, float, int64_t, int64_t, int64_t,
+                         hipStream_t);
 int64_t calib_sink_len();
 int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
 int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
@@ -74,7 +75,7 @@ extern "C" {
 
 const char* mw8_last_error(void) { return mw8::g_last_error; }
 
-int mw8_version(void) { return 100; }
+int mw8_version(void) { return 200; }
 
 int mw8_device_info(int32_t device, int32_t* num_cu, int32_t* clock_khz, int64_t* l2_bytes) {
   MW8_REQUIRE(num_cu && clock_khz && l2_bytes, mw8::kErrArg, "device_info: null pointer");
@@ -104,6 +105,10 @@ void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg) {
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return mw8::gemm_workspace_bytes(M, N, K);
 }
+
+size_t mw8_gemm_workspace_max_bytes(void) { return mw8::gemm_workspace_max_bytes(); }
+
+int32_t mw8_tuning_count(int32_t kind) { return mw8::tuning_count(kind); }
 
 int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,
@@ -157,16 +162,6 @@ int mw8_moe_gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W
                                    top_k, num_valid, N, K, E, block_size, act, out, S(stream)));
 }
 
-int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                               const int32_t* sorted_ids, const int32_t* expert_ids,
-                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
-                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E,
-                               int32_t block_size, void* cache, void* out, int32_t* counters,
-                               mw8_stream_t stream) {
-  MW8_ENTRY(mw8::moe_gemm_sum_w8a8(A, sa, W, sw, sorted_ids, expert_ids, num_post_pad, max_sorted, topk_w,
-                                   top_k, num_valid, N, K, E, block_size, cache, out, counters, S(stream)));
-}
-
 int mw8_moe_route_quant(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,
                         int32_t renorm, const void* hidden, int64_t H, float* topk_w, int32_t* topk_ids,
                         int8_t* q, float* s, mw8_stream_t stream) {
@@ -191,6 +186,11 @@ int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, voi
 int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, float eps, int64_t M,
                            int64_t H, int8_t* q, float* s, void* y, mw8_stream_t st) {
   MW8_ENTRY(mw8::rmsnorm_quant_bf16(x, residual, weight, eps, M, H, q, s, y, S(st)));
+}
+
+int mw8_rmsnorm_strided_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, const void* weight, float eps,
+                             int64_t G, int64_t inner, int64_t H, mw8_stream_t st) {
+  MW8_ENTRY(mw8::rmsnorm_strided_bf16(x, ldx, y, ldy, weight, eps, G, inner, H, S(st)));
 }
 
 int64_t mw8_calib_sink_len(void) { return mw8::calib_sink_len(); }

@@ -8,18 +8,18 @@
 //   out[row, n]         bf16 (scaled epilogue) or int32 (raw accumulators)
 //
 // Cores:
-//   tile_core   -- large M (prefill): BM x BN x 128 block tile, 4 waves, each
-//                  wave a (BM/WM) x (BN/WN) tile of v_mfma_i32_32x32x32_i8,
-//                  A/W tiles double-buffered in LDS with an XOR swizzle of
-//                  16-byte chunks (chunk ^ (row & 7)) so that the 32 rows
-//                  read by one MFMA fragment load hit distinct banks.
-//   decode_gemm_kernel   -- dense small M (decode): weight streaming with
-//                  v_mfma_i32_16x16x64_i8, weight rows as the MFMA "A"
-//                  operand read straight from HBM into registers, up to 64
-//                  tokens as the "B" operand, K split across the waves of a
-//                  block and reduced in LDS.
-//   grouped_stream_kernel -- the same streaming idea for 16-row expert
-//                  blocks of the fused-MoE GEMM (token rows gathered in LDS).
+//   tile_gemm_kernel  -- register-staged MFMA tile (any K % 16 == 0).
+//   tile3_gemm_kernel -- the large-M ring: direct-to-LDS DMA of A and W
+//                  tiles, NSTAGE-deep ring, v_mfma_i32_32x32x32_i8, K split
+//                  of the last partial wave of tiles (split_reduce_kernel).
+//   grouped_persist_kernel -- the same ring walking (expert chunk, column
+//                  tile) items of the fused-MoE GEMM.
+//   decode_gemm_kernel / decode3_gemm_kernel -- dense small M (decode):
+//                  weight streaming with v_mfma_i32_16x16x64_i8, weight rows
+//                  as the MFMA "A" operand, up to 64 tokens as the "B"
+//                  operand, K split across the waves of a block and reduced
+//                  in LDS; decode3 streams through a per-wave LDS DMA ring
+//                  and also serves 16/32-row fused-MoE alignment blocks.
 //
 // MFMA lane layouts (checked on gfx950 by an in-bounds probe):
 //   32x32x32: lane l feeds A row l%32 / B col l%32 with 16 K-bytes of group
@@ -34,10 +34,8 @@
 
 namespace mw8 {
 
-// kEpiBf16Sum: the bf16 epilogue of the MoE layer's GEMM2 followed by the
-// fused slot sum (slot_sum_step); instantiated only for that entry point.
-enum EpiKind : int { kEpiBf16 = 0, kEpiI32 = 1, kEpiBf16Sum = 2 };
-constexpr bool epi_bf16_out(int e) { return e != kEpiI32; }
+enum EpiKind : int { kEpiBf16 = 0, kEpiI32 = 1 };
+constexpr bool epi_bf16_out(int e) { return e == kEpiBf16; }
 
 // Everything a core needs to know about rows, experts and the epilogue.
 struct GemmArgs {
@@ -73,12 +71,6 @@ struct GemmArgs {
   // blocks behind expert_ids / num_post_pad (the tile height BM is a
   // multiple of it)
   int32_t align_bsz;
-  // fused slot sum (EPI kEpiBf16Sum, slot_sum_step): sum_out bf16
-  // [num_valid / sum_k][N], sum_cnt int32 [num_valid / sum_k][ceil(N/16)]
-  // (zero on entry, left zero)
-  uint16_t* sum_out;
-  int32_t* sum_cnt;
-  int32_t sum_k;
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -89,27 +81,10 @@ __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, co
   return f32_to_bf16(t);
 }
 
-// Output stores of a grouped bf16 epilogue.  With the fused slot sum
-// (kEpiBf16Sum) the rows are read back by other blocks in the same launch,
-// so they are written as device-scope (agent) atomic stores, which the
-// compiler emits as stores coherent across the XCDs' L2 caches; otherwise
-// non-temporal.
-__device__ __forceinline__ void store_out16(uint16_t* dst, v4i d, bool coherent) {
-  if (coherent) {
-    uint64_t* q = reinterpret_cast<uint64_t*>(dst);
-    __hip_atomic_store(q, static_cast<uint64_t>(static_cast<uint32_t>(d[0])) |
-                              (static_cast<uint64_t>(static_cast<uint32_t>(d[1])) << 32),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 1, static_cast<uint64_t>(static_cast<uint32_t>(d[2])) |
-                                  (static_cast<uint64_t>(static_cast<uint32_t>(d[3])) << 32),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(dst));
-  }
-}
-__device__ __forceinline__ void store_out1(uint16_t* dst, uint16_t v, bool coherent) {
-  if (coherent) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *dst = v;
+// Output stores of a bf16 epilogue: 16-byte rows non-temporal (the output is
+// written once; gate_up M=8192 1405 -> 1377 us on MI355X).
+__device__ __forceinline__ void store_out16(uint16_t* dst, v4i d) {
+  __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(dst));
 }
 
 // ------------------------------------------------------------------------
@@ -434,76 +409,6 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// Fused slot sum (the MoE layer's GEMM2, routed weight applied): after a
-// block has stored its output rows -- row r of the block holds pair
-// row_p(r) (-1: none) for columns [n0, n0 + ncols) -- it counts, per
-// (token p / sum_k, 16-column group), the slots it completed.  The block
-// whose count completes a group's sum_k slots sums the token's sum_k rows
-// of out in slot order in fp32 (moe_sum_reduce_kernel's arithmetic) into
-// sum_out and resets the counter to zero for the next call.  The rows are
-// exchanged through device-coherent accesses only (store_out* with the
-// slot sum, agent-scope atomic loads here): every wave waits until its
-// stores have completed before the block counts, and the completing thread
-// issues its loads after its count has returned.  No cache write-back or
-// invalidation is needed (a device-scope fence per block, which writes back
-// the XCD's L2, made the launch several times slower than the separate sum
-// kernel), and no block waits for another.  Needs N % 8 == 0 and 16-byte
-// aligned out / sum_out.
-template <class RowP>
-__device__ __forceinline__ void slot_sum_step(const GemmArgs& g, int nrows, int64_t n0, int ncols, RowP row_p) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's coherent stores have completed
-  __syncthreads();
-  const int groups = ncols / 16;
-  const int64_t G = (g.N + 15) / 16;
-  const int k = g.sum_k;
-  for (int it = threadIdx.x; it < nrows * groups; it += blockDim.x) {
-    const int r = it / groups;
-    const int64_t n = n0 + 16 * (it % groups);
-    const int32_t p = row_p(r);
-    if (p < 0 || n >= g.N) continue;
-    const int64_t t = p / k;
-    int32_t* cnt = g.sum_cnt + t * G + n / 16;
-    if (atomicAdd(cnt, 1) != k - 1) continue;
-    *cnt = 0;
-    const bool two = n + 8 < g.N;  // N % 8 == 0: the group holds 8 or 16 columns
-    const uint64_t* src = reinterpret_cast<const uint64_t*>(static_cast<const uint16_t*>(g.out) + t * k * g.ldo + n);
-    const int64_t ld64 = g.ldo / 4;
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-    for (int i = 0; i < k; ++i) {
-      uint64_t w[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-        w[h] = (h < 2 || two) ? __hip_atomic_load(src + i * ld64 + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : uint64_t{0};
-      const v4i lo = v4i{static_cast<int>(w[0]), static_cast<int>(w[0] >> 32), static_cast<int>(w[1]),
-                         static_cast<int>(w[1] >> 32)};
-      const v4i hi = v4i{static_cast<int>(w[2]), static_cast<int>(w[2] >> 32), static_cast<int>(w[3]),
-                         static_cast<int>(w[3] >> 32)};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t a = static_cast<uint32_t>(lo[j]), b = static_cast<uint32_t>(hi[j]);
-        acc[2 * j] = acc[2 * j] + bf16_to_f32(static_cast<uint16_t>(a & 0xFFFFu));
-        acc[2 * j + 1] = acc[2 * j + 1] + bf16_to_f32(static_cast<uint16_t>(a >> 16));
-        acc[8 + 2 * j] = acc[8 + 2 * j] + bf16_to_f32(static_cast<uint16_t>(b & 0xFFFFu));
-        acc[8 + 2 * j + 1] = acc[8 + 2 * j + 1] + bf16_to_f32(static_cast<uint16_t>(b >> 16));
-      }
-    }
-    v4i o0, o1;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o0[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[2 * j])) |
-                               (static_cast<uint32_t>(f32_to_bf16(acc[2 * j + 1])) << 16));
-      o1[j] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(acc[8 + 2 * j])) |
-                               (static_cast<uint32_t>(f32_to_bf16(acc[8 + 2 * j + 1])) << 16));
-    }
-    uint16_t* dst = g.sum_out + t * g.N + n;
-    *reinterpret_cast<v4i*>(dst) = o0;
-    if (two) *reinterpret_cast<v4i*>(dst + 8) = o1;
-  }
 }
 
 // One BM x BN output tile over K stages [kt_begin, kt_end) of the ring core.
@@ -858,11 +763,9 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         const int64_t n = n0 + ch * 8;
         if (orow >= 0 && n < g.N) {
           const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
-          // non-temporal: the output is written once (gate_up M=8192 1405 -> 1377 us)
-          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d, EPI == kEpiBf16Sum);
+          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d);
         }
       }
-      if constexpr (EPI == kEpiBf16Sum) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
       return;
     }
   }
@@ -895,16 +798,14 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
         if constexpr (epi_bf16_out(EPI)) {
-          store_out1(static_cast<uint16_t*>(g.out) + orow * g.ldo + n,
-                     epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr),
-                     EPI == kEpiBf16Sum);
+          static_cast<uint16_t*>(g.out)[orow * g.ldo + n] =
+              epi_bf16(a, sa, sw[n], g.bias, n, routed, g.topk_w != nullptr);
         } else {
           static_cast<int32_t*>(g.out)[orow * g.ldo + n] = a;
         }
       }
     }
   }
-  if constexpr (EPI == kEpiBf16Sum) slot_sum_step(g, BM, n0, BN, [&](int r) { return meta_p[r]; });
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -939,83 +840,20 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // pass only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
   extern __shared__ __align__(16) unsigned char lds[];
-  const int lane = threadIdx.x & 63;
-  const int8_t* W = g.W;
-  const float* sw = g.sw;
-  int64_t m0, n0;
-  int64_t split_unit = -1;  // split-tail unit (writes an int32 partial tile), -1: whole tile
-  int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
-  int rows_valid = BM;      // tile rows that hold sorted positions of this tile's run
-  // grouped grids: x = N tile, y = alignment block (an XCD-contiguous walk
-  // of the (block, N tile) pairs measured slower at 256 and 1024 tokens)
-  const int64_t gx = blockIdx.x, gy = blockIdx.y;
-  if constexpr (Rows::kRuns) {
-    n0 = gx * BN;
-    const int ab = g.align_bsz;
-    const int64_t y = gy;
-    const int64_t npp = *g.num_post_pad;
-    if (y * ab >= npp) return;
-    const int e = g.expert_ids[y];
-    if (e < 0 || e >= g.num_experts) return;
-    // distance j from the first alignment block of expert e: expert_ids is
-    // non-decreasing over the used blocks, so scan back 64 blocks per step
-    // for the nearest block of another expert (index < 0 counts as one)
-    int64_t first = 0;
-    for (int64_t base = y;; base -= 64) {
-      const int64_t idx = base - lane;
-      const int v = idx >= 0 ? g.expert_ids[idx] : -2;
-      const uint64_t other = __ballot(v != e);
-      if (other != 0) {
-        first = base - (__ffsll(static_cast<unsigned long long>(other)) - 1) + 1;
-        break;
-      }
-    }
-    const int per_tile = BM / ab;
-    if ((y - first) % per_tile != 0) return;
-    const int64_t used = npp / ab;
-    const int64_t nxt = y + lane;
-    const int same = (lane < per_tile && nxt < used) ? (g.expert_ids[nxt] == e) : 0;
-    const uint64_t run = __ballot(same != 0);
-    rows_valid = ab * __popcll(run);  // the run's blocks are contiguous from y
-    m0 = y * ab;
-    W += static_cast<int64_t>(e) * g.N * g.K;
-    sw += static_cast<int64_t>(e) * g.N;
-  } else if constexpr (Rows::kGrouped) {
-    n0 = gx * BN;
-    m0 = gy * BM;
+  static_assert(!Rows::kRuns, "run tiles are walked by grouped_persist_kernel");
+  if constexpr (Rows::kGrouped) {
+    // grouped grid: x = N tile, y = alignment block of BM sorted rows (an
+    // XCD-contiguous walk of the (block, N tile) pairs measured slower at
+    // 256 and 1024 tokens)
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN, m0 = static_cast<int64_t>(blockIdx.y) * BM;
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
-    const int e = g.expert_ids[gy];
+    const int e = g.expert_ids[blockIdx.y];
     if (e < 0 || e >= g.num_experts) return;
-    W += static_cast<int64_t>(e) * g.N * g.K;
-    sw += static_cast<int64_t>(e) * g.N;
+    const TileJob job{m0, n0, g.W + static_cast<int64_t>(e) * g.N * g.K, g.sw + static_cast<int64_t>(e) * g.N,
+                      0, static_cast<int>(g.K / BK), BM, -1};
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
   } else {
     tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, dense_tile_job<BM, BN, BK>(g, blockIdx.x));
-    return;
-  }
-
-  TileJob job{m0, n0, W, sw, kt_begin, kt_end, rows_valid, split_unit};
-  tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
-#endif  // __HIP_DEVICE_COMPILE__
-}
-
-// Persistent dense ring GEMM: gridDim.x resident blocks (a multiple of the
-// XCD count) walk the units of tile3_gemm_kernel's grid -- unit u runs on
-// block u % gridDim.x, so on the same XCD as in the one-block-per-unit
-// launch -- with one barrier between units (the staged epilogue's LDS reads
-// and metadata tables are done before the next unit's DMA refills the
-// ring).  The previous unit's output stores drain while the next unit's
-// first stages load: the stage waits count loads, which complete in issue
-// order among themselves, so stores still in flight only make them wait
-// longer, never shorter.
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI>
-__global__ __launch_bounds__(64 * WM * WN) void tile3_persist_kernel(GemmArgs g) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  extern __shared__ __align__(16) unsigned char lds[];
-  const int64_t tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  const int64_t units = g.tail_split > 1 ? g.full_tiles + (tiles - g.full_tiles) * g.tail_split : tiles;
-  for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, DenseRows>(g, lds, dense_tile_job<BM, BN, BK>(g, u));
-    __syncthreads();
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -1141,102 +979,6 @@ void grouped_persist_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
-// Grouped small-block core (fused-MoE decode): weight streaming
-// ------------------------------------------------------------------------
-// Block = 4 waves = 64 weight rows of one expert; wave w owns rows
-// n0 + 16w .. +16.  The block's 16 sorted (token, slot) rows are gathered
-// once into an LDS panel [16][K] (zeros for padding rows); per 256-K step a
-// lane streams 64 contiguous weight bytes (4 x 16 B) from HBM into
-// registers and issues 4 v_mfma_i32_16x16x64_i8 with the weight rows as
-// the MFMA rows.  Grid (N/64, expert blocks); blocks past the padded count
-// exit on the device-side count.
-constexpr int kStreamRows = 64;
-constexpr int kStreamStep = 256;  // K bytes per lane step (4 MFMAs)
-
-template <int EPI>
-__global__ __launch_bounds__(256) void grouped_stream_kernel(GemmArgs g) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kStreamRows;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16;
-  if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
-  const int e = g.expert_ids[blockIdx.y];
-  if (e < 0 || e >= g.num_experts) return;
-  const int8_t* W = g.W + static_cast<int64_t>(e) * g.N * g.K;
-  const float* sw = g.sw + static_cast<int64_t>(e) * g.N;
-  const int kc = static_cast<int>(g.K);
-  const int kc_pad = ((kc + kStreamStep - 1) / kStreamStep) * kStreamStep;
-  const int ldl = kc_pad + 16;  // padded LDS row: 16 token rows hit 16 bank groups
-
-  // ---- gather the block's 16 token rows into LDS (zeros outside)
-  {
-    const int chunks_per_row = kc_pad / 16;
-    for (int id = tid; id < 16 * chunks_per_row; id += 256) {
-      const int r = id / chunks_per_row, c = id % chunks_per_row;
-      const int32_t p = g.sorted_ids[m0 + r];
-      v4i v = v4i{0};
-      if (p < g.num_valid && 16 * c < kc)
-        v = *reinterpret_cast<const v4i*>(g.A + static_cast<int64_t>(p / g.top_k) * g.lda + 16 * c);
-      *reinterpret_cast<v4i*>(lds + r * ldl + 16 * c) = v;
-    }
-  }
-  __syncthreads();
-
-  const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t wrow = n0 + 16 * wave + r16;
-  const int8_t* wp = W + (wrow < g.N ? wrow : g.N - 1) * g.K + 64 * grp;
-  v4i acc = v4i{0};
-  const int steps = kc_pad / kStreamStep;
-  int s = 0;
-  for (; s + 2 <= steps; s += 2) {
-    v4i w[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int koff = s * kStreamStep + (j >> 2) * kStreamStep + 16 * (j & 3);
-      w[j] = (koff + 64 * grp < kc) ? *reinterpret_cast<const v4i*>(wp + koff) : v4i{0};
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kk = (s + (j >> 2)) * kStreamStep + 64 * grp + 16 * (j & 3);
-      const v4i b = *reinterpret_cast<const v4i*>(lds + r16 * ldl + kk);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc, 0, 0, 0);
-    }
-  }
-  for (; s < steps; ++s) {
-    v4i w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int koff = s * kStreamStep + 16 * j;
-      w[j] = (koff + 64 * grp < kc) ? *reinterpret_cast<const v4i*>(wp + koff) : v4i{0};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kk = s * kStreamStep + 64 * grp + 16 * j;
-      const v4i b = *reinterpret_cast<const v4i*>(lds + r16 * ldl + kk);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], b, acc, 0, 0, 0);
-    }
-  }
-
-  // D reg v of lane l: weight row n0 + 16*wave + 4*(l/16) + v, token row l%16
-  const int64_t nb = n0 + 16 * wave + 4 * grp;
-  const int32_t p = g.sorted_ids[m0 + r16];
-  if (p >= g.num_valid) return;
-  const int64_t arow = p / g.top_k;
-  const float sa = EPI == kEpiBf16 ? g.sa[arow] : 0.0f;
-  const float routed = g.topk_w ? g.topk_w[p] : 1.0f;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int64_t n = nb + v;
-    if (n >= g.N) continue;
-    if constexpr (EPI == kEpiBf16)
-      static_cast<uint16_t*>(g.out)[p * g.ldo + n] =
-          epi_bf16(acc[v], sa, sw[n], nullptr, n, routed, g.topk_w != nullptr);
-    else
-      static_cast<int32_t*>(g.out)[p * g.ldo + n] = acc[v];
-  }
-}
-
-// ------------------------------------------------------------------------
 // Dense small-M core: weight streaming with in-block split-K
 // ------------------------------------------------------------------------
 // Block = WAVES waves over the same RG*16 weight rows; wave w accumulates
@@ -1324,129 +1066,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_gemm_kernel(GemmArgs g) {
   }
 }
 
-// ------------------------------------------------------------------------
-// Dense small-M core, pipelined: weight streaming with every load batch in
-// flight while the previous batch's MFMAs run
-// ------------------------------------------------------------------------
-// Same data mapping and in-block K split as decode_gemm_kernel, restructured
-// for memory-level parallelism: wave w streams K steps [s_begin, s_end) of
-// the block's RG*16 weight rows in batches of U 64-byte steps; batch b+1 is
-// requested before the MFMAs of batch b (two register sets, the phase order
-// pinned with scheduling barriers).  No load is predicated: weight loads
-// read a clamped in-bounds address, and the token operand of a step past
-// the wave's range, of K bytes past the row end, or of a token row >= M is
-// read from a block of zeros instead, so its products vanish and no select
-// waits on loaded data.  With WAVES up to 16 (1024-thread blocks) a block
-// keeps WAVES * U * RG KB of weights in flight, enough to request a whole
-// 26-89 MB weight matrix almost at once.
-// Never written: a global (not constant) object, so that a select between it
-// and a kernel-argument pointer still yields a global-memory load.
+// A block of zeros the decode cores read in place of a token row past M (or
+// of K bytes past a row end).  Never written: a global (not constant)
+// object, so that a select between it and a kernel-argument pointer still
+// yields a global-memory load.
 __device__ __align__(16) int8_t kZeroChunk[16] = {0};
-
-template <int RG, int TG, int WAVES, int U, int EPI>
-__global__ __launch_bounds__(64 * WAVES) void decode2_gemm_kernel(GemmArgs g) {
-  constexpr int kAcc = RG * TG * 4;  // int32 accumulators per lane
-  __shared__ int32_t red[kAcc][64];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) (&red[0][0])[e] = 0;
-  const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * RG);
-  const int64_t steps = (g.K + 63) / 64;
-  const int64_t s_begin = steps * wave / WAVES, s_end = steps * (wave + 1) / WAVES;
-  const int64_t k_last = g.K - 16;  // last valid 16-byte chunk start (K % 16 == 0)
-
-  const int8_t* wp[RG];
-#pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
-    const int64_t n = n0 + 16 * rg + r16;
-    wp[rg] = g.W + (n < g.N ? n : g.N - 1) * g.K;
-  }
-  const int8_t* xp[TG];
-  bool xok[TG];
-#pragma unroll
-  for (int tg = 0; tg < TG; ++tg) {
-    const int64_t m = 16 * tg + r16;
-    xok[tg] = m < g.M;
-    xp[tg] = g.A + (xok[tg] ? m : 0) * g.lda;
-  }
-  v4i acc[RG][TG];
-#pragma unroll
-  for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-    for (int tg = 0; tg < TG; ++tg) acc[rg][tg] = v4i{0};
-
-  v4i wv[2][U][RG], xv[2][U][TG];
-  // batch starting at step s0 into register set b
-  auto load_batch = [&](int b, int64_t s0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t k = (s0 + u) * 64 + 16 * grp;
-      const bool in = (s0 + u < s_end) && (k < g.K);
-      const int64_t kc = k < k_last ? k : k_last;
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg) wv[b][u][rg] = *reinterpret_cast<const v4i*>(wp[rg] + kc);
-#pragma unroll
-      for (int tg = 0; tg < TG; ++tg)
-        xv[b][u][tg] = *reinterpret_cast<const v4i*>((in && xok[tg]) ? xp[tg] + kc : kZeroChunk);
-    }
-  };
-  auto mfma_batch = [&](int b) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-        for (int tg = 0; tg < TG; ++tg)
-          acc[rg][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[b][u][rg], xv[b][u][tg], acc[rg][tg], 0, 0, 0);
-  };
-
-  if (s_begin < s_end) {
-    load_batch(0, s_begin);
-    int64_t s0 = s_begin;
-    // two batches per trip so that the register sets are compile-time indices
-    for (; s0 + 2 * U < s_end; s0 += 2 * U) {
-      load_batch(1, s0 + U);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_batch(0);
-      __builtin_amdgcn_sched_barrier(0);
-      load_batch(0, s0 + 2 * U);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_batch(1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (s0 + U < s_end) {
-      load_batch(1, s0 + U);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_batch(0);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_batch(1);
-    } else {
-      mfma_batch(0);
-    }
-  }
-
-  __syncthreads();  // red[] zeroed by every thread before any wave adds into it
-#pragma unroll
-  for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-    for (int tg = 0; tg < TG; ++tg)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) atomicAdd(&red[(rg * TG + tg) * 4 + v][lane], acc[rg][tg][v]);
-  __syncthreads();
-  for (int e = tid; e < kAcc * 64; e += 64 * WAVES) {
-    const int j = e >> 6, l = e & 63;
-    const int rg = j / (TG * 4), tg = (j / 4) % TG, v = j & 3;
-    const int64_t n = n0 + 16 * rg + 4 * (l >> 4) + v;
-    const int64_t m = 16 * tg + (l & 15);
-    if (n >= g.N || m >= g.M) continue;
-    const int32_t a = red[j][l];
-    if constexpr (EPI == kEpiBf16)
-      static_cast<uint16_t*>(g.out)[m * g.ldo + n] = epi_bf16(a, g.sa[m], g.sw[n], g.bias, n, 1.0f, false);
-    else
-      static_cast<int32_t*>(g.out)[m * g.ldo + n] = a;
-  }
-}
 
 // ------------------------------------------------------------------------
 // Dense small-M core, DMA ring: weights streamed to LDS in row-contiguous
@@ -1720,17 +1344,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       } else {
         if (g.bias) t = t + e_x[ui];
       }
-      store_out1(static_cast<uint16_t*>(g.out) + static_cast<int64_t>(e_orow[ui]) * g.ldo + n, f32_to_bf16(t),
-                 EPI == kEpiBf16Sum);
+      static_cast<uint16_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = f32_to_bf16(t);
     } else {
       static_cast<int32_t*>(g.out)[static_cast<int64_t>(e_orow[ui]) * g.ldo + n] = a;
     }
-  }
-  if constexpr (Rows::kGrouped && EPI == kEpiBf16Sum) {
-    slot_sum_step(g, 16 * TG, n0, 16 * RG, [&](int r) {
-      const int32_t p = g.sorted_ids[m0 + r];
-      return p < g.num_valid ? p : -1;
-    });
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }

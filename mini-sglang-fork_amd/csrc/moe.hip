@@ -7,10 +7,9 @@
 
 namespace mw8 {
 
-void launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
-void launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
-void launch_grouped_sum(const GemmArgs& g, unsigned blocks, int bm, hipStream_t st);
-void launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
+int launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
+int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
+int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
 
 namespace {
 
@@ -515,49 +514,10 @@ int moe_gemm_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   g.align_bsz = bsz;
-  if (bsz <= 32) {
-    launch_grouped_small(g, static_cast<unsigned>(blocks), epi, st);
-  } else {
-    launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);
-  }
+  const int rc = bsz <= 32 ? launch_grouped_small(g, static_cast<unsigned>(blocks), epi, st)
+                           : launch_grouped_tile(g, static_cast<unsigned>(blocks), bsz, epi, st);
+  if (rc != kOk) return rc;
   return check_launch("moe_gemm");
-}
-
-int moe_gemm_sum_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
-                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* npp,
-                      int64_t max_sorted, const float* topk_w, int top_k, int64_t num_valid,
-                      int64_t N, int64_t K, int E, int bsz, void* cache, void* out, int32_t* counters,
-                      hipStream_t st) {
-  MW8_REQUIRE(A && sa && W && sw && sorted_ids && expert_ids && npp && cache && out && counters, kErrArg,
-              "moe_gemm_sum: null pointer");
-  MW8_REQUIRE(N > 0 && N % 8 == 0 && K > 0 && K % 64 == 0 && K <= (1ll << 17), kErrShape,
-              "moe_gemm_sum: need N %% 8 == 0, K %% 64 == 0 and K <= 131072 (N=%lld K=%lld)", (long long)N,
-              (long long)K);
-  MW8_REQUIRE(bsz == 16 || bsz == 32 || bsz == 64 || bsz == 128, kErrShape,
-              "moe_gemm_sum: block size must be 16, 32, 64 or 128 (got %d)", bsz);
-  MW8_REQUIRE(top_k >= 1 && E >= 1 && num_valid >= 0 && num_valid % top_k == 0 && max_sorted >= 0, kErrShape,
-              "moe_gemm_sum: bad routing sizes (num_valid %% top_k must be 0)");
-  MW8_REQUIRE(aligned16(A) && aligned16(W) && aligned16(cache) && aligned16(out), kErrAlign,
-              "moe_gemm_sum: A, W, cache and out need 16-byte alignment");
-  MW8_REQUIRE((num_valid + 1) * K < (1ll << 31), kErrShape,
-              "moe_gemm_sum: activation matrix of %lld x %lld bytes exceeds 2^31", (long long)num_valid,
-              (long long)K);
-  const int64_t blocks = max_sorted / bsz;
-  if (blocks == 0 || num_valid == 0) return kOk;
-  MW8_REQUIRE(blocks < 65536, kErrShape, "moe_gemm_sum: too many expert blocks");
-  GemmArgs g{};
-  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = cache;
-  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
-  g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
-  // A rows and cache rows are indexed by the pair itself (GEMM2 addressing)
-  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = 1; g.num_experts = E;
-  g.staged_out = 1;
-  g.align_bsz = bsz;
-  g.sum_out = static_cast<uint16_t*>(out);
-  g.sum_cnt = counters;
-  g.sum_k = top_k;
-  launch_grouped_sum(g, static_cast<unsigned>(blocks), bsz, st);
-  return check_launch("moe_gemm_sum");
 }
 
 int moe_gemm_act_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
@@ -585,7 +545,7 @@ int moe_gemm_act_w8a8(const int8_t* A, const float* sa, const int8_t* W, const f
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.staged_out = 1;
   g.align_bsz = bsz;
-  launch_grouped_act(g, act, st);
+  if (const int rc = launch_grouped_act(g, act, st)) return rc;
   return check_launch("moe_gemm_act");
 }
 

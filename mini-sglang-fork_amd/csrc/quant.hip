@@ -212,9 +212,17 @@ __global__ __launch_bounds__(kBlock) void act_rows_kernel(
   }
   m = row_max<TPR>(m, red);
   if (!live) return;
+  U16x8* ar = a_out ? reinterpret_cast<U16x8*>(a_out + row * d) : nullptr;
+  if (q == nullptr) {  // activation only (launch-uniform): no requant
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+      if (idx < nvec) st_row16(ar + idx, v[i]);
+    }
+    return;
+  }
   const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(m)));
   uint2* qr = reinterpret_cast<uint2*>(q + row * d);
-  U16x8* ar = a_out ? reinterpret_cast<U16x8*>(a_out + row * d) : nullptr;
   if (rs.fast) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -269,11 +277,16 @@ __device__ __forceinline__ double row_sum_f64(double v, double* red) {
   }
 }
 
+// Rows of x and y_out are addressed as [G, inner, H] with outer strides ldx
+// / ldy (elements) and the inner rows contiguous at stride H: row r lives at
+// (r / inner) * ld + (r % inner) * H.  inner = 1, ld = H is a plain [M, H]
+// matrix; a per-head view q.view(M, heads, D) of a row of qkv is inner =
+// heads, ld = qkv width.  residual, q and s are plain [M, H] / [M].
 template <int TPR, int VPT, bool RES, bool QUANT>
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(
-    const uint16_t* __restrict__ x, uint16_t* __restrict__ res, const uint16_t* __restrict__ w,
+    const uint16_t* x, uint16_t* __restrict__ res, const uint16_t* __restrict__ w,
     float eps, int64_t M, int64_t H, int8_t* __restrict__ q, float* __restrict__ s,
-    uint16_t* __restrict__ y_out) {
+    uint16_t* y_out, int64_t inner, int64_t ldx, int64_t ldy) {
   __shared__ double dred[kBlock / 64];
   __shared__ uint32_t red[kBlock / 64];
   constexpr int kRowsPerBlock = kBlock / TPR;
@@ -281,7 +294,9 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(
   const int t = threadIdx.x % TPR;
   const bool live = row < M;  // uniform per wave (TPR >= 64)
   const int64_t nvec = H >> 3;
-  const U16x8* xr = reinterpret_cast<const U16x8*>(x + (live ? row : 0) * H);
+  const int64_t lrow = live ? row : 0;
+  const int64_t grp = inner == 1 ? lrow : lrow / inner, sub = lrow - grp * inner;
+  const U16x8* xr = reinterpret_cast<const U16x8*>(x + grp * ldx + sub * H);
   U16x8* rr = RES ? reinterpret_cast<U16x8*>(res + (live ? row : 0) * H) : nullptr;
   const U16x8* wr = reinterpret_cast<const U16x8*>(w);
 
@@ -350,7 +365,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(
     if (t == 0) s[row] = rs.s;
   }
   if (y_out) {
-    U16x8* yr = reinterpret_cast<U16x8*>(y_out + row * H);
+    U16x8* yr = reinterpret_cast<U16x8*>(y_out + grp * ldy + sub * H);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int64_t idx = t + static_cast<int64_t>(i) * TPR;
@@ -425,19 +440,20 @@ template <int TPR, int VPT>
 struct NormLaunch {
   static constexpr bool kHalfWaveRows = false;
   static void run(dim3 grid, hipStream_t st, const uint16_t* x, uint16_t* res, const uint16_t* w,
-                  float eps, int64_t M, int64_t H, int8_t* q, float* s, uint16_t* y) {
+                  float eps, int64_t M, int64_t H, int8_t* q, float* s, uint16_t* y, int64_t inner,
+                  int64_t ldx, int64_t ldy) {
     if (res && q)
       hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, true, true>), grid, dim3(kBlock), 0, st, x, res,
-                         w, eps, M, H, q, s, y);
+                         w, eps, M, H, q, s, y, inner, ldx, ldy);
     else if (res)
       hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, true, false>), grid, dim3(kBlock), 0, st, x, res,
-                         w, eps, M, H, q, s, y);
+                         w, eps, M, H, q, s, y, inner, ldx, ldy);
     else if (q)
       hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, false, true>), grid, dim3(kBlock), 0, st, x, res,
-                         w, eps, M, H, q, s, y);
+                         w, eps, M, H, q, s, y, inner, ldx, ldy);
     else
       hipLaunchKernelGGL((rmsnorm_rows_kernel<TPR, VPT, false, false>), grid, dim3(kBlock), 0, st, x, res,
-                         w, eps, M, H, q, s, y);
+                         w, eps, M, H, q, s, y, inner, ldx, ldy);
   }
 };
 
@@ -466,7 +482,8 @@ int quant_per_token_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_
 
 int act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int act, int8_t* q, float* s,
                            void* a_out, hipStream_t st) {
-  MW8_REQUIRE(x && q && s, kErrArg, "act_and_mul_quant: null pointer");
+  MW8_REQUIRE(x && ((q && s) || (!q && !s && a_out)), kErrArg,
+              "act_and_mul_quant: null pointer (q and s both given, or both NULL with act_out)");
   MW8_REQUIRE(act == 0 || act == 1, kErrArg, "act_and_mul_quant: act must be 0 (silu) or 1 (gelu)");
   MW8_REQUIRE(R >= 0 && two_d > 0 && two_d % 16 == 0, kErrShape,
               "act_and_mul_quant: need 2d %% 16 == 0, got %lld", (long long)two_d);
@@ -498,10 +515,35 @@ int rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, float 
   const bool ok = dispatch_rows<NormLaunch>(H / 8, M, st, static_cast<const uint16_t*>(x),
                                             static_cast<uint16_t*>(residual),
                                             static_cast<const uint16_t*>(weight), eps, M, H, q, s,
-                                            static_cast<uint16_t*>(y));
+                                            static_cast<uint16_t*>(y), int64_t{1}, H, H);
   MW8_REQUIRE(ok, kErrShape, "rmsnorm_quant: H=%lld exceeds the register-resident limit 32768",
               (long long)H);
   return check_launch("rmsnorm_quant");
+}
+
+int rmsnorm_strided_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, const void* weight, float eps,
+                         int64_t G, int64_t inner, int64_t H, hipStream_t st) {
+  MW8_REQUIRE(x && y && weight, kErrArg, "rmsnorm_strided: null pointer");
+  MW8_REQUIRE(G >= 0 && inner > 0 && H > 0 && H % 8 == 0, kErrShape,
+              "rmsnorm_strided: need H %% 8 == 0 and inner > 0 (G=%lld inner=%lld H=%lld)", (long long)G,
+              (long long)inner, (long long)H);
+  MW8_REQUIRE(ldx >= inner * H && ldy >= inner * H && ldx % 8 == 0 && ldy % 8 == 0, kErrShape,
+              "rmsnorm_strided: strides ldx=%lld ldy=%lld must be multiples of 8 and >= inner * H = %lld",
+              (long long)ldx, (long long)ldy, (long long)(inner * H));
+  MW8_REQUIRE(eps >= 0.0f, kErrArg, "rmsnorm_strided: eps must be >= 0");
+  if (G == 0) return kOk;
+  const int64_t M = G * inner;
+  MW8_REQUIRE(M < (1ll << 31) && M / inner == G, kErrShape, "rmsnorm_strided: too many rows");
+  MW8_REQUIRE(aligned16(x) && aligned16(y) && aligned16(weight), kErrAlign,
+              "rmsnorm_strided: x, y and weight need 16-byte alignment");
+  const bool ok = dispatch_rows<NormLaunch>(H / 8, M, st, static_cast<const uint16_t*>(x),
+                                            static_cast<uint16_t*>(nullptr),
+                                            static_cast<const uint16_t*>(weight), eps, M, H,
+                                            static_cast<int8_t*>(nullptr), static_cast<float*>(nullptr),
+                                            static_cast<uint16_t*>(y), inner, ldx, ldy);
+  MW8_REQUIRE(ok, kErrShape, "rmsnorm_strided: H=%lld exceeds the register-resident limit 32768",
+              (long long)H);
+  return check_launch("rmsnorm_strided");
 }
 
 }  // namespace mw8

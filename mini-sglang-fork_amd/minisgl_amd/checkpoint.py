@@ -2,11 +2,14 @@
 
 Format (safetensors, the reference's per-projection key names):
 
-* every linear projection ``<p>.{q,k,v,o,gate,up,down}_proj`` (and the MoE
-  router ``<p>.mlp.gate``) stores ``<...>.weight`` int8 [N, K] (the
-  reference's [out, in] layout) and ``<...>.weight_scale`` fp32 [N]
-  (``weight = rint(w / weight_scale)``, ``weight_scale = amax_k |w| / 127``
-  per output channel); a bias stays bf16;
+* every linear projection ``<p>.{q,k,v,o,gate,up,down}_proj`` stores
+  ``<...>.weight`` int8 [N, K] (the reference's [out, in] layout) and
+  ``<...>.weight_scale`` fp32 [N] (``weight = rint(w / weight_scale)``,
+  ``weight_scale = amax_k |w| / 127`` per output channel); a bias stays bf16;
+* the MoE router ``<p>.mlp.gate`` stays bf16, as the reference's router is a
+  bf16 ``LinearReplicated`` (python/minisgl/models/utils.py:62-66): top-k
+  selection is discontinuous, so int8 router logits could send a token to
+  other experts than the bf16 router does;
 * expert projections ``<p>.experts.<i>.{gate,up,down}_proj`` likewise;
 * everything else (embeddings, norms, lm_head) stays bf16.
 
@@ -60,7 +63,7 @@ _EXPERT_RENAME = {
     "gate_up_proj.weight_scale": "gate_up_scale",
     "down_proj.weight_scale": "down_scale",
 }
-_QUANTIZED = re.compile(r"(_proj|\.mlp\.gate)\.weight$")
+_QUANTIZED = re.compile(r"_proj\.weight$")
 
 
 def is_quantized_weight(key: str) -> bool:

@@ -32,6 +32,8 @@ SIGNATURES = {
     "mw8_act_and_mul_quant_bf16": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _P, _P, _P]),
     "mw8_set_tuning": (None, [_I32, _I32, _I32]),
     "mw8_gemm_workspace_bytes": (c_size_t, [_I64, _I64, _I64]),
+    "mw8_gemm_workspace_max_bytes": (c_size_t, []),
+    "mw8_tuning_count": (_I32, [_I32]),
     "mw8_gemm_w8a8_bf16": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, c_size_t, _P],
@@ -53,10 +55,6 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P],
     ),
-    "mw8_moe_gemm_sum_w8a8_bf16": (
-        ctypes.c_int,
-        [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P],
-    ),
     "mw8_moe_route_quant": (
         ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P]
     ),
@@ -65,6 +63,7 @@ SIGNATURES = {
         [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _I32, _I32, _P, _P, _P, _P],
     ),
     "mw8_rmsnorm_quant_bf16": (ctypes.c_int, [_P, _P, _P, c_float, _I64, _I64, _P, _P, _P, _P]),
+    "mw8_rmsnorm_strided_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _P, c_float, _I64, _I64, _I64, _P]),
     "mw8_calib_sink_len": (_I64, []),
     "mw8_calib_mfma_i8": (ctypes.c_int, [_I32, _I32, _P, _I64, _P]),
     "mw8_calib_read": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),

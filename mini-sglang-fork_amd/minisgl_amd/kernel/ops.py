@@ -40,23 +40,35 @@ def _on_gpu(*ts: Optional[torch.Tensor]) -> None:
 _WORKSPACE: Dict[torch.device, torch.Tensor] = {}
 
 
-def gemm_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
-    """Workspace for the GEMM's tail-wave K split at (M, N, K), cached per
-    device and grown on demand (None when no split applies).
-
-    It holds int32 partial tiles only for the duration of one call, so it is
-    reusable by any calls ordered on one stream.  Reserve the largest size
-    before capturing a graph (growing it allocates).
-    """
-    need = int(load().mw8_gemm_workspace_bytes(M, N, K))
-    if need == 0:
-        return None
+def reserve_gemm_workspace(device: torch.device) -> torch.Tensor:
+    """The GEMM workspace of ``device``: one buffer of
+    ``mw8_gemm_workspace_max_bytes()`` (the bound over every shape and
+    tiling, 64 MiB on a 256-CU MI355X), allocated on first use and never
+    grown, replaced or freed.  So a HIP graph that captured a GEMM keeps a
+    valid workspace pointer whatever runs later, and no call inside a
+    capture allocates once the workspace exists (the reference engine runs
+    each batch size eagerly before capturing it, which reserves it,
+    python/minisgl/engine/graph.py:129-144).  The buffer holds int32
+    partial tiles only during one call, so calls ordered on one stream
+    share it; calls on concurrent streams must not."""
     dev = torch.device(device)
+    if dev.index is None:
+        dev = torch.device(dev.type, torch.cuda.current_device())
     ws = _WORKSPACE.get(dev)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+    if ws is None:
+        with torch.cuda.device(dev):
+            need = int(load().mw8_gemm_workspace_max_bytes())
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
         _WORKSPACE[dev] = ws
     return ws
+
+
+def gemm_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
+    """Workspace for the GEMM's K split at (M, N, K): the device's reserved
+    buffer (reserve_gemm_workspace), or None when no split applies."""
+    if int(load().mw8_gemm_workspace_bytes(M, N, K)) == 0:
+        return None
+    return reserve_gemm_workspace(device)
 
 
 # ----------------------------------------------------------------- quantizer
@@ -83,23 +95,31 @@ def quant_per_token(
 
 
 def act_and_mul_quant(
-    x: torch.Tensor, activation: str = "silu", return_act: bool = False
+    x: torch.Tensor, activation: str = "silu", return_act: bool = False, quantize: bool = True,
+    act_out: Optional[torch.Tensor] = None,
 ):
-    """bf16 [R, 2d] -> (int8 [R, d], fp32 [R][, bf16 act [R, d]])."""
-    _on_gpu(x)
+    """bf16 [R, 2d] -> (int8 [R, d], fp32 [R][, bf16 act [R, d]]);
+    ``quantize=False`` computes the activation only and returns it."""
+    _on_gpu(x, act_out)
     _need(activation in _ACT, f"unsupported activation {activation}")
     _need(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x: bf16 [R, 2d]")
     R, two_d = x.shape
     d = two_d // 2
-    q = torch.empty((R, d), dtype=torch.int8, device=x.device)
-    s = torch.empty((R,), dtype=torch.float32, device=x.device)
-    a = torch.empty((R, d), dtype=torch.bfloat16, device=x.device) if return_act else None
+    q = torch.empty((R, d), dtype=torch.int8, device=x.device) if quantize else None
+    s = torch.empty((R,), dtype=torch.float32, device=x.device) if quantize else None
+    a = act_out
+    if a is None and (return_act or not quantize):
+        a = torch.empty((R, d), dtype=torch.bfloat16, device=x.device)
+    if a is not None:
+        _need(a.dtype == torch.bfloat16 and a.shape == (R, d) and a.is_contiguous(), "act_out: bf16 [R, d]")
     if R > 0:
         check(
             load().mw8_act_and_mul_quant_bf16(
                 _ptr(x), R, two_d, _ACT[activation], _ptr(q), _ptr(s), _ptr(a), _stream(x)
             )
         )
+    if not quantize:
+        return a
     return (q, s, a) if return_act else (q, s)
 
 
@@ -143,6 +163,48 @@ def rmsnorm_quant(
     if not quantize:
         return y
     return (q, s, y) if (return_y or y is not None) else (q, s)
+
+
+def _row_groups(t: torch.Tensor) -> Optional[Tuple[int, int, int]]:
+    """(G, inner, ld) if the rows of ``t`` [..., H] sit at g * ld + i * H
+    (g < G, i < inner, the last dim contiguous), else None."""
+    if t.dim() < 2 or t.stride(-1) != 1:
+        return None
+    H = t.shape[-1]
+    if t.is_contiguous():
+        return t.numel() // H, 1, H
+    if t.dim() == 2:
+        G, inner, ld = t.shape[0], 1, (t.stride(0) if t.shape[0] > 1 else H)
+    elif t.dim() == 3 and (t.stride(1) == H or t.shape[1] == 1):
+        G, inner, ld = t.shape[0], t.shape[1], (t.stride(0) if t.shape[0] > 1 else t.shape[1] * H)
+    else:
+        return None
+    return (G, inner, ld) if ld >= inner * H else None
+
+
+def rmsnorm_strided(x: torch.Tensor, weight: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None) -> bool:
+    """Plain RMSNorm of the rows of a strided view ``x`` [G, inner, H] (or
+    [R, H] with a row stride) into ``out`` (default: in place, ``out = x``).
+    Returns False when the layout is not expressible as [G, inner, H] row
+    groups with 16-byte aligned rows (the caller then copies)."""
+    out = x if out is None else out
+    _on_gpu(x, weight, out)
+    _need(x.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and x.shape == out.shape, "x/out: bf16, same shape")
+    H = x.shape[-1]
+    _need(weight.dtype == torch.bfloat16 and weight.shape == (H,) and weight.is_contiguous(), "weight: bf16 [H]")
+    gx, go = _row_groups(x), _row_groups(out)
+    if gx is None or go is None or gx[:2] != go[:2] or H % 8 or gx[2] % 8 or go[2] % 8:
+        return False
+    if x.data_ptr() % 16 or out.data_ptr() % 16:
+        return False
+    G, inner, ldx = gx
+    if G * inner > 0:
+        check(
+            load().mw8_rmsnorm_strided_bf16(
+                _ptr(x), ldx, _ptr(out), go[2], _ptr(weight), float(eps), G, inner, H, _stream(x)
+            )
+        )
+    return True
 
 
 # ----------------------------------------------------------------- dense GEMM
@@ -407,70 +469,6 @@ def fused_moe_kernel_act_w8a8(
     )
 
 
-_SLOT_COUNTERS: Dict[torch.device, torch.Tensor] = {}
-
-
-def slot_sum_counters(tokens: int, N: int, device: torch.device) -> torch.Tensor:
-    """Counters of the fused slot sum for ``tokens`` x ``N`` outputs: int32
-    [tokens * ceil(N / 16)], zero-filled once, cached per device and grown on
-    demand.  Every call of fused_moe_kernel_sum_w8a8 leaves them zero, so any
-    calls ordered on one stream share them.  Reserve the largest size before
-    capturing a graph (growing it allocates)."""
-    need = tokens * ((N + 15) // 16)
-    dev = torch.device(device)
-    buf = _SLOT_COUNTERS.get(dev)
-    if buf is None or buf.numel() < need:
-        buf = torch.zeros(max(need, 1 << 16), dtype=torch.int32, device=dev)
-        _SLOT_COUNTERS[dev] = buf
-    return buf
-
-
-def fused_moe_kernel_sum_w8a8(
-    A: torch.Tensor,
-    A_scale: torch.Tensor,
-    B: torch.Tensor,
-    B_scale: torch.Tensor,
-    C: torch.Tensor,
-    out: torch.Tensor,
-    topk_weights: torch.Tensor,
-    sorted_token_ids: torch.Tensor,
-    expert_ids: torch.Tensor,
-    num_tokens_post_padded: torch.Tensor,
-    top_k: int,
-    block_size: int,
-    num_valid_tokens: int,
-    counters: Optional[torch.Tensor] = None,
-) -> None:
-    """GEMM2 of the MoE layer with the slot sum fused in: C bf16 [M*k, N]
-    receives the routed-weighted expert outputs of every pair (as
-    fused_moe_kernel_w8a8 with MUL_ROUTED_WEIGHT and top_k = 1) and out bf16
-    [M, N] their sum over the k slots (as moe_sum_reduce, the same bits),
-    from one launch.  Every pair's expert must lie in [0, E)."""
-    _on_gpu(A, A_scale, B, B_scale, C, out, topk_weights)
-    _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [M*k, K]")
-    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
-    E, N, K = B.shape
-    _need(A.shape == (num_valid_tokens, K), "A: [M*k, K]")
-    _need(A_scale.dtype == torch.float32 and A_scale.shape == (num_valid_tokens,), "A_scale: fp32 [M*k]")
-    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
-    _need(num_valid_tokens % top_k == 0, "num_valid_tokens: a multiple of top_k")
-    M = num_valid_tokens // top_k
-    _need(C.dtype == torch.bfloat16 and C.is_contiguous() and C.numel() == num_valid_tokens * N, "C: bf16 [M*k, N]")
-    _need(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == M * N, "out: bf16 [M, N]")
-    _need(topk_weights.dtype == torch.float32 and topk_weights.is_contiguous() and topk_weights.numel() == num_valid_tokens,
-          "topk_weights: fp32 [M, k]")
-    if counters is None:
-        counters = slot_sum_counters(M, N, A.device)
-    _need(counters.dtype == torch.int32 and counters.numel() >= M * ((N + 15) // 16), "counters: int32 [M * ceil(N/16)]")
-    check(
-        load().mw8_moe_gemm_sum_w8a8_bf16(
-            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids), _ptr(expert_ids),
-            _ptr(num_tokens_post_padded), sorted_token_ids.shape[0], _ptr(topk_weights), top_k,
-            num_valid_tokens, N, K, E, block_size, _ptr(C), _ptr(out), _ptr(counters), _stream(A),
-        )
-    )
-
-
 def fused_moe_kernel_w8a8_i32(
     A: torch.Tensor,
     B: torch.Tensor,
@@ -511,9 +509,11 @@ def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
 
 __all__ = [
     "gemm_workspace",
+    "reserve_gemm_workspace",
     "quant_per_token",
     "act_and_mul_quant",
     "rmsnorm_quant",
+    "rmsnorm_strided",
     "gemm_w8a8",
     "gemm_w8a8_i32",
     "topk_softmax",
@@ -521,8 +521,6 @@ __all__ = [
     "fused_moe_kernel_w8a8",
     "fused_moe_kernel_w8a8_i32",
     "fused_moe_kernel_act_w8a8",
-    "fused_moe_kernel_sum_w8a8",
-    "slot_sum_counters",
     "moe_prepare_small",
     "moe_route_quant",
     "moe_sum_reduce",

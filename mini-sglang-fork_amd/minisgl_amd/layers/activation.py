@@ -11,13 +11,16 @@ from ..kernel import act_and_mul_quant
 
 
 def _act_bf16(x: torch.Tensor, activation: str, out: torch.Tensor | None) -> torch.Tensor:
+    """The activation alone (no requant): one read of x, one write of the result."""
     x2 = x.reshape(-1, x.shape[-1])
-    _, _, a = act_and_mul_quant(x2, activation, return_act=True)
-    a = a.view(*x.shape[:-1], x.shape[-1] // 2)
+    d = x.shape[-1] // 2
+    direct = out is not None and out.is_contiguous()
+    a = act_and_mul_quant(x2, activation, quantize=False, act_out=out.view(-1, d) if direct else None)
     if out is not None:
-        out.copy_(a)
+        if not direct:
+            out.copy_(a.view(out.shape))
         return out
-    return a
+    return a.view(*x.shape[:-1], d)
 
 
 def silu_and_mul(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

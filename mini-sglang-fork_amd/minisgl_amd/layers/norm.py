@@ -23,12 +23,14 @@ from typing import Optional, Tuple
 
 import torch
 
-from ..kernel import rmsnorm_quant
+from ..kernel import rmsnorm_quant, rmsnorm_strided
 from .base import BaseOP
 
 
 def _rows(x: torch.Tensor) -> torch.Tensor:
-    return x.reshape(-1, x.shape[-1])
+    """x as a contiguous [rows, size] matrix: a view of x when x is
+    contiguous, otherwise a copy (which in-place callers copy back)."""
+    return x.reshape(-1, x.shape[-1]) if x.is_contiguous() else x.contiguous().view(-1, x.shape[-1])
 
 
 class RMSNorm(BaseOP):
@@ -37,12 +39,26 @@ class RMSNorm(BaseOP):
         self.weight = torch.empty(size, dtype=torch.bfloat16)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_contiguous():
+            y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+            if rmsnorm_strided(x, self.weight, self.eps, out=y):
+                return y
         y = rmsnorm_quant(_rows(x), self.weight, self.eps, quantize=False)
-        return y.view_as(x)
+        return y.view(x.shape)
 
     def forward_inplace(self, x: torch.Tensor) -> None:
-        x2 = _rows(x)
-        rmsnorm_quant(x2, self.weight, self.eps, y=x2, quantize=False)
+        """Normalizes x in place, also when x is a strided view such as the
+        per-head q.view(-1, heads, head_dim) of a qkv split
+        (python/minisgl/layers/attention.py:49-53): such views are
+        normalized where they lie, and any other layout is normalized in a
+        copy that is written back into x."""
+        if x.is_contiguous():
+            x2 = _rows(x)
+            rmsnorm_quant(x2, self.weight, self.eps, y=x2, quantize=False)
+        elif not rmsnorm_strided(x, self.weight, self.eps):
+            x2 = _rows(x)
+            rmsnorm_quant(x2, self.weight, self.eps, y=x2, quantize=False)
+            x.copy_(x2.view(x.shape))
 
 
 class RMSNormFused(BaseOP):
@@ -55,9 +71,15 @@ class RMSNormFused(BaseOP):
     ) -> Tuple[torch.Tensor, torch.Tensor]:
         if residual is None:
             y = rmsnorm_quant(_rows(x), self.weight, self.eps, quantize=False)
-            return y.view_as(x), x
-        x2 = _rows(x)
-        rmsnorm_quant(x2, self.weight, self.eps, residual=_rows(residual), y=x2, quantize=False)
+            return y.view(x.shape), x
+        # in place on x and residual (fused_add_rmsnorm, python/minisgl/layers/norm.py:33-38);
+        # non-contiguous tensors are processed in copies written back afterwards
+        x2, r2 = _rows(x), _rows(residual)
+        rmsnorm_quant(x2, self.weight, self.eps, residual=r2, y=x2, quantize=False)
+        if not x.is_contiguous():
+            x.copy_(x2.view(x.shape))
+        if not residual.is_contiguous():
+            residual.copy_(r2.view(residual.shape))
         return x, residual
 
 
@@ -75,7 +97,10 @@ class RMSNormQuant(BaseOP):
         if residual is None:
             q, s = rmsnorm_quant(x2, self.weight, self.eps)
             return q, s, x
-        q, s = rmsnorm_quant(x2, self.weight, self.eps, residual=_rows(residual))
+        r2 = _rows(residual)
+        q, s = rmsnorm_quant(x2, self.weight, self.eps, residual=r2)
+        if not residual.is_contiguous():
+            residual.copy_(r2.view(residual.shape))
         return q, s, residual
 
 

@@ -55,20 +55,32 @@ def fused_topk(
     gating_output: torch.Tensor,
     topk: int,
     renormalize: bool,
+    num_token_non_padded: torch.Tensor | None = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(topk_weights fp32 [M, k], topk_ids int32 [M, k]); one HIP kernel
-    (python/minisgl/moe/fused.py:9-28)."""
+    (python/minisgl/moe/fused.py:9-28).  Tokens at or past
+    ``num_token_non_padded`` (a device tensor, so no host sync) get ids -1,
+    which the alignment skips (:25-27)."""
     assert hidden_states.shape[0] == gating_output.shape[0], "Number of tokens mismatch"
-    return topk_softmax(gating_output.contiguous(), topk, renormalize)
+    topk_weights, topk_ids = topk_softmax(gating_output.contiguous(), topk, renormalize)
+    if num_token_non_padded is not None:
+        indices = torch.arange(0, topk_ids.shape[0], device=topk_ids.device)
+        topk_ids[indices >= num_token_non_padded, :] = -1
+    return topk_weights, topk_ids
 
 
 def get_default_config(M: int, E: int, N: int, K: int, topk: int) -> Dict[str, int]:
     """Two tile regimes keyed on tokens vs experts, as the reference
-    (python/minisgl/moe/fused.py:92-113): a 16-row block when M <= E
-    (decode: weight streaming), otherwise a 64-row block (MFMA tiles)."""
+    (python/minisgl/moe/fused.py:92-113), with the same keys.  BLOCK_SIZE_M
+    is the alignment block: 16 rows when M <= E (decode: weight streaming),
+    otherwise 64 (MFMA tiles).  The other keys describe this build's
+    kernels for that regime: the weight rows a block streams and the K
+    bytes of one ring stage (16 rows x 256 bytes for 16-row blocks; 128 or
+    256 columns x 64 bytes for the tile walk), and GROUP_SIZE_M = 1 (the
+    tiles are ordered per XCD instead of by a GROUP_M swizzle)."""
     if M <= E:
-        return {"BLOCK_SIZE_M": 16}
-    return {"BLOCK_SIZE_M": 64}
+        return {"BLOCK_SIZE_M": 16, "BLOCK_SIZE_N": 16, "BLOCK_SIZE_K": 256, "GROUP_SIZE_M": 1}
+    return {"BLOCK_SIZE_M": 64, "BLOCK_SIZE_N": 128, "BLOCK_SIZE_K": 64, "GROUP_SIZE_M": 1}
 
 
 def try_get_optimal_moe_config(w1_shape, w2_shape, top_k: int, M: int) -> Dict[str, int]:
@@ -162,6 +174,13 @@ class FusedMoeW8A8(BaseMoeBackend):
             raise ValueError("the W8A8 MoE backend needs w1_scale and w2_scale")
         M, H = hidden_states.shape
         E = w1.shape[0]
+        # int8 GEMM operand granularity: both contraction sizes (H for GEMM1,
+        # I for GEMM2) must be multiples of 16
+        if H % 16 != 0 or w2.shape[2] % 16 != 0 or w1.shape[1] != 2 * w2.shape[2]:
+            raise ValueError(
+                f"W8A8 MoE needs hidden and intermediate sizes that are multiples of 16 and "
+                f"w1 [E, 2I, H] / w2 [E, H, I] (got w1 {tuple(w1.shape)}, w2 {tuple(w2.shape)})"
+            )
         # the contract fused_experts_impl_w8a8 asserts, for the fast paths too
         assert H == w1.shape[2], "Hidden size mismatch"
         assert hidden_states.dtype == torch.bfloat16, "W8A8 MoE takes bf16 activations"
@@ -172,7 +191,6 @@ class FusedMoeW8A8(BaseMoeBackend):
             bsz == 16
             and 0 < M * topk <= PREPARE_MAX_PAIRS
             and E + 1 <= 512
-            and H % 8 == 0
             and hidden_states.is_contiguous()
             and gating_output.is_contiguous()
         ):
@@ -184,7 +202,7 @@ class FusedMoeW8A8(BaseMoeBackend):
                 hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, sorted_ids,
                 expert_ids, npp, topk, bsz, activation, apply_router_weight_on_input,
             )
-        if H % 8 == 0 and hidden_states.is_contiguous() and gating_output.is_contiguous():
+        if hidden_states.is_contiguous() and gating_output.is_contiguous():
             # router and hidden quantization in one launch (one wave per token)
             topk_weights, topk_ids, q_h, s_h = moe_route_quant(gating_output, hidden_states, topk, renormalize)
             sorted_ids, expert_ids, npp = moe_align_block_size(topk_ids, bsz, E)
@@ -192,6 +210,9 @@ class FusedMoeW8A8(BaseMoeBackend):
                 hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, sorted_ids, expert_ids,
                 npp, topk, bsz, activation, apply_router_weight_on_input,
             )
+        # step by step (a non-contiguous router output, or a non-contiguous
+        # hidden_states, which fused_experts_impl_w8a8 rejects as the
+        # reference does, python/minisgl/moe/fused.py:140-145)
         topk_weights, topk_ids = fused_topk(hidden_states, gating_output, topk, renormalize)
         return fused_experts_impl_w8a8(
             hidden_states, w1, w1_scale, w2, w2_scale, topk_weights, topk_ids, activation,

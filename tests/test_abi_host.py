@@ -60,13 +60,34 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_gemm_workspace_bytes(512, 5120, 5120 + 64) == 0  # K % 128 != 0
     assert lib.mw8_gemm_workspace_bytes(512, 7168, 5120) == 0  # 128x128 ring (no split) chosen
     # the 64x128 ring (forced): 272 tiles, 16 in the tail, 16 K ranges each
-    lib.mw8_set_tuning(-1, 25, -1)
+    lib.mw8_set_tuning(-1, 5, -1)
     try:
         assert lib.mw8_gemm_workspace_bytes(64, 34816, 5120) == 16 * 16 * 64 * 128 * 4
         assert lib.mw8_gemm_workspace_bytes(40, 1024, 1024) == 8 * 8 * 64 * 128 * 4  # all 8 tiles split
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
     assert lib.mw8_gemm_workspace_bytes(32, 34816, 5120) == 0  # decode core
+
+
+def test_workspace_bound_and_tuning_counts(lib):
+    """mw8_gemm_workspace_max_bytes bounds every plan (r * sp <= S slots of
+    the largest split tile), so one reservation never has to grow; the
+    tuning tables have the documented sizes.  Without a GPU the library
+    plans for 256 CUs."""
+    mx = lib.mw8_gemm_workspace_max_bytes()
+    assert mx == 256 * 256 * 256 * 4
+    counts = [lib.mw8_tuning_count(k) for k in range(4)]
+    assert counts == [8, 6, 2, 3] and lib.mw8_tuning_count(9) == 0
+    worst = 0
+    try:
+        for tile in range(-1, counts[1]):
+            lib.mw8_set_tuning(-1, tile, -1)
+            for M in (33, 40, 64, 65, 100, 128, 200, 256, 300, 512, 1000, 2080, 4096, 8192):
+                for N, K in ((5120, 5120), (7168, 5120), (34816, 5120), (5120, 17408), (1000, 1024), (64, 128)):
+                    worst = max(worst, lib.mw8_gemm_workspace_bytes(M, N, K))
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+    assert 0 < worst <= mx
 
 
 FAKE_A, FAKE_B, FAKE_C = 4096, 8192, 12288  # aligned non-null stand-ins: never dereferenced
@@ -107,19 +128,11 @@ def test_argument_errors_return_codes(lib):
     assert prep(FAKE_A, 1, 4, 16, 8, 1, FAKE_B, 64, None, FAKE_C, FAKE_C, FAKE_C, 17, 16,
                 FAKE_A, FAKE_B, FAKE_C, None) == E["MW8_ERR_ARG"]
     assert lib.mw8_moe_sum_reduce_bf16(FAKE_A, 4, 8, 12, FAKE_B, None) == E["MW8_ERR_SHAPE"]
-    # GEMM2 with the fused slot sum: null counters, N % 8 != 0, K % 64 != 0,
-    # num_valid not a multiple of top_k
-    gsum = lib.mw8_moe_gemm_sum_w8a8_bf16
-    args = [FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 64, FAKE_B, 8, 64, 64, 128, 4, 16,
-            FAKE_A, FAKE_B, FAKE_C, None]
-    bad = list(args); bad[17] = None
-    assert gsum(*bad) == E["MW8_ERR_ARG"]
-    bad = list(args); bad[11] = 60
-    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
-    bad = list(args); bad[12] = 96
-    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
-    bad = list(args); bad[10] = 60
-    assert gsum(*bad) == E["MW8_ERR_SHAPE"]
+    # strided RMSNorm: H % 8 != 0, stride below inner * H, null weight
+    assert lib.mw8_rmsnorm_strided_bf16(FAKE_A, 96, FAKE_A, 96, FAKE_B, 1e-6, 4, 8, 12, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_rmsnorm_strided_bf16(FAKE_A, 64, FAKE_A, 64, FAKE_B, 1e-6, 4, 8, 16, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_rmsnorm_strided_bf16(FAKE_A, 256, FAKE_A, 256, None, 1e-6, 4, 8, 16, None) == E["MW8_ERR_ARG"]
+    assert lib.mw8_rmsnorm_strided_bf16(FAKE_A + 2, 256, FAKE_A, 256, FAKE_B, 1e-6, 4, 8, 16, None) == E["MW8_ERR_ALIGN"]
     # empty problems are no-ops
     assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0
 

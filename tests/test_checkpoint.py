@@ -75,7 +75,8 @@ def ckpt(tmp_path_factory):
 def test_quantized_key_set():
     assert is_quantized_weight("model.layers.0.self_attn.q_proj.weight")
     assert is_quantized_weight("model.layers.1.mlp.experts.3.down_proj.weight")
-    assert is_quantized_weight("model.layers.1.mlp.gate.weight")
+    # the MoE router stays bf16 (python/minisgl/models/utils.py:62-66)
+    assert not is_quantized_weight("model.layers.1.mlp.gate.weight")
     assert not is_quantized_weight("model.layers.0.input_layernorm.weight")
     assert not is_quantized_weight("model.embed_tokens.weight")
     assert not is_quantized_weight("lm_head.weight")
@@ -132,6 +133,8 @@ def test_tensor_parallel_sharding_rules(ckpt, rank):
     assert sd[f"{p1}.mlp.experts.down_scale"].shape == (E, H)
     assert sd[f"{p1}.mlp.experts.gate_up_scale"].shape == (E, IE)
     assert torch.equal(sd[f"{p1}.mlp.gate.weight"], w8[f"{p1}.mlp.gate.weight"])
+    assert sd[f"{p1}.mlp.gate.weight"].dtype == torch.bfloat16  # bf16 router, no weight_scale
+    assert f"{p1}.mlp.gate.weight_scale" not in sd
 
 
 def test_more_tp_ranks_than_kv_heads(ckpt):

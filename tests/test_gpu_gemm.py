@@ -74,13 +74,15 @@ def test_gemm_qwen3_14b(M, K, N):
 
 
 @pytest.mark.parametrize("M", [4096, 8192])
-@pytest.mark.parametrize("K,N", [(5120, 7168), (17408, 5120)])
+@pytest.mark.parametrize("K,N", [(5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120)])
 def test_gemm_qwen3_14b_large_m_sampled(M, K, N):
-    """Large M: every output is computed on the GPU; a fixed sample of rows
-    (first, last, and random rows of each 128-row tile band) is checked."""
+    """Large M at all four Qwen3-14B shapes, under the tiling the library
+    picks for each (gate_up M=8192 is the benchmark's dominant launch):
+    every output is computed on the GPU; a sample of rows (first, last, and
+    random rows, each row spanning every column tile) is checked."""
     announce(f"gemm 14B large M={M} K={K} N={N}")
-    rng = np.random.default_rng(M + K)
-    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 62, replace=False)]))
+    rng = np.random.default_rng(M + K + N)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 40, replace=False)]))
     _run_case(M, K, N, seed=0, rows=rows)
 
 
@@ -137,7 +139,7 @@ def test_gemm_split_tail(M, K, N):
     r = T % 256
     sp = min(256 // r, K // 128, 16) if r else 0
     want_ws = r * sp * 65536 * 4 if sp >= 2 else 0
-    lib.mw8_set_tuning(-1, 14, -1)  # the 8-wave 256x256 ring
+    lib.mw8_set_tuning(-1, 2, -1)  # the 8-wave 256x256 ring
     try:
         assert lib.mw8_gemm_workspace_bytes(M, N, K) == want_ws
         rows = None if M <= 1024 else np.unique(np.concatenate([[0, M - 1], np.arange(M - 300, M, 7)]))
@@ -193,7 +195,10 @@ def test_linear_layers_drop_in():
             assert bf16_bits_equal(y, y_ref).all()
 
 
-NUM_TILE_CFGS = 28  # kTileCfgs in csrc/gemm.hip
+def _tuning_count(kind):
+    from minisgl_amd.kernel.lib import load
+
+    return int(load().mw8_tuning_count(kind))
 
 
 @pytest.mark.parametrize(
@@ -205,7 +210,7 @@ def test_gemm_every_tile_config(M, K, N):
     """Each tile configuration (forced through mw8_set_tuning) on ragged
     shapes; K % 64 != 0 makes the direct-to-LDS configs fall back.  33-64
     rows take the tile core only when a tile configuration is forced; with
-    few tiles the skinny rings (18-23) split every tile's K range."""
+    few tiles the split-capable rings split every tile's K range."""
     from minisgl_amd.kernel.lib import load
 
     announce(f"gemm all tile cfgs M={M} K={K} N={N}")
@@ -217,7 +222,7 @@ def test_gemm_every_tile_config(M, K, N):
     y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
     lib = load()
     try:
-        for cfg in range(NUM_TILE_CFGS):
+        for cfg in range(_tuning_count(1)):
             lib.mw8_set_tuning(-1, cfg, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
@@ -225,34 +230,6 @@ def test_gemm_every_tile_config(M, K, N):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
-@pytest.mark.parametrize("M,K,N,bias", [(4096, 128, 8192, False), (4000, 384, 8168, True), (4096, 256, 8192, True)])
-def test_gemm_persistent_two_tiles_per_block(M, K, N, bias):
-    """The persistent 256x256 walk (tile cfg 27) with 512 tiles: every
-    block runs two whole tiles back to back on one LDS ring, including a
-    one-stage K, edge tiles and a bias; bit-exact against the oracle."""
-    from minisgl_amd.kernel.lib import load
-
-    announce(f"gemm persistent two tiles M={M} K={K} N={N} bias={bias}")
-    gen = torch.Generator().manual_seed(M + K)
-    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
-    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
-    s_w = torch.rand(N, generator=gen) * 9e-3 + 1e-3
-    b = (torch.randn(N, generator=gen) * 0.1).to(torch.bfloat16) if bias else None
-    q, s = quant_per_token(x.to(DEV))
-    q_ref, s_ref = orc.quant_per_token(f32(x))
-    acc_ref = orc.gemm_i32(q_ref, w.numpy())
-    y_ref = orc.epilogue(acc_ref, s_ref, s_w.numpy(), bias=None if b is None else f32(b))
-    lib = load()
-    try:
-        lib.mw8_set_tuning(-1, 27, -1)
-        y = gemm_w8a8(q, s, w.to(DEV), s_w.to(DEV), None if b is None else b.to(DEV))
-        torch.cuda.synchronize()
-        assert bf16_bits_equal(y, y_ref).all()
-    finally:
-        lib.mw8_set_tuning(-1, -1, -1)
-
-
-NUM_DECODE_CFGS = 32  # kDecodeCfgs in csrc/gemm.hip
 
 
 @pytest.mark.parametrize(
@@ -275,7 +252,7 @@ def test_gemm_every_decode_config(M, K, N):
     y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
     lib = load()
     try:
-        for cfg in range(NUM_DECODE_CFGS):
+        for cfg in range(_tuning_count(0)):
             lib.mw8_set_tuning(cfg, -1, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"

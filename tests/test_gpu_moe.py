@@ -14,7 +14,6 @@ from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
 from minisgl_amd.kernel import (
     act_and_mul_quant,
     fused_moe_kernel_act_w8a8,
-    fused_moe_kernel_sum_w8a8,
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
@@ -204,7 +203,10 @@ def _ragged_expert_case(seed, M=50, k=2, E=8, N=208, K=384):
     return logits, W, SW, act
 
 
-NUM_MOE_CFGS = 20  # grouped configurations in csrc/gemm.hip (7, 8: run tiles; 9-19: persistent)
+def _tuning_count(kind):
+    from minisgl_amd.kernel import lib as mw8lib
+
+    return int(mw8lib.load().mw8_tuning_count(kind))
 
 
 @pytest.mark.parametrize("shape", ["cfg3", "ragged"])
@@ -249,7 +251,7 @@ def test_grouped_every_tile_config(shape):
             )
             for B in (64, 128):
                 sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, E)
-                for cfg in range(-1, NUM_MOE_CFGS):
+                for cfg in range(-1, _tuning_count(2)):
                     announce(f"grouped {shape} gemm{which} B={B} cfg={cfg}")
                     lib.mw8_set_tuning(-1, -1, cfg)
                     out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
@@ -298,17 +300,13 @@ def test_fused_activation_gemm_equals_gemm_then_activation(shape, B):
             assert torch.equal(a.view(torch.int16), a_ref.view(torch.int16)), f"{act_name} routed={routed}"
 
 
-NUM_SMALL_CFGS = 9  # 16-row block configurations in csrc/gemm.hip (0: register streaming, 1-6: DMA ring, 7-8: ring over 32 weight rows)
-
-
 @pytest.mark.parametrize("shape", ["cfg3", "ragged", "longk"])
 def test_grouped_small_blocks_every_config(shape):
     """16-row alignment blocks (the decode regime) through every small-block
-    configuration: the register-streaming core (cfg 0, K <= 4080) and the
-    LDS DMA ring with gathered token rows (1-6), gate_up-style and
-    down-style, bit-exact against the oracle.  The ragged case has K and N
-    off the 256 / 16 grids; the long-K case (K = 4160) exceeds the
-    streaming core's LDS panel, so cfg 0 runs the ring as well."""
+    configuration of the LDS DMA ring with gathered token rows,
+    gate_up-style and down-style, bit-exact against the oracle.  The ragged
+    case has K and N off the 256 / 16 grids; the long-K case has K = 4160
+    (17 ring stages of 256 bytes, split unevenly over the waves)."""
     from minisgl_amd.kernel import lib as mw8lib
 
     lib = mw8lib.load()
@@ -342,7 +340,7 @@ def test_grouped_small_blocks_every_config(shape):
                 q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
                 routed=None if routed is None else w_ref, return_acc=True,
             )
-            for cfg in range(-1, NUM_SMALL_CFGS):
+            for cfg in range(-1, _tuning_count(3)):
                 announce(f"grouped small {shape} gemm{which} cfg={cfg}")
                 lib.mw8_set_tuning(-1, -1, cfg)
                 out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
@@ -357,15 +355,14 @@ def test_grouped_small_blocks_every_config(shape):
 
 
 @pytest.mark.parametrize("B", [64, 128])
-def test_grouped_run_tiles(B):
-    """Run tiles (one tile over up to 256 / B consecutive alignment blocks
-    of one expert) on skewed routing: one expert owns 68+ blocks (the
-    backward scan for its first block crosses 64 blocks and its runs split
-    into several tiles), others own 1-3 blocks (short runs), some none;
-    N and the pair count are not tile multiples.  Bit-exact int32 and bf16
-    for the run-tile and persistent configurations (whose item lists cut
-    the long runs into chunks and skip padding fragments), gate_up-style
-    (A row = pair // top_k) and down-style (top_k 1, routed weight)."""
+def test_grouped_skewed_routing(B):
+    """Skewed routing: one expert owns 70 alignment blocks (its run is cut
+    into several chunk items), others own 1-3 blocks (short runs), some
+    none; N and the pair count are not tile multiples.  Bit-exact int32
+    and bf16 for the one-tile-per-block grid and the persistent walk
+    (whose item lists cut the long runs into chunks and skip padding
+    fragments), gate_up-style (A row = pair // top_k) and down-style
+    (top_k 1, routed weight)."""
     from minisgl_amd.kernel import lib as mw8lib
 
     announce(f"grouped run tiles B={B}")
@@ -396,7 +393,7 @@ def test_grouped_run_tiles(B):
                 q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, top_k,
                 routed=routed, return_acc=True,
             )
-            for cfg in (-1, 0, 7, 8, *range(9, 20)):
+            for cfg in range(-1, _tuning_count(2)):
                 announce(f"run tiles B={B} gemm{which} cfg={cfg}")
                 lib.mw8_set_tuning(-1, -1, cfg)
                 out = torch.empty(M * k, N, dtype=torch.bfloat16, device=DEV)
@@ -408,49 +405,6 @@ def test_grouped_run_tiles(B):
                 assert bf16_bits_equal(out, y_ref).all(), f"cfg {cfg}"
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
-
-
-@pytest.mark.parametrize("shape", ["cfg3", "ragged", "ragged_big"])
-@pytest.mark.parametrize("B", [16, 32, 64, 128])
-def test_fused_slot_sum_equals_gemm_then_sum(shape, B):
-    """GEMM2 with the slot sum fused in (one launch): the pair rows equal
-    fused_moe_kernel_w8a8 (routed weight, top_k 1) and the token rows equal
-    moe_sum_reduce of them, bit for bit, against the oracle, on the DMA ring
-    (16- and 32-row blocks), the one-tile-per-block grid and the persistent
-    walk (ragged_big: at least 32 pairs per expert).  Each case runs twice
-    on one counter buffer, the second time on fewer tokens, and the
-    counters must be back to zero after each call."""
-    if shape == "cfg3":
-        c = moe_case(96, seed=97)
-        M, k = 96, 8
-        logits, W, SW = c["logits"], c["w2"], c["s_w2"]
-        gen = torch.Generator().manual_seed(97)
-        act = torch.randn(M * k, W.shape[2], generator=gen).to(torch.bfloat16)
-    elif shape == "ragged":
-        M, k = 50, 2
-        logits, W, SW, act = _ragged_expert_case(13, M=M, k=k, E=8, N=208, K=384)
-    else:
-        M, k = 400, 2
-        logits, W, SW, act = _ragged_expert_case(14, M=M, k=k, E=8, N=208, K=384)
-    E, N, K = W.shape
-    Wd, SWd = W.to(DEV), SW.to(DEV)
-    counters = torch.zeros(M * ((N + 15) // 16), dtype=torch.int32, device=DEV)
-    for m in (M, M // 3):  # second call: fewer tokens on the same counters
-        announce(f"fused slot sum {shape} B={B} M={m}")
-        w_ref, ids_ref = orc.topk_softmax(f32(logits[:m]), k, True)
-        q, s = quant_per_token(act[: m * k].to(DEV))
-        y_ref = orc.grouped_gemm_w8a8(q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(), ids_ref, 1,
-                                      routed=w_ref)
-        o_ref = orc.moe_sum_reduce(y_ref.reshape(m, k, N))
-        sorted_ids, expert_ids, npp = moe_align_block_size(torch.from_numpy(ids_ref).to(DEV), B, E)
-        cache = torch.empty(m * k, N, dtype=torch.bfloat16, device=DEV)
-        out = torch.empty(m, N, dtype=torch.bfloat16, device=DEV)
-        fused_moe_kernel_sum_w8a8(q, s, Wd, SWd, cache, out, torch.from_numpy(w_ref).to(DEV), sorted_ids,
-                                  expert_ids, npp, k, B, m * k, counters=counters)
-        torch.cuda.synchronize()
-        assert bf16_bits_equal(cache, y_ref).all(), f"M={m}: pair rows"
-        assert bf16_bits_equal(out, o_ref).all(), f"M={m}: slot sums"
-        assert int(counters.abs().sum().item()) == 0, f"M={m}: counters not reset"
 
 
 def test_sum_reduce():
@@ -523,3 +477,126 @@ def test_moe_layer_stagewise(M):
     o_ref = orc.moe_sum_reduce(f32(c3).reshape(M, 8, 2048))
     assert bf16_bits_equal(o, o_ref).all()
     assert bf16_bits_equal(out, o_ref).all()  # the layer's result equals the staged chain
+
+
+def _moe_layer(c, apply_router_weight_on_input=False, E=128, k=8, H=2048, I=768):
+    layer = MoELayer(E, k, H, I, renormalize=True, apply_router_weight_on_input=apply_router_weight_on_input)
+    layer.load_state_dict({
+        "gate_up_proj": c["w1"].to(DEV), "down_proj": c["w2"].to(DEV),
+        "gate_up_scale": c["s_w1"].to(DEV), "down_scale": c["s_w2"].to(DEV),
+    })
+    return layer
+
+
+@pytest.mark.parametrize("M", [4, 64, 300, 4096])
+def test_moe_layer_router_weight_on_input(M):
+    """apply_router_weight_on_input=True through MoELayer: the routed weight
+    multiplies GEMM1's epilogue and GEMM2 runs without it
+    (python/minisgl/moe/fused.py:201,217).  Stage-wise against the oracle on
+    the GPU's own stage inputs, the layer bit-identical to the staged chain,
+    and the end-to-end CPU chain within 1e-3."""
+    announce(f"moe router weight on input M={M}")
+    c = moe_case(M, seed=M + 3)
+    layer = _moe_layer(c, apply_router_weight_on_input=True)
+    set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+    try:
+        h = c["hidden"].to(DEV)
+        out = layer.forward(h, c["logits"].to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        reset_global_ctx()
+    ref = orc.fused_moe_w8a8(f32(c["hidden"]), c["w1"].numpy(), c["s_w1"].numpy(), c["w2"].numpy(),
+                             c["s_w2"].numpy(), f32(c["logits"]), 8, apply_router_weight_on_input=True)
+    assert rel_l2(f32(out), ref) <= 1e-3
+    # stage-wise
+    tw, ids = topk_softmax(c["logits"].to(DEV), 8, True)
+    w_ref, ids_ref = orc.topk_softmax(f32(c["logits"]), 8, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    hq, hs = quant_per_token(c["hidden"].to(DEV))
+    q_ref, s_ref = orc.quant_per_token(f32(c["hidden"]))
+    B = get_default_config(M, 128, 0, 0, 8)["BLOCK_SIZE_M"]
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, B, 128)
+    c1 = torch.empty(M * 8, 1536, dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_w8a8(hq, hs, c["w1"].to(DEV), c["s_w1"].to(DEV), c1, tw, sorted_ids, expert_ids, npp,
+                          True, 8, B, M * 8)
+    c1_ref = orc.grouped_gemm_w8a8(q_ref, s_ref, c["w1"].numpy(), c["s_w1"].numpy(), ids_ref, 8,
+                                   routed=tw.cpu().numpy())
+    assert bf16_bits_equal(c1, c1_ref).all()
+    qa, sa = act_and_mul_quant(c1, "silu")
+    _, _, a = act_and_mul_quant(c1, "silu", return_act=True)
+    qa_ref, sa_ref = orc.quant_per_token(f32(a))
+    np.testing.assert_array_equal(qa.cpu().numpy(), qa_ref)
+    c3 = torch.empty(M * 8, 2048, dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_w8a8(qa, sa, c["w2"].to(DEV), c["s_w2"].to(DEV), c3, tw, sorted_ids, expert_ids, npp,
+                          False, 1, B, M * 8)
+    c3_ref = orc.grouped_gemm_w8a8(qa_ref, sa_ref, c["w2"].numpy(), c["s_w2"].numpy(), ids_ref, 1)
+    assert bf16_bits_equal(c3, c3_ref).all()
+    o_ref = orc.moe_sum_reduce(f32(c3).reshape(M, 8, 2048))
+    assert bf16_bits_equal(out, o_ref).all()
+
+
+@pytest.mark.parametrize("M", [8, 300])
+def test_moe_step_by_step_path(M):
+    """The step-by-step orchestration (fused_topk -> fused_experts_impl_w8a8,
+    the counterpart of python/minisgl/moe/fused.py:127-227) that the
+    backend takes for a non-contiguous router output, bit-identical to the
+    fast paths on the same inputs; a non-contiguous hidden_states is
+    rejected as the reference rejects it (:142)."""
+    from minisgl_amd.moe.fused import fused_experts_impl_w8a8, fused_topk
+
+    announce(f"moe step-by-step M={M}")
+    c = moe_case(M, seed=M + 11)
+    layer = _moe_layer(c)
+    set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+    try:
+        fast = c["hidden"].to(DEV)
+        layer.forward(fast, c["logits"].to(DEV))
+        wide = torch.zeros(M, 256, dtype=torch.bfloat16, device=DEV)
+        wide[:, :128] = c["logits"].to(DEV)
+        slow = c["hidden"].to(DEV)
+        layer.forward(slow, wide[:, :128])  # non-contiguous gating_output
+        h = c["hidden"].to(DEV)
+        tw, ids = fused_topk(h, c["logits"].to(DEV), 8, True)
+        direct = fused_experts_impl_w8a8(h, layer.gate_up_proj, layer.gate_up_scale, layer.down_proj,
+                                         layer.down_scale, tw, ids)
+        torch.cuda.synchronize()
+        assert torch.equal(slow.view(torch.int16), fast.view(torch.int16))
+        assert torch.equal(direct.view(torch.int16), fast.view(torch.int16))
+        strided = torch.zeros(M, 4096, dtype=torch.bfloat16, device=DEV)[:, :2048]
+        with pytest.raises(AssertionError, match="contiguous"):
+            layer.forward(strided, c["logits"].to(DEV))
+    finally:
+        reset_global_ctx()
+    ref = orc.fused_moe_w8a8(f32(c["hidden"]), c["w1"].numpy(), c["s_w1"].numpy(), c["w2"].numpy(),
+                             c["s_w2"].numpy(), f32(c["logits"]), 8)
+    assert rel_l2(f32(fast), ref) <= 1e-3
+
+
+def test_fused_topk_marks_padded_tokens():
+    """num_token_non_padded (a device tensor): tokens at or past it get ids
+    -1 (python/minisgl/moe/fused.py:25-27), which the alignment skips."""
+    from minisgl_amd.moe.fused import fused_topk
+
+    announce("fused_topk padding")
+    gen = torch.Generator().manual_seed(9)
+    logits = torch.randn(10, 16, generator=gen).to(torch.bfloat16).to(DEV)
+    h = torch.zeros(10, 64, dtype=torch.bfloat16, device=DEV)
+    w, ids = fused_topk(h, logits, 4, True, num_token_non_padded=torch.tensor(7, device=DEV))
+    w_ref, ids_ref = orc.topk_softmax(f32(logits), 4, True)
+    got = ids.cpu().numpy()
+    np.testing.assert_array_equal(got[:7], ids_ref[:7])
+    assert (got[7:] == -1).all()
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, 16, 16)
+    torch.cuda.synchronize()
+    s = sorted_ids.cpu().numpy()[: int(npp.item())]
+    assert set(s[s < 40].tolist()) == set(range(28))  # only the 7 x 4 unpadded pairs are placed
+
+
+def test_backend_rejects_unsupported_sizes():
+    be = create_moe_backend("fused_w8a8")
+    h = torch.zeros(2, 40, dtype=torch.bfloat16, device=DEV)
+    w1 = torch.zeros(4, 64, 40, dtype=torch.int8, device=DEV)
+    w2 = torch.zeros(4, 40, 32, dtype=torch.int8, device=DEV)
+    with pytest.raises(ValueError, match="multiples of 16"):
+        be.forward(h, w1, w2, torch.zeros(2, 4, device=DEV), 2, True,
+                   w1_scale=torch.ones(4, 64, device=DEV), w2_scale=torch.ones(4, 40, device=DEV))

@@ -112,3 +112,68 @@ def test_rmsnorm_quant_in_a_graph():
         torch.cuda.synchronize()
         np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
         np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("M", [1, 37, 300])
+def test_rmsnorm_inplace_on_qkv_head_views(M):
+    """The Qwen3 q/k norms normalize per-head views of a qkv split in place
+    (RMSNorm.forward_inplace(q.view(-1, heads, head_dim)),
+    python/minisgl/layers/attention.py:49-53).  Those views are not
+    contiguous (row stride = qkv width); the result must land in qkv itself:
+    q and k rows bit-exact against the oracle's RMSNorm of each head row, v
+    untouched."""
+    announce(f"rmsnorm qk head views M={M}")
+    nq, nkv, D = 8, 2, 128
+    gen = torch.Generator().manual_seed(M)
+    qkv_cpu = torch.randn(M, (nq + 2 * nkv) * D, generator=gen).to(torch.bfloat16)
+    wq = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    eps = 1e-6
+    qkv = qkv_cpu.to(DEV)
+    q, k, v = qkv.split([nq * D, nkv * D, nkv * D], dim=-1)
+    qn, kn = RMSNorm(D, eps), RMSNorm(D, eps)
+    qn.weight, kn.weight = wq.to(DEV), wk.to(DEV)
+    # out-of-place forward on the view returns the normalized heads
+    y = qn.forward(q.view(-1, nq, D))
+    qn.forward_inplace(q.view(-1, nq, D))
+    kn.forward_inplace(k.view(-1, nkv, D))
+    torch.cuda.synchronize()
+    q_rows = f32(qkv_cpu[:, : nq * D]).reshape(M * nq, D)
+    k_rows = f32(qkv_cpu[:, nq * D : (nq + nkv) * D]).reshape(M * nkv, D)
+    yq = orc.rmsnorm_quant(q_rows, f32(wq), eps)[2].reshape(M, nq * D)
+    yk = orc.rmsnorm_quant(k_rows, f32(wk), eps)[2].reshape(M, nkv * D)
+    got = qkv.cpu()
+    assert bf16_bits_equal(got[:, : nq * D], yq).all()
+    assert bf16_bits_equal(got[:, nq * D : (nq + nkv) * D], yk).all()
+    assert torch.equal(got[:, (nq + nkv) * D :].view(torch.int16), qkv_cpu[:, (nq + nkv) * D :].view(torch.int16))
+    assert y.shape == (M, nq, D) and bf16_bits_equal(y.reshape(M, nq * D), yq).all()
+
+
+def test_rmsnorm_inplace_other_layouts_written_back():
+    """Layouts that are not [G, inner, H] row groups (a transposed view, a
+    residual update on a sliced view) are normalized in a copy and written
+    back into the caller's tensor."""
+    announce("rmsnorm other layouts")
+    gen = torch.Generator().manual_seed(5)
+    H, M = 256, 24
+    base = torch.randn(H, M, generator=gen).to(torch.bfloat16)
+    w = (torch.rand(H, generator=gen) + 0.5).to(torch.bfloat16)
+    xt = base.to(DEV).t()  # [M, H] with stride (1, M): last dim not contiguous
+    norm = RMSNorm(H, 1e-6)
+    norm.weight = w.to(DEV)
+    norm.forward_inplace(xt)
+    torch.cuda.synchronize()
+    y_ref = orc.rmsnorm_quant(f32(base.t().contiguous()), f32(w), 1e-6)[2]
+    assert bf16_bits_equal(xt.contiguous(), y_ref).all()
+    # fused residual add on strided views of wider buffers
+    xb = torch.randn(M, 2 * H, generator=gen).to(torch.bfloat16)
+    rb = torch.randn(M, 2 * H, generator=gen).to(torch.bfloat16)
+    xd, rd = xb.to(DEV), rb.to(DEV)
+    fused = RMSNormFused(H, 1e-6)
+    fused.weight = w.to(DEV)
+    xo, ro = fused.forward(xd[:, :H], rd[:, H:])
+    torch.cuda.synchronize()
+    _, _, y2, h2 = orc.rmsnorm_quant(f32(xb[:, :H]), f32(w), 1e-6, residual=f32(rb[:, H:]))
+    assert bf16_bits_equal(xd[:, :H].contiguous(), y2).all()
+    assert bf16_bits_equal(rd[:, H:].contiguous(), h2).all()
+    assert xo.data_ptr() == xd.data_ptr() and ro.data_ptr() == rd.data_ptr() + 2 * H
