@@ -163,6 +163,22 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
                        size_t workspace_bytes, mw8_stream_t stream);
 
 /*
+ * mw8_gemm_w8a8_bf16 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The K split's partial tiles go to a static 64 MiB device
+ * array of the library (held on every device it runs on until the process
+ * ends); a shape whose split would need more returns MW8_ERR_WORKSPACE
+ * (none does on a 256-CU MI355X: the bound is mw8_gemm_workspace_max_bytes).
+ * Calls on one device share that array: calls that overlap on one device
+ * (concurrent streams) race.  Allocates nothing; results equal
+ * mw8_gemm_w8a8_bf16's bit for bit.
+ */
+int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                               mw8_stream_t stream);
+
+/*
  * Same GEMM, raw int32 accumulators acc [M, N] (parity hook; no scales).
  * Test hook for the A4 int32 contract; no reference counterpart.
  */

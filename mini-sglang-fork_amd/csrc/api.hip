@@ -36,6 +36,8 @@ int gemm_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, con
                    int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 int gemm_w8a8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, void*, size_t,
                   hipStream_t);
+int gemm_w8a8_bf16_noalloc(const int8_t*, const float*, const int8_t*, const float*, const void*, void*,
+                           int64_t, int64_t, int64_t, hipStream_t);
 int topk_softmax(const void*, int, int64_t, int, int, int, float*, int32_t*, hipStream_t);
 int64_t moe_align_max_padded(int64_t, int, int);
 int moe_align_block_size(const int32_t*, int64_t, int, int, int32_t*, int32_t*, int32_t*, hipStream_t);
@@ -114,6 +116,11 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,
                        size_t ws_bytes, mw8_stream_t st) {
   MW8_ENTRY(mw8::gemm_w8a8_bf16(A, sa, W, sw, bias, y, M, N, K, ws, ws_bytes, S(st)));
+}
+
+int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const void* bias, void* y, int64_t M, int64_t N, int64_t K, mw8_stream_t st) {
+  MW8_ENTRY(mw8::gemm_w8a8_bf16_noalloc(A, sa, W, sw, bias, y, M, N, K, S(st)));
 }
 
 int mw8_gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int64_t N,
