@@ -194,6 +194,11 @@ def main() -> int:
                          "shapes with M >= 512")
     ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=1,
+                    help="--mode gemm: distinct weight copies the launches rotate through (the timed "
+                         "configuration keeps >= 600 MB of copies per shape, past the 256 MB MALL)")
+    ap.add_argument("--tuning", default="-1,-1,-1",
+                    help="--mode gemm: decode,tile,moe configuration override (mw8_set_tuning)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); "
@@ -301,10 +306,7 @@ def main() -> int:
             "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2),
             "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
             "bound": bound, "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
-            # the library's path choice: the LDS-ring decode core up to 32 rows
-            # (the register decode core at 33-64 rows when K % 128 != 0)
-            "kernel": ("decode3_gemm_kernel" if M <= 32 else
-                       "decode_gemm_kernel" if M <= 64 and K % 128 else "tile3_gemm_kernel"),
+            "kernel": lib.mw8_gemm_kernel_name(M, N, K).decode(),
         })
     dom = max(shapes, key=lambda r: r["us"])
     dom_ops = 2.0 * dom["M"] * dom["N"] * dom["K"]
@@ -409,15 +411,22 @@ def profile_mode(args) -> int:
         print(json.dumps({"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
                           "reps": args.reps}))
         return 0
+    from minisgl_amd.kernel import load
+
+    lib = load()
     M, N, K = (int(v) for v in args.shape.split(","))
-    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev)
+    d_cfg, t_cfg, m_cfg = (int(v) for v in args.tuning.split(","))
+    lib.mw8_set_tuning(d_cfg, t_cfg, m_cfg)
+    ws = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev)
+          for _ in range(max(1, args.copies))]
     sw = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
     q, s = quant_per_token(torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16))
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    for _ in range(args.reps):
-        gemm_w8a8(q, s, w, sw, out=y)
+    for i in range(args.reps):
+        gemm_w8a8(q, s, ws[i % len(ws)], sw, out=y)
     torch.cuda.synchronize()
-    print(json.dumps({"mode": "gemm", "M": M, "N": N, "K": K, "reps": args.reps,
+    print(json.dumps({"mode": "gemm", "M": M, "N": N, "K": K, "reps": args.reps, "copies": len(ws),
+                      "kernel": lib.mw8_gemm_kernel_name(M, N, K).decode(), "tuning": args.tuning,
                       "algorithmic_bytes": gemm_bytes(M, N, K)}))
     return 0
 

@@ -129,6 +129,15 @@ void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 int32_t mw8_tuning_count(int32_t kind);
 
 /*
+ * Name of the kernel family mw8_gemm_w8a8_* runs for (M, N, K) under the
+ * current tuning ("decode3_gemm_kernel", "decode_gemm_kernel",
+ * "ksplit_gemm_kernel", "tile3_gemm_kernel", "tile_gemm_kernel"; "" for
+ * invalid sizes), matching the names in a kernel trace.  Profiling aid; no
+ * reference counterpart.
+ */
+const char* mw8_gemm_kernel_name(int64_t M, int64_t N, int64_t K);
+
+/*
  * Bytes of workspace mw8_gemm_w8a8_* uses for (M, N, K): the int32 partial
  * tiles of the tile core's K split (for the tiling the call will choose,
  * including a mw8_set_tuning override: with T tiles and S = CUs x resident

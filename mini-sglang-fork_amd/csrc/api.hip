@@ -32,6 +32,7 @@ size_t gemm_workspace_bytes(int64_t, int64_t, int64_t);
 size_t gemm_workspace_max_bytes();
 void set_tuning(int, int, int);
 int tuning_count(int);
+const char* gemm_kernel_name(int64_t, int64_t, int64_t);
 int gemm_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, const void*, void*,
                    int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 int gemm_w8a8_i32(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, void*, size_t,
@@ -111,6 +112,8 @@ size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 size_t mw8_gemm_workspace_max_bytes(void) { return mw8::gemm_workspace_max_bytes(); }
 
 int32_t mw8_tuning_count(int32_t kind) { return mw8::tuning_count(kind); }
+
+const char* mw8_gemm_kernel_name(int64_t M, int64_t N, int64_t K) { return mw8::gemm_kernel_name(M, N, K); }
 
 int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,

@@ -2,8 +2,10 @@
 // when K % 128 != 0: weight streaming, in-block split-K) and the MFMA tile
 // ring, plus the grouped-tile launchers used by the fused-MoE GEMM.
 #include <atomic>
+#include <type_traits>
 
 #include "gemm_kernels.h"
+#include "gemm_ksplit.h"
 
 namespace mw8 {
 
@@ -178,7 +180,47 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 128, true, 128, 2, true},    // 4: ring, 4 waves (2x2), 2 stages, two per CU
     {64, 128, true, 128, 1, true},     // 5: ring, 4 waves (1x4), 4 stages
 };
-constexpr int kNumTileCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
+constexpr int kNumRingCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
+
+// In-block split-K configurations (ksplit_gemm_kernel), tile cfg
+// kNumRingCfgs + i: block tile BM x BN, KG K groups of WM x WN waves, KS
+// 32-byte k-steps per group and stage, NSTAGE stages.
+struct KsplitCfg {
+  int bm, bn, kg, wm, wn, ks, nstage;
+};
+constexpr KsplitCfg kKsplitCfgs[] = {
+    {64, 32, 8, 1, 1, 1, 4},    // 0: 256-byte stages, waves of 64 x 32
+    {64, 32, 8, 1, 1, 2, 3},    // 1: 512-byte stages, waves of 64 x 32
+    {64, 64, 8, 1, 1, 1, 4},    // 2: 256-byte stages, waves of 64 x 64
+    {128, 64, 4, 2, 1, 2, 3},   // 3: 256-byte stages, waves of 64 x 64, 2 k-steps per stage
+    {128, 128, 2, 2, 2, 2, 4},  // 4: 128-byte stages, waves of 64 x 64, 2 k-steps
+    {128, 128, 2, 2, 2, 4, 2},  // 5: 256-byte stages, waves of 64 x 64, 4 k-steps
+    {128, 128, 4, 2, 1, 1, 4},  // 6: 128-byte stages, waves of 64 x 128
+    {128, 128, 4, 2, 1, 2, 2},  // 7: 256-byte stages, waves of 64 x 128, 2 k-steps
+    {128, 96, 4, 2, 1, 2, 2},   // 8: 256-byte stages, waves of 64 x 96, 2 k-steps
+    {64, 128, 4, 1, 2, 2, 3},   // 9: 256-byte stages, waves of 64 x 64, 2 k-steps
+};
+constexpr int kNumKsplitCfgs = sizeof(kKsplitCfgs) / sizeof(kKsplitCfgs[0]);
+constexpr int kNumTileCfgs = kNumRingCfgs + kNumKsplitCfgs;
+
+constexpr int ksplit_sk(const KsplitCfg& c) { return c.kg * c.ks * 32; }
+
+// Column ranges of a ksplit grid over N: the fewest whose boundaries are
+// multiples of 16 and whose widest range fits BN, raised so that the grid
+// of gm x gn blocks fills whole waves of the CUs.  0 if no range fits.
+int64_t ksplit_ranges(int64_t M, int64_t N, const KsplitCfg& c, int64_t& gm) {
+  gm = (M + c.bm - 1) / c.bm;
+  const int64_t n16 = N / 16, tail = N % 16;
+  const int64_t q = (c.bn - tail) / 16;  // 16-column groups a range may hold
+  if (q < 1) return 0;
+  int64_t gn = n16 == 0 ? 1 : (n16 + q - 1) / q;
+  const int64_t cus = device_cus();
+  const int64_t waves = (gm * gn + cus - 1) / cus;
+  const int64_t fill = waves * cus / gm;
+  const int64_t most = n16 > 0 ? n16 : 1;  // every range keeps at least 16 columns
+  if (fill > gn) gn = fill < most ? fill : most;
+  return gn;
+}
 
 // K split of a ring tiling.  With T tiles and S = CUs * per_cu resident
 // slots: T >= S cuts the r = T mod S tiles of the last, partial wave into
@@ -252,8 +294,30 @@ double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
   return us > stream_us ? us : stream_us;
 }
 
+// In-block split-K choice, measured on MI355X (us per launch, weights
+// streamed from HBM; auto = the best ring configuration):
+//              M = 40     64    128    256    512   1024
+//   qkv  ks     12.8   14.3   18.6   24.1   36.8   69.6
+//        auto   16.5   16.8   23.6   27.0   38.7   42.9
+//   o    ks     11.8   13.2   16.7   21.8   32.3   62.4
+//        auto   15.9   16.5   19.3   26.1   37.4   40.5
+// (ks: 64 x 32 tiles with 512-byte stages up to 64 rows, 64 x 64 tiles to
+// 128, 128 x 64 to 256-384, 128 x 128 with two K groups above.)  With K >
+// 8192 (down, K = 17408) every block re-reads a long token panel and with
+// N > 16384 (gate_up) the ring already fills the CUs: the ring wins there.
+int default_ksplit_cfg(int64_t M, int64_t N, int64_t K) {
+  if (M > 768 || N > 16384 || K > 8192) return -1;
+  if (M <= 64) return K % 512 == 0 ? 1 : (K % 256 == 0 ? 0 : -1);
+  if (K % 256 != 0) return -1;
+  if (M <= 128) return 2;
+  if (M <= 384) return 3;
+  return 4;
+}
+
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   if (K % 64 != 0) return 0;
+  const int ks = default_ksplit_cfg(M, N, K);
+  if (ks >= 0) return kNumRingCfgs + ks;
   int best = 1;
   double best_us = 1e300;
   for (const ModelCfg& mc : kModelCfgs) {
@@ -268,11 +332,46 @@ int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
 }
 
 // The ring configuration a dense call at (M, N, K) runs (override first).
+bool tile_cfg_fits(int cfg, int64_t M, int64_t N, int64_t K) {
+  if (cfg < 0 || cfg >= kNumTileCfgs) return false;
+  if (cfg < kNumRingCfgs) return !kTileCfgs[cfg].dma || K % kTileCfgs[cfg].bk == 0;
+  const KsplitCfg& c = kKsplitCfgs[cfg - kNumRingCfgs];
+  int64_t gm = 0;
+  return K % ksplit_sk(c) == 0 && ksplit_ranges(M, N, c, gm) > 0;
+}
+
 int select_tile_cfg(int64_t M, int64_t N, int64_t K) {
   const int cfg = g_tile_cfg.load(std::memory_order_relaxed);
-  if (cfg < 0 || cfg >= kNumTileCfgs || (kTileCfgs[cfg].dma && K % kTileCfgs[cfg].bk != 0))
-    return default_tile_cfg(M, N, K);
+  if (!tile_cfg_fits(cfg, M, N, K)) return default_tile_cfg(M, N, K);
   return cfg;
+}
+
+template <int BM, int BN, int KG, int WM, int WN, int KS, int NSTAGE, int EPI>
+int launch_ksplit(const GemmArgs& g, hipStream_t st) {
+  using Sh = KsplitShape<BM, BN, KG, WM, WN, KS, NSTAGE>;
+  constexpr auto kern = ksplit_gemm_kernel<BM, BN, KG, WM, WN, KS, NSTAGE, EPI>;
+  if (const int rc = set_lds_limit<kern>(Sh::kLds)) return rc;
+  int64_t gm = 0;
+  const int64_t gn = ksplit_ranges(g.M, g.N, KsplitCfg{BM, BN, KG, WM, WN, KS, NSTAGE}, gm);
+  MW8_REQUIRE(gn > 0 && gm * gn < (int64_t{1} << 31), kErrShape, "gemm: no ksplit grid for N=%lld", (long long)g.N);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(gm * gn)), dim3(Sh::kThreads), Sh::kLds, st, g);
+  return kOk;
+}
+
+template <int EPI>
+int dispatch_ksplit(int i, const GemmArgs& g, hipStream_t st) {
+  switch (i) {
+    case 0: return launch_ksplit<64, 32, 8, 1, 1, 1, 4, EPI>(g, st);
+    case 1: return launch_ksplit<64, 32, 8, 1, 1, 2, 3, EPI>(g, st);
+    case 2: return launch_ksplit<64, 64, 8, 1, 1, 1, 4, EPI>(g, st);
+    case 3: return launch_ksplit<128, 64, 4, 2, 1, 2, 3, EPI>(g, st);
+    case 4: return launch_ksplit<128, 128, 2, 2, 2, 2, 4, EPI>(g, st);
+    case 5: return launch_ksplit<128, 128, 2, 2, 2, 4, 2, EPI>(g, st);
+    case 6: return launch_ksplit<128, 128, 4, 2, 1, 1, 4, EPI>(g, st);
+    case 7: return launch_ksplit<128, 128, 4, 2, 1, 2, 2, EPI>(g, st);
+    case 8: return launch_ksplit<128, 96, 4, 2, 1, 2, 2, EPI>(g, st);
+    default: return launch_ksplit<64, 128, 4, 1, 2, 2, 3, EPI>(g, st);
+  }
 }
 
 template <int BM, int BN, int EPI>
@@ -286,6 +385,7 @@ int launch_split_reduce(const GemmArgs& g, const SplitPlan& sp, hipStream_t st) 
 template <int EPI>
 int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   const int cfg = select_tile_cfg(g.M, g.N, g.K);
+  if (cfg >= kNumRingCfgs) return dispatch_ksplit<EPI>(cfg - kNumRingCfgs, g, st);
   const TileCfg c = kTileCfgs[cfg];
   unsigned tiles = static_cast<unsigned>(((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn));
   // K split (ring configurations): needs the caller's workspace
@@ -375,7 +475,8 @@ int tuning_count(int kind);
 
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || !use_tile_path(M, K)) return 0;
-  return plan_split(M, N, K, kTileCfgs[select_tile_cfg(M, N, K)]).ws;
+  const int cfg = select_tile_cfg(M, N, K);
+  return cfg < kNumRingCfgs ? plan_split(M, N, K, kTileCfgs[cfg]).ws : 0;
 }
 
 size_t gemm_workspace_max_bytes() {
@@ -533,6 +634,20 @@ int launch_grouped_small_epi(const GemmArgs& g, unsigned blocks, hipStream_t st)
 }
 
 }  // namespace
+
+// Name of the kernel family a dense GEMM at (M, N, K) runs (tuning and
+// profiling aid: matches the kernel names of a trace).
+const char* gemm_kernel_name(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return "";
+  if (!use_tile_path(M, K)) {
+    int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+    if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
+    return kDecodeCfgs[cfg].core == 0 ? "decode_gemm_kernel" : "decode3_gemm_kernel";
+  }
+  const int cfg = select_tile_cfg(M, N, K);
+  if (cfg >= kNumRingCfgs) return "ksplit_gemm_kernel";
+  return kTileCfgs[cfg].dma ? "tile3_gemm_kernel" : "tile_gemm_kernel";
+}
 
 int tuning_count(int kind) {
   switch (kind) {

@@ -34,6 +34,7 @@ SIGNATURES = {
     "mw8_gemm_workspace_bytes": (c_size_t, [_I64, _I64, _I64]),
     "mw8_gemm_workspace_max_bytes": (c_size_t, []),
     "mw8_tuning_count": (_I32, [_I32]),
+    "mw8_gemm_kernel_name": (ctypes.c_char_p, [_I64, _I64, _I64]),
     "mw8_gemm_w8a8_bf16": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, c_size_t, _P],

@@ -202,30 +202,36 @@ def _tuning_count(kind):
 
 
 @pytest.mark.parametrize(
-    "M,K,N",
-    [(300, 640, 520), (257, 1024, 300), (129, 192, 64), (1000, 2048, 1000),
-     (40, 1024, 520), (64, 2560, 1100), (130, 3072, 700)],
+    "M,K,N,bias",
+    [(300, 640, 520, False), (257, 1024, 300, False), (129, 192, 64, False), (1000, 2048, 1000, False),
+     (40, 1024, 520, False), (64, 2560, 1100, False), (130, 3072, 700, False),
+     # K % 512 == 0: every in-block split-K configuration applies (partial row
+     # tiles, N off the 16-column grid, column ranges narrower than the tile)
+     (33, 1024, 1000, True), (64, 2048, 520, False), (100, 512, 36, True), (300, 1536, 1100, True),
+     (1000, 1024, 2000, False), (2080, 512, 5120, True)],
 )
-def test_gemm_every_tile_config(M, K, N):
+def test_gemm_every_tile_config(M, K, N, bias):
     """Each tile configuration (forced through mw8_set_tuning) on ragged
-    shapes; K % 64 != 0 makes the direct-to-LDS configs fall back.  33-64
-    rows take the tile core only when a tile configuration is forced; with
-    few tiles the split-capable rings split every tile's K range."""
+    shapes; a configuration whose K granularity does not divide K falls
+    back to the automatic choice.  33-64 rows take the tile core only when a
+    tile configuration is forced; with few tiles the split-capable rings
+    split every tile's K range."""
     from minisgl_amd.kernel.lib import load
 
-    announce(f"gemm all tile cfgs M={M} K={K} N={N}")
-    c = linear_case(M, K, N, seed=M)
+    announce(f"gemm all tile cfgs M={M} K={K} N={N} bias={bias}")
+    c = linear_case(M, K, N, seed=M, bias=bias)
     q, s = quant_per_token(c["x"].to(DEV))
     w, s_w = c["w"].to(DEV), c["s_w"].to(DEV)
+    b = c["bias"].to(DEV) if bias else None
     q_ref, s_ref = orc.quant_per_token(f32(c["x"]))
     acc_ref = orc.gemm_i32(q_ref, c["w"].numpy())
-    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy())
+    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy(), f32(c["bias"]) if bias else None)
     lib = load()
     try:
         for cfg in range(_tuning_count(1)):
             lib.mw8_set_tuning(-1, cfg, -1)
             np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
-            assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
+            assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w, b), y_ref).all(), f"cfg {cfg}"
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
 

@@ -38,14 +38,15 @@ def test_noalloc_gemm_equals_workspace_gemm():
     lib = load()
     # (M, N, K): o_proj at M=4096 (320 tiles of 256x256, 64 split into 4 K
     # ranges: 64 MiB of partial tiles, the whole scratch), then a smaller
-    # split shape, then a decode shape (no split)
-    for M, N, K, seed in ((4096, 5120, 5120, 1), (300, 1024, 2048, 2), (8, 2048, 1024, 3)):
+    # input that splits (gate_up at 64 tokens: 272 tiles of 64x128, 16 of
+    # them split 16 ways), then a decode shape (no split)
+    for M, N, K, seed in ((4096, 5120, 5120, 1), (64, 34816, 5120, 2), (8, 2048, 1024, 3)):
         announce(f"noalloc gemm M={M} N={N} K={K}")
         c = linear_case(M, K, N, seed=seed)
         q, s = quant_per_token(c["x"].to(DEV))
         w, sw = c["w"].to(DEV), c["s_w"].to(DEV)
         need = lib.mw8_gemm_workspace_bytes(M, N, K)
-        if M >= 300:
+        if M >= 64:
             assert need > 0, "the case must exercise the K split"
         y_ws, y_na = _both(lib, q, s, w, sw, M, N, K)
         assert torch.equal(y_na.view(torch.int16), y_ws.view(torch.int16)), f"M={M}"
