@@ -131,6 +131,81 @@ def roofline_frac(ops: float, nbytes: float, t_s: float, peak_tops: float) -> fl
 # CPU baseline: the CPU oracle (numpy, the "port") and the reference's CPU
 # torch op F.linear(x_bf16, W.bfloat16()) on a bounded sample of the sweep.
 # --------------------------------------------------------------------------
+def host_info():
+    """CPU model, core count, torch threads and torch's parallel_info of
+    the host the CPU baseline runs on."""
+    import subprocess
+
+    import torch
+
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:  # pragma: no cover - lscpu missing
+        pass
+    if model is None:
+        try:
+            with open("/proc/cpuinfo") as f:
+                model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+        except OSError:
+            model = None
+    info = torch.__config__.parallel_info()
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "parallel_info": [ln.strip() for ln in info.splitlines() if ln.strip()][:8]}
+
+
+def median_time(fn, warmup=3, runs=10, budget_s=60.0):
+    """Median wall time (s) of fn over up to `runs` runs after `warmup`
+    calls, within a wall budget (as the reference's CPU timing plan);
+    returns (median, runs done), or (None, 0) when the warm-ups exhaust it."""
+    t_start = time.perf_counter()
+    for _ in range(warmup):
+        fn()
+        if time.perf_counter() - t_start > budget_s:
+            return None, 0
+    times = []
+    while len(times) < runs and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_reference_configs():
+    """The BASELINE plan's CPU lines on the configurations it names: config
+    0 (the reference's bf16 F.linear and the W8A8 oracle, full shape) and
+    config 3 at 16 tokens (the oracle's restatement of fused_experts_impl,
+    per-expert loop), each the median of up to 10 runs after 3 warm-ups."""
+    import torch
+    import torch.nn.functional as F
+
+    from minisgl_amd.benchmark import linear_case, moe_case
+    from oracle import w8a8 as orc
+
+    res = {}
+    c = linear_case(16, 1024, 6144, seed=0)
+    wb = c["w"].to(torch.bfloat16)
+    t_ref, n_ref = median_time(lambda: F.linear(c["x"], wb))
+    xf, wn, sw = c["x"].float().numpy(), c["w"].numpy(), c["s_w"].numpy()
+    t_orc, n_orc = median_time(lambda: orc.linear_w8a8(xf, wn, sw))
+    ops = 2.0 * 16 * 1024 * 6144
+    res["cfg0"] = {"shape": "M16 K1024 N6144",
+                   "reference_torch_bf16_linear_ms": round(t_ref * 1e3, 4), "runs_ref": n_ref,
+                   "reference_torch_bf16_linear_tops": round(ops / t_ref / 1e12, 4),
+                   "oracle_w8a8_ms": round(t_orc * 1e3, 4), "runs_oracle": n_orc}
+    m = moe_case(16, seed=0)
+    args = (m["hidden"].float().numpy(), m["w1"].numpy(), m["s_w1"].numpy(), m["w2"].numpy(),
+            m["s_w2"].numpy(), m["logits"].float().numpy(), 8)
+    t_moe, n_moe = median_time(lambda: orc.fused_moe_w8a8(*args))
+    res["cfg3_m16"] = {"oracle_fused_moe_ms": None if t_moe is None else round(t_moe * 1e3, 3), "runs": n_moe,
+                       "oracle_tokens_per_s": None if t_moe is None else round(16 / t_moe, 1),
+                       "note": "oracle restatement of fused_experts_impl: route, quant, per-expert exact int "
+                               "GEMMs (fp64 BLAS), silu*mul, requant, routed GEMM2, slot sum"}
+    return res
 def cpu_baseline(shapes, m_sample: int, budget_s: float):
     import numpy as np
     import torch
@@ -188,10 +263,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
-    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "vendor"], default="bench",
-                    help="bench: the contract line; gemm / copy: one workload for rocprofv3 passes; "
-                         "vendor: this library against hipBLASLt int8 (torch._int_mm) at the config-1 "
-                         "shapes with M >= 512")
+    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "moe", "vendor"], default="bench",
+                    help="bench: the contract line; gemm / copy / moe: one workload for rocprofv3 passes "
+                         "(moe: the config-3 MoE layer at --tokens); vendor: this library against "
+                         "hipBLASLt int8 (torch._int_mm) at the config-1 shapes with M >= 512")
+    ap.add_argument("--tokens", type=int, default=4096, help="--mode moe: tokens per layer call")
     ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copies", type=int, default=1,
@@ -341,8 +417,20 @@ def main() -> int:
     secondary = None if args.no_secondary else run_secondary(dev, peak_tops)
     cpu = None if args.no_cpu_baseline else cpu_baseline(QWEN3_14B_SHAPES, 512, args.cpu_budget)
     if cpu:
+        cpu["host"] = host_info()
+        cpu["configs"] = cpu_reference_configs()
+        if secondary:
+            g0 = secondary.get("cfg0", {})
+            c0 = cpu["configs"]["cfg0"]
+            if g0.get("gemm_us"):
+                c0["gpu_gemm_us"] = g0["gemm_us"]
+                c0["gpu_speedup_vs_reference_cpu"] = round(c0["reference_torch_bf16_linear_ms"] * 1e3 / g0["forward_us"], 1)
+            g3 = secondary.get("moe_cfg3", {}).get("16")
+            if g3 and cpu["configs"]["cfg3_m16"]["oracle_fused_moe_ms"]:
+                cpu["configs"]["cfg3_m16"]["gpu_tokens_per_s"] = g3["tokens_per_s"]
         log(f"cpu baseline: {cpu['value']:.3f} TOPS ({cpu['cores']} threads); torch bf16 "
-            f"F.linear {cpu['reference_torch_bf16_linear_tops']:.3f} TOPS")
+            f"F.linear {cpu['reference_torch_bf16_linear_tops']:.3f} TOPS; host {cpu['host']['cpu_model']}; "
+            f"configs {cpu['configs']}")
 
     out = {
         "metric": METRIC,
@@ -401,6 +489,27 @@ def profile_mode(args) -> int:
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
+    if args.mode == "moe":
+        from minisgl_amd.benchmark import moe_case
+        from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
+        from minisgl_amd.kernel import load
+        from minisgl_amd.layers import MoELayer
+        from minisgl_amd.moe import create_moe_backend
+
+        d_cfg, t_cfg, m_cfg = (int(v) for v in args.tuning.split(","))
+        load().mw8_set_tuning(d_cfg, t_cfg, m_cfg)
+        c = moe_case(args.tokens, seed=0)
+        layer = MoELayer(128, 8, 2048, 768)
+        layer.load_state_dict({"gate_up_proj": c["w1"].to(dev), "down_proj": c["w2"].to(dev),
+                               "gate_up_scale": c["s_w1"].to(dev), "down_scale": c["s_w2"].to(dev)})
+        set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+        h0, lg = c["hidden"].to(dev), c["logits"].to(dev)
+        for _ in range(args.reps):
+            layer.forward(h0.clone(), lg)
+        torch.cuda.synchronize()
+        reset_global_ctx()
+        print(json.dumps({"mode": "moe", "tokens": args.tokens, "reps": args.reps, "tuning": args.tuning}))
+        return 0
     if args.mode == "copy":
         nbytes = 1 << 30
         src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, generator=gen, device=dev)
@@ -503,6 +612,51 @@ def run_secondary(dev, peak_tops):
 
     res = {}
     gen = torch.Generator(device=dev).manual_seed(1)
+
+    # config 0 (M=16, K=1024, N=6144) and the Qwen3-14B shapes at M <= 16:
+    # the GEMM alone and the layer's full forward (per-token quantization of
+    # the bf16 input + GEMM), each launch on its own weight copy (>= 600 MB
+    # of copies, past the MALL)
+    from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES
+    from minisgl_amd.layers.linear import LinearReplicated
+
+    def small_m(M, K, N, label):
+        ncopy = max(16, -(-600_000_000 // (N * K)))
+        ws = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev) for _ in range(ncopy)]
+        sw = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        q, s = quant_per_token(x)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        i = [0]
+
+        def gemm():
+            gemm_w8a8(q, s, ws[i[0] % ncopy], sw, out=y)
+            i[0] += 1
+
+        layers = []
+        for w in ws:
+            layer = LinearReplicated(K, N, has_bias=False)
+            layer.weight, layer.weight_scale = w, sw
+            layers.append(layer)
+
+        def forward():
+            layers[i[0] % ncopy].forward(x)
+            i[0] += 1
+
+        t_g = perf_hip(gemm, graph_calls=ncopy, repetitions=3) * 1e-3
+        t_f = perf_hip(forward, graph_calls=ncopy, repetitions=3) * 1e-3
+        nb = gemm_bytes(M, N, K)
+        return {"shape": label, "M": M, "K": K, "N": N, "gemm_us": round(t_g * 1e6, 2),
+                "forward_us": round(t_f * 1e6, 2), "gemm_gbps": round(nb / t_g / 1e9, 1),
+                "gemm_roofline_frac": round(roofline_frac(2.0 * M * N * K, nb, t_g, peak_tops), 4),
+                "forward_roofline_frac": round(roofline_frac(2.0 * M * N * K, nb + 3 * M * K + 4 * M, t_f, peak_tops), 4)}
+
+    res["cfg0"] = small_m(16, 1024, 6144, "cfg0 Qwen3-0.6B gate_up")
+    log(f"cfg0: {res['cfg0']}")
+    res["forward_small_m"] = [small_m(M, K, N, name) for M in (1, 8) for name, K, N in QWEN3_14B_SHAPES]
+    for r in res["forward_small_m"]:
+        log(f"forward {r['shape']:8s} M={r['M']}: gemm {r['gemm_us']} us, quant+gemm {r['forward_us']} us")
+
     # config 2: quantizer [8192, 17408]
     M, K = 8192, 17408
     x = torch.randn(M, K, generator=gen, device=dev)
