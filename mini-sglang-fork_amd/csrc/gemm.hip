@@ -194,11 +194,6 @@ constexpr KsplitCfg kKsplitCfgs[] = {
     {64, 64, 8, 1, 1, 1, 4},    // 2: 256-byte stages, waves of 64 x 64
     {128, 64, 4, 2, 1, 2, 3},   // 3: 256-byte stages, waves of 64 x 64, 2 k-steps per stage
     {128, 128, 2, 2, 2, 2, 4},  // 4: 128-byte stages, waves of 64 x 64, 2 k-steps
-    {128, 128, 2, 2, 2, 4, 2},  // 5: 256-byte stages, waves of 64 x 64, 4 k-steps
-    {128, 128, 4, 2, 1, 1, 4},  // 6: 128-byte stages, waves of 64 x 128
-    {128, 128, 4, 2, 1, 2, 2},  // 7: 256-byte stages, waves of 64 x 128, 2 k-steps
-    {128, 96, 4, 2, 1, 2, 2},   // 8: 256-byte stages, waves of 64 x 96, 2 k-steps
-    {64, 128, 4, 1, 2, 2, 3},   // 9: 256-byte stages, waves of 64 x 64, 2 k-steps
 };
 constexpr int kNumKsplitCfgs = sizeof(kKsplitCfgs) / sizeof(kKsplitCfgs[0]);
 constexpr int kNumTileCfgs = kNumRingCfgs + kNumKsplitCfgs;
@@ -365,12 +360,7 @@ int dispatch_ksplit(int i, const GemmArgs& g, hipStream_t st) {
     case 1: return launch_ksplit<64, 32, 8, 1, 1, 2, 3, EPI>(g, st);
     case 2: return launch_ksplit<64, 64, 8, 1, 1, 1, 4, EPI>(g, st);
     case 3: return launch_ksplit<128, 64, 4, 2, 1, 2, 3, EPI>(g, st);
-    case 4: return launch_ksplit<128, 128, 2, 2, 2, 2, 4, EPI>(g, st);
-    case 5: return launch_ksplit<128, 128, 2, 2, 2, 4, 2, EPI>(g, st);
-    case 6: return launch_ksplit<128, 128, 4, 2, 1, 1, 4, EPI>(g, st);
-    case 7: return launch_ksplit<128, 128, 4, 2, 1, 2, 2, EPI>(g, st);
-    case 8: return launch_ksplit<128, 96, 4, 2, 1, 2, 2, EPI>(g, st);
-    default: return launch_ksplit<64, 128, 4, 1, 2, 2, 3, EPI>(g, st);
+    default: return launch_ksplit<128, 128, 2, 2, 2, 2, 4, EPI>(g, st);
   }
 }
 

@@ -16,8 +16,10 @@
 //    of W, moved global -> LDS with buffer_load ... lds (1 KB per wave
 //    instruction, 16-byte chunks XOR-swizzled by row so the fragment reads
 //    are bank-conflict-free), NSTAGE stages in flight, one barrier each;
-//  * after the last stage the KG partial tiles are summed with LDS integer
-//    atomics (exact, order-free) and the epilogue runs once per element;
+//  * after the last stage the KG partial tiles are summed through LDS:
+//    each K group finalizes 1/KG of every lane's accumulators (exact int32
+//    adds), applies the epilogue with scales fetched before the main loop,
+//    and stages its bf16 values for 16-byte row stores;
 //  * the grid is G_m x G_n blocks: G_m = ceil(M / BM) row tiles and G_n
 //    column ranges whose boundaries are multiples of 16 and whose count
 //    makes the grid a multiple of the CU count, so every CU streams the same
@@ -61,18 +63,31 @@ struct KsplitShape {
   static constexpr int kLA = (kInstA + kWaves - 1) / kWaves, kLB = (kInstB + kWaves - 1) / kWaves;
   static constexpr int kL = kLA + kLB;
   static constexpr bool kPad = kLA * kWaves != kInstA || kLB * kWaves != kInstB;
-  static constexpr int kRedLd = BN + 8;               // reduction row stride (ints): rows r, r+4 on disjoint banks
   static constexpr int kRing = NSTAGE * kStage + (kPad ? 1024 : 0);
-  static constexpr int kRed = BM * kRedLd * 4;
-  static constexpr int kLds = kRing > kRed ? kRing : kRed;
   static constexpr int kWaveM = BM / WM, kWaveN = BN / WN, kFM = kWaveM / 32, kFN = kWaveN / 32;
   static constexpr int kSets = KS == 1 ? 1 : 2;       // fragment register sets
+  // Reduction of the KG partial tiles: each lane holds 16 * kF accumulators
+  // (flat index f * 16 + v over its kF = kFM * kFN fragments); K group g
+  // finalizes the kP of them in [g * kP, (g + 1) * kP) and receives the
+  // other groups' values of that range through LDS exchange slots, one per
+  // (owner, writer) pair: (KG - 1) * KG slots of WM * WN waves x kP / 4
+  // chunks x 64 lanes x 16 bytes.  The bf16 tile is then staged row-major
+  // (BN / 8 chunks of 16 bytes per row) behind the slots for 16-byte stores.
+  static constexpr int kF = kFM * kFN;
+  static constexpr int kP = 16 * kF / KG;
+  static constexpr int kXchg = (KG - 1) * KG * WM * WN * 64 * kP * 4;
+  static constexpr int kOC = BN / 8;
+  static constexpr int kEpi = kXchg + BM * BN * 2;
+  static constexpr int kLds = kRing > kEpi ? kRing : kEpi;
+  static_assert(kP % 4 == 0 && kP * KG == 16 * kF, "each K group finalizes whole 4-row groups");
+  static_assert(kOC == 4 || kOC == 8 || kOC == 16, "staged row of 4, 8 or 16 chunks");
+  static_assert(kThreads >= BM && kThreads >= BN, "one scale-table entry per thread");
   static_assert(kSK == 64 || kSK == 128 || kSK == 256 || kSK == 512, "stage of 64 - 512 K bytes");
   static_assert(KS == 1 || KS % 2 == 0, "one k-step per stage, or an even count");
   static_assert(kInstA * kRowsPerInst == BM && kInstB * kRowsPerInst == BN, "whole rows per DMA instruction");
   static_assert(kFM >= 1 && kFN >= 1 && kFM * 32 * WM == BM && kFN * 32 * WN == BN, "32 x 32 MFMA tiles");
   static_assert(NSTAGE >= 2 && (NSTAGE - 2) * kL < 64, "stages in flight fit the vmcnt counter");
-  static_assert(kLds <= 163840, "LDS budget");
+  static_assert(kLds + 4 * (BM + 2 * BN) <= 163840, "LDS budget (ring or exchange + staging, scale tables)");
 };
 
 template <int BM, int BN, int KG, int WM, int WN, int KS, int NSTAGE, int EPI>
@@ -97,6 +112,20 @@ __global__ __launch_bounds__(64 * KG * WM * WN) void ksplit_gemm_kernel(GemmArgs
   const int64_t n0 = ks_col0(g.N, jn, gn), nr = ks_col0(g.N, jn + 1, gn) - n0;
   const int64_t mr = g.M - m0 < BM ? g.M - m0 : BM;
   if (nr <= 0) return;  // block-uniform (host keeps every range non-empty)
+
+  // epilogue operands (row scales, column scales, bias) are loaded here into
+  // registers and kept in LDS tables from the prologue on, so the epilogue
+  // has no dependent global loads
+  constexpr bool kBf16 = epi_bf16_out(EPI);
+  __shared__ float t_sa[kBf16 ? BM : 1], t_sw[kBf16 ? BN : 1], t_bias[kBf16 ? BN : 1];
+  float v_sa = 0.0f, v_sw = 0.0f, v_bias = 0.0f;
+  if constexpr (kBf16) {
+    if (tid < mr) v_sa = g.sa[m0 + tid];
+    if (tid < nr) {
+      v_sw = g.sw[n0 + tid];
+      if (g.bias) v_bias = bf16_to_f32(g.bias[n0 + tid]);
+    }
+  }
 
   // buffer views: A rows [m0, m0 + mr), W rows [n0, n0 + nr); rows past them read zeros
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -181,6 +210,13 @@ __global__ __launch_bounds__(64 * KG * WM * WN) void ksplit_gemm_kernel(GemmArgs
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; ++s)
     if (s < nk) issue(s);
+  if constexpr (kBf16) {  // read after the main loop's barriers
+    if (tid < BM) t_sa[tid] = v_sa;
+    if (tid < BN) {
+      t_sw[tid] = v_sw;
+      t_bias[tid] = v_bias;
+    }
+  }
   for (int kt = 0; kt < nk; ++kt) {
     const int later = nk - 1 - kt;
     wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
@@ -194,52 +230,136 @@ __global__ __launch_bounds__(64 * KG * WM * WN) void ksplit_gemm_kernel(GemmArgs
     }
   }
 
-  // ---- sum the KG partial tiles in LDS (integer atomics: exact, order-free)
+  // ---- reduce the KG partial tiles (exact int32 adds).  Chunk q = (i * kFN
+  // + j) * 4 + h of a lane is the 4 accumulators v = 4h .. 4h + 3 of
+  // fragment (i, j): rows wm * kWaveM + 32 i + 8 h + 4 (lane / 32) + 0..3 of
+  // column wn * kWaveN + 32 j + lane % 32.  K group g finalizes chunks
+  // [g * kQo, (g + 1) * kQo); every other group writes its values of them
+  // to the slot (g, writer), conflict-free (64 lanes x 16 bytes per chunk).
+  constexpr int kQo = S::kP / 4;  // chunks each K group finalizes
   __syncthreads();  // every wave is past its last fragment read of the ring
-  int32_t* red = reinterpret_cast<int32_t*>(lds);
-  for (int e = tid; e < BM * S::kRedLd; e += S::kThreads) red[e] = 0;
-  __syncthreads();
+  auto slot = [&](int owner, int writer, int c) -> v4i* {
+    const int sl = owner * (KG - 1) + (writer < owner ? writer : writer - 1);
+    return reinterpret_cast<v4i*>(lds + ((sl * (WM * WN) + wsub) * kQo + c) * 1024 + lane * 16);
+  };
+  if constexpr (KG > 1) {
 #pragma unroll
-  for (int i = 0; i < kFM; ++i)
+    for (int i = 0; i < kFM; ++i)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = wm * S::kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+      for (int j = 0; j < kFN; ++j)
 #pragma unroll
-      for (int j = 0; j < kFN; ++j) atomicAdd(&red[r * S::kRedLd + wn * S::kWaveN + 32 * j + frow], acc[i][j][v]);
-    }
-  __syncthreads();
+        for (int h = 0; h < 4; ++h) {
+          const int q = (i * kFN + j) * 4 + h;
+          if (q / kQo != grp)
+            *slot(q / kQo, grp, q % kQo) =
+                v4i{acc[i][j][4 * h], acc[i][j][4 * h + 1], acc[i][j][4 * h + 2], acc[i][j][4 * h + 3]};
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int q = (i * kFN + j) * 4 + h;
+          if (q / kQo != grp) continue;
+          for (int w = 0; w < KG; ++w) {
+            if (w == grp) continue;
+            const v4i d = *slot(grp, w, q % kQo);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[i][j][4 * h + u] += d[u];
+          }
+        }
+  }
 
-  // ---- epilogue: 8 consecutive columns of one row per thread and step
-  constexpr int kC8 = BN / 8;
-  for (int it = tid; it < BM * kC8; it += S::kThreads) {
-    const int r = it / kC8, c = (it % kC8) * 8;
-    if (r >= mr || c >= nr) continue;
-    const int64_t m = m0 + r, n = n0 + c;
-    const v4i x0 = *reinterpret_cast<const v4i*>(red + r * S::kRedLd + c);
-    const v4i x1 = *reinterpret_cast<const v4i*>(red + r * S::kRedLd + c + 4);
-    const int32_t a[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-    const int cnt = nr - c < 8 ? static_cast<int>(nr - c) : 8;
-    if constexpr (EPI == kEpiBf16) {
-      const float sa = g.sa[m];
-      uint16_t o[8];
+  // ---- epilogue of the owned chunks
+  if constexpr (kBf16) {
+    if (g.staged_out) {
+      // bf16 tile staged row-major behind the exchange slots, then written
+      // with 16-byte row stores.  Lanes 2k / 2k+1 swap one value so that each
+      // writes two adjacent columns of one row as a 32-bit word; chunk c of
+      // row r sits at c ^ sf(r), which spreads the rows R, R+1, R+4, R+5 of
+      // one write instruction over distinct banks.
+      unsigned char* stg = lds + S::kXchg;
+      constexpr int kRowB = BN * 2, kOC = S::kOC;
+      auto sf = [](int r) -> int {
+        if constexpr (kOC == 16) return 4 * ((r & 1) | (((r >> 2) & 1) << 1));
+        else if constexpr (kOC == 8) return 4 * ((r >> 2) & 1);
+        else return 0;
+      };
+      const bool odd = (lane & 1) != 0;
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t nn = j < cnt ? n + j : n;
-        o[j] = epi_bf16(a[j], sa, g.sw[nn], g.bias, nn, 1.0f, false);
-      }
-      uint16_t* dst = static_cast<uint16_t*>(g.out) + m * g.ldo + n;
-      if (g.staged_out && cnt == 8) {  // N % 8 == 0 and 16-byte aligned rows: n is a multiple of 8
-        v4i d;
+      for (int i = 0; i < kFM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d[j] = static_cast<int>(o[2 * j] | (static_cast<uint32_t>(o[2 * j + 1]) << 16));
-        store_out16(dst, d);
-      } else {
-        for (int j = 0; j < cnt; ++j) dst[j] = o[j];
+        for (int j = 0; j < kFN; ++j)
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const int q = (i * kFN + j) * 4 + h;
+            if (q / kQo != grp) continue;
+            const int r0 = wm * S::kWaveM + 32 * i + 8 * h + 4 * fgrp, c = wn * S::kWaveN + 32 * j + frow;
+            const float swv = t_sw[c], bv = t_bias[c];
+            float tv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              tv[u] = epi_scale(acc[i][j][4 * h + u], t_sa[r0 + u], swv);
+              if (g.bias) tv[u] = tv[u] + bv;
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const float t0 = tv[2 * p], t1 = tv[2 * p + 1];
+              const float send = odd ? t0 : t1;
+              const float got = __builtin_bit_cast(
+                  float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+              const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
+              const int rr = r0 + 2 * p + (odd ? 1 : 0), cc = odd ? c - 1 : c;
+              *reinterpret_cast<bf16x2*>(stg + rr * kRowB + (((cc >> 3) ^ sf(rr)) << 4) + (cc & 7) * 2) = pr;
+            }
+          }
+      __syncthreads();
+      // N % 8 == 0 (staged_out), so every column range is whole 8-column chunks
+      for (int it = tid; it < BM * kOC; it += S::kThreads) {
+        const int r = it / kOC, ch = it % kOC;
+        if (r < mr && ch * 8 < nr) {
+          const v4i d = *reinterpret_cast<const v4i*>(stg + r * kRowB + ((ch ^ sf(r)) << 4));
+          store_out16(static_cast<uint16_t*>(g.out) + (m0 + r) * g.ldo + n0 + ch * 8, d);
+        }
       }
     } else {
-      int32_t* dst = static_cast<int32_t*>(g.out) + m * g.ldo + n;
-      for (int j = 0; j < cnt; ++j) dst[j] = a[j];
+#pragma unroll
+      for (int i = 0; i < kFM; ++i)
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const int q = (i * kFN + j) * 4 + h;
+            if (q / kQo != grp) continue;
+            const int r0 = wm * S::kWaveM + 32 * i + 8 * h + 4 * fgrp, c = wn * S::kWaveN + 32 * j + frow;
+            if (c >= nr) continue;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              if (r0 + u >= mr) continue;
+              float tv = epi_scale(acc[i][j][4 * h + u], t_sa[r0 + u], t_sw[c]);
+              if (g.bias) tv = tv + t_bias[c];
+              static_cast<uint16_t*>(g.out)[(m0 + r0 + u) * g.ldo + n0 + c] = f32_to_bf16(tv);
+            }
+          }
     }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int q = (i * kFN + j) * 4 + h;
+          if (q / kQo != grp) continue;
+          const int r0 = wm * S::kWaveM + 32 * i + 8 * h + 4 * fgrp, c = wn * S::kWaveN + 32 * j + frow;
+          if (c >= nr) continue;
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (r0 + u < mr) static_cast<int32_t*>(g.out)[(m0 + r0 + u) * g.ldo + n0 + c] = acc[i][j][4 * h + u];
+        }
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }

@@ -77,7 +77,7 @@ def test_workspace_bound_and_tuning_counts(lib):
     mx = lib.mw8_gemm_workspace_max_bytes()
     assert mx == 256 * 256 * 256 * 4
     counts = [lib.mw8_tuning_count(k) for k in range(4)]
-    assert counts == [8, 16, 2, 3] and lib.mw8_tuning_count(9) == 0
+    assert counts == [8, 11, 2, 3] and lib.mw8_tuning_count(9) == 0
     worst = 0
     try:
         for tile in range(-1, counts[1]):
