@@ -15,8 +15,8 @@ copies, so no launch finds its weights in the 256 MB MALL.
 
 Printed (one JSON line): whole-step throughput in TOPS (value, wall clock
 over the K steps), per-shape time / TOPS / GB/s / roofline fraction from
-HIP events (the fastest of the timed pass and two passes enqueued back to
-back after it, so no graph waits for its host submission), the dominant
+HIP events (the median of three passes enqueued back to back after the
+timed pass, so no graph waits for its host submission), the dominant
 kernel's roofline, the
 CPU baseline (the CPU oracle, timed on the host on a bounded sample, plus
 the reference's bf16 ``F.linear`` CPU op on the same sample), and secondary
@@ -120,6 +120,108 @@ def device_ceilings(lib, dev):
         del buf
     torch.cuda.synchronize()
     return res
+
+
+def data_path_ceilings(lib, dev):
+    """The operand path of the GEMM rings (16-byte buffer_load ... lds) in
+    three regimes, aggregate TB/s over 256 blocks of 4 waves: an L2-resident
+    region per XCD read 64 times; a 64 MB region per XCD streamed once by its
+    32 blocks in lockstep (each line fetched from HBM once and requested by
+    32 blocks together -- the pattern of a tile kernel's shared operand
+    panels); and a private 4 MB region per block (a plain HBM stream)."""
+    import torch
+
+    from minisgl_amd.kernel.lib import check
+
+    n = int(lib.mw8_calib_sink_len())
+    sink = torch.empty(n, dtype=torch.int32, device=dev)
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    st = torch.cuda.Stream()
+    res = {}
+    cases = (("l2_resident_tbps", 1 << 20, 64, 1), ("lockstep_shared_hbm_tbps", 64 << 20, 1, 1),
+             ("private_hbm_tbps", 4 << 20, 1, 0))
+    with torch.cuda.stream(st):
+        for key, region, passes, shared in cases:
+            launch = lambda: check(lib.mw8_calib_stream_lds(buf.data_ptr(), region, passes, shared,  # noqa: E731
+                                                            sink.data_ptr(), n, st.cuda_stream))
+            launch()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(5):
+                launch()
+            e1.record(st)
+            e1.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / 5
+            res[key] = round(region * passes * 256 / t / 1e12, 2)
+    del buf
+    torch.cuda.synchronize()
+    return res
+
+
+def decode_floors(lib, dev):
+    """Under the bench's own timing (a HIP graph of launches replayed between
+    events): the per-node cost of a trivial kernel, and at each Qwen3-14B
+    decode weight size the library's plain streaming read next to the
+    decode GEMM at M = 1 over the same number of bytes (distinct buffers per
+    launch, past the MALL)."""
+    import torch
+
+    from minisgl_amd.benchmark import perf_hip
+    from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES
+    from minisgl_amd.kernel import gemm_w8a8, quant_per_token
+    from minisgl_amd.kernel.lib import check
+
+    n = int(lib.mw8_calib_sink_len())
+    sink = torch.empty(n, dtype=torch.int32, device=dev)
+    one = torch.zeros(1, device=dev)
+    res = {"graph_node_us": round(perf_hip(lambda: one.add_(1.0), graph_calls=20) * 1e3, 2), "shapes": []}
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for name, K, N in QWEN3_14B_SHAPES:
+        size = N * K
+        ncopy = (1 << 30) // size
+        slot = [0]
+
+        def rd():
+            off = (slot[0] % ncopy) * size
+            slot[0] += 1
+            check(lib.mw8_calib_read(buf.data_ptr() + off, size, sink.data_ptr(), n,
+                                     torch.cuda.current_stream().cuda_stream))
+
+        t_read = perf_hip(rd, graph_calls=ncopy, repetitions=3) * 1e3
+        x = torch.randn(1, K, generator=gen, device=dev).to(torch.bfloat16)
+        q, s = quant_per_token(x)
+        sw = torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3
+        y = torch.empty(1, N, dtype=torch.bfloat16, device=dev)
+        w = buf[: ncopy * size].view(ncopy, N, K).view(torch.int8)
+        i = [0]
+
+        def gm():
+            gemm_w8a8(q, s, w[i[0] % ncopy], sw, out=y)
+            i[0] += 1
+
+        t_gemm = perf_hip(gm, graph_calls=ncopy, repetitions=3) * 1e3
+        res["shapes"].append({"shape": name, "mb": round(size / 1e6, 1), "plain_read_us": round(t_read, 2),
+                              "gemm_m1_us": round(t_gemm, 2)})
+    del buf
+    torch.cuda.synchronize()
+    return res
+
+
+def ceilings_mode(args) -> int:
+    import torch
+
+    from minisgl_amd.kernel import load
+
+    lib = load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    out = {"mode": "ceilings", "device": device_peaks(lib)}
+    out["device"]["measured"] = device_ceilings(lib, dev)
+    out["data_path"] = data_path_ceilings(lib, dev)
+    out["decode_floors"] = decode_floors(lib, dev)
+    print(json.dumps(out))
+    return 0
 
 
 def roofline_frac(ops: float, nbytes: float, t_s: float, peak_tops: float) -> float:
@@ -263,10 +365,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
-    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "moe", "vendor"], default="bench",
+    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "moe", "vendor", "ceilings"], default="bench",
                     help="bench: the contract line; gemm / copy / moe: one workload for rocprofv3 passes "
                          "(moe: the config-3 MoE layer at --tokens); vendor: this library against "
-                         "hipBLASLt int8 (torch._int_mm) at the config-1 shapes with M >= 512")
+                         "hipBLASLt int8 (torch._int_mm) at the config-1 shapes with M >= 512; ceilings: "
+                         "the device's measured data-path ceilings and the decode-size floors")
     ap.add_argument("--tokens", type=int, default=4096, help="--mode moe: tokens per layer call")
     ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
     ap.add_argument("--reps", type=int, default=3)
@@ -285,6 +388,8 @@ def main() -> int:
 
     if args.mode == "vendor":
         return vendor_mode(args)
+    if args.mode == "ceilings":
+        return ceilings_mode(args)
     if args.mode != "bench":
         return profile_mode(args)
 
@@ -355,11 +460,11 @@ def main() -> int:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         # Per-shape times: the first graphs after the synchronize wait for
-        # the host to submit them, which the events count.  Two more passes,
-        # enqueued back to back outside the timed region, run with the host
-        # ahead of the GPU; each shape reports its fastest of the three.
+        # the host to submit them, which the events count.  Three more
+        # passes, enqueued back to back outside the timed region, run with
+        # the host ahead of the GPU; each shape reports their median.
         extra = []
-        for _ in range(2):
+        for _ in range(3):
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                   for _ in plan]
             for g, (e0, e1) in zip(graphs, ev):
@@ -373,7 +478,7 @@ def main() -> int:
 
     shapes = []
     for i, (M, name, K, N) in enumerate(plan):
-        t = min(ev[i][0].elapsed_time(ev[i][1]) for ev in [events] + extra) * 1e-3 / args.steps
+        t = sorted(ev[i][0].elapsed_time(ev[i][1]) for ev in extra)[1] * 1e-3 / args.steps
         ops = 2.0 * M * N * K
         nb = gemm_bytes(M, N, K)
         ai = ops / nb
@@ -453,8 +558,8 @@ def main() -> int:
                          "M in {1,8,64,512,4096,8192}; one step = 24 GEMM launches"),
             "weight_copy_mb_per_shape": args.copy_mb,
             "timing": ("value: wall clock over the K steps; per shape: HIP graph of `steps` "
-                       "launches replayed between HIP events, fastest of the timed pass and "
-                       "two back-to-back passes after it"),
+                       "launches replayed between HIP events, median of three back-to-back "
+                       "passes after the timed pass"),
             "ops_per_step": ops_step,
         },
         "device": peaks,

@@ -314,12 +314,22 @@ int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, voi
  *   1 random ones (the power-limited rate int8 GEMMs on real data see).
  * mw8_calib_read: grid-stride streaming read of `bytes` (multiple of 16,
  *   16-byte aligned) -- the practical HBM read rate at that size.
+ * mw8_calib_stream_lds: 256 blocks x 4 waves moving region_bytes (a
+ *   multiple of 32 KiB, at most 1 GiB) per block, `passes` times, from
+ *   global memory into LDS with 16-byte buffer_load ... lds, 8-16 KB in
+ *   flight per wave.  shared = 1: block b reads region b % 8, so the 32
+ *   blocks of an XCD share one region (L2-resident for a small region read
+ *   several times; for a large one a lockstep stream in which each line is
+ *   fetched once and requested 32 times together); shared = 0: block b
+ *   reads region b.  buf holds region_bytes x (shared ? 8 : 256) bytes.
  */
 int64_t mw8_calib_sink_len(void);
 int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int64_t sink_len,
                       mw8_stream_t stream);
 int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len,
                    mw8_stream_t stream);
+int mw8_calib_stream_lds(const void* buf, int64_t region_bytes, int32_t passes, int32_t shared,
+                         int32_t* sink, int64_t sink_len, mw8_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,7 @@ int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, floa
 int64_t calib_sink_len();
 int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
 int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
+int calib_stream_lds(const void*, int64_t, int, int, int32_t*, int64_t, hipStream_t);
 
 }  // namespace mw8
 
@@ -212,6 +213,11 @@ int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int
 
 int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, mw8_stream_t st) {
   MW8_ENTRY(mw8::calib_read(buf, bytes, sink, sink_len, S(st)));
+}
+
+int mw8_calib_stream_lds(const void* buf, int64_t region_bytes, int32_t passes, int32_t shared, int32_t* sink,
+                         int64_t sink_len, mw8_stream_t st) {
+  MW8_ENTRY(mw8::calib_stream_lds(buf, region_bytes, passes, shared, sink, sink_len, S(st)));
 }
 
 }  // extern "C"

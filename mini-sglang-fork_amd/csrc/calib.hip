@@ -11,7 +11,14 @@
 // eight loads in flight, non-temporal) -- the practical HBM read ceiling
 // for a given buffer size.
 //
-// Both write one int per thread to `sink` so that nothing is optimised
+// calib_stream_lds_kernel: the GEMM rings' operand path (16-byte
+// buffer_load ... lds) streaming a region per block, shared by the 32
+// blocks of an XCD or private to each block -- the L2-resident rate, the
+// rate of lockstep streaming where every line is one miss and 31 merged
+// requests (the pattern of a tile kernel's shared operand panels), and the
+// plain HBM rate through this path.
+//
+// All write one int per thread to `sink` so that nothing is optimised
 // away; the caller times the launches with events on the same stream.
 #include "mw8_common.h"
 
@@ -79,6 +86,41 @@ __global__ __launch_bounds__(kReadThreads) void calib_read_kernel(const v4i* __r
   sink[tid] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+// Streams a region from global memory into LDS with 16-byte buffer_load ...
+// lds (the operand path of the GEMM rings): each of a block's 4 waves keeps
+// 8-16 instructions (1 KB each) in flight through a 64 KB LDS ring.  Block
+// b reads region b % 8 (shared) or region b (not shared), `passes` times.
+constexpr int kStreamBlocks = 256;
+__global__ __launch_bounds__(256) void calib_stream_lds_kernel(const char* buf, int64_t region, int passes,
+                                                               int shared, int32_t* sink) {
+  __shared__ __align__(16) unsigned char ring[65536];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t r = shared ? blockIdx.x % 8 : blockIdx.x;
+  const uint64_t base = reinterpret_cast<uint64_t>(buf + r * region);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(base)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(base >> 32)));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, 0x7fffffff, 0x00020000);
+  const int64_t per_wave = region / 4096;  // 1 KB instructions per wave and pass (a multiple of 8)
+  int slot = 0;
+  for (int p = 0; p < passes; ++p) {
+    for (int64_t i = 0; i < per_wave; i += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int off = static_cast<int>(((i + u) * 4 + wave) * 1024);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(ring + ((slot + u) & 15) * 4096 + wave * 1024), 16,
+            static_cast<uint32_t>(lane * 16), off, 0, 0);
+      }
+      slot += 8;
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  sink[blockIdx.x * 256 + threadIdx.x] = ring[threadIdx.x * 16];
+}
+
 }  // namespace
 
 int64_t calib_sink_len() {
@@ -108,6 +150,19 @@ int calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, 
   hipLaunchKernelGGL(calib_read_kernel, dim3(kReadBlocks), dim3(kReadThreads), 0, st,
                      static_cast<const v4i*>(buf), bytes / 16, sink);
   return check_launch("calib_read");
+}
+
+int calib_stream_lds(const void* buf, int64_t region_bytes, int passes, int shared, int32_t* sink,
+                     int64_t sink_len, hipStream_t st) {
+  MW8_REQUIRE(buf != nullptr && sink != nullptr, kErrArg, "calib_stream_lds: null pointer");
+  MW8_REQUIRE(region_bytes >= 32768 && region_bytes % 32768 == 0 && region_bytes <= (int64_t{1} << 30), kErrShape,
+              "calib_stream_lds: region_bytes must be a multiple of 32 KiB, at most 1 GiB");
+  MW8_REQUIRE(passes >= 1 && (shared == 0 || shared == 1), kErrArg, "calib_stream_lds: passes >= 1, shared 0 or 1");
+  MW8_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15u) == 0, kErrAlign, "calib_stream_lds: 16-byte alignment");
+  MW8_REQUIRE(sink_len >= static_cast<int64_t>(kStreamBlocks) * 256, kErrShape, "calib_stream_lds: sink too short");
+  hipLaunchKernelGGL(calib_stream_lds_kernel, dim3(kStreamBlocks), dim3(256), 0, st, static_cast<const char*>(buf),
+                     region_bytes, passes, shared, sink);
+  return check_launch("calib_stream_lds");
 }
 
 }  // namespace mw8

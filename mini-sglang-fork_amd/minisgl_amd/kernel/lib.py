@@ -69,6 +69,7 @@ SIGNATURES = {
     "mw8_calib_sink_len": (_I64, []),
     "mw8_calib_mfma_i8": (ctypes.c_int, [_I32, _I32, _P, _I64, _P]),
     "mw8_calib_read": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
+    "mw8_calib_stream_lds": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _I64, _P]),
 }
 
 ERROR_NAMES = {
