@@ -129,11 +129,12 @@ void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg);
 int32_t mw8_tuning_count(int32_t kind);
 
 /*
- * Name of the kernel family mw8_gemm_w8a8_* runs for (M, N, K) under the
- * current tuning ("decode3_gemm_kernel", "decode_gemm_kernel",
- * "ksplit_gemm_kernel", "tile3_gemm_kernel", "tile_gemm_kernel"; "" for
- * invalid sizes), matching the names in a kernel trace.  Profiling aid; no
- * reference counterpart.
+ * Name of the kernel mw8_gemm_w8a8_* runs for (M, N, K) under the current
+ * tuning: "decode3_gemm_kernel" or "decode_gemm_kernel" for the decode
+ * cores, else the tile kernel with its leading template arguments as a
+ * kernel trace prints them (e.g. "tile3_gemm_kernel<256, 256, 128, 4, 2,
+ * 2>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"); "" for invalid
+ * sizes.  Profiling aid; no reference counterpart.
  */
 const char* mw8_gemm_kernel_name(int64_t M, int64_t N, int64_t K);
 

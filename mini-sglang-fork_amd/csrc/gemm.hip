@@ -171,14 +171,24 @@ struct TileCfg {
   bool dma;
   int bk, per_cu;
   bool split;
+  const char* name;  // kernel name with its leading template arguments, as a trace shows it
 };
 constexpr TileCfg kTileCfgs[] = {
-    {128, 128, false, 128, 2, false},  // 0: register-staged, 4 waves
-    {128, 128, true, 64, 2, false},    // 1: ring, 4 waves (2x2), 4 stages, two per CU
-    {256, 256, true, 128, 1, true},    // 2: ring, 8 waves (4x2), 2 stages
-    {256, 128, true, 128, 1, false},   // 3: ring, 8 waves (4x2), 3 stages: grids of 129-256 tiles
-    {128, 128, true, 128, 2, true},    // 4: ring, 4 waves (2x2), 2 stages, two per CU
-    {64, 128, true, 128, 1, true},     // 5: ring, 4 waves (1x4), 4 stages
+    // 0: register-staged, 4 waves
+    {128, 128, false, 128, 2, false, "tile_gemm_kernel<128, 128, 128, 2, 2>"},
+    // 1: ring, 4 waves (2x2), 4 stages, two per CU
+    {128, 128, true, 64, 2, false, "tile3_gemm_kernel<128, 128, 64, 2, 2, 4>"},
+    // 2: ring, 8 waves (4x2), 2 stages
+    {256, 256, true, 128, 1, true, "tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"},
+    // 3: ring, 8 waves (4x2), 3 stages: grids of 129-256 tiles
+    {256, 128, true, 128, 1, false, "tile3_gemm_kernel<256, 128, 128, 4, 2, 3>"},
+    // 4: ring, 4 waves (2x2), 2 stages, two per CU
+    {128, 128, true, 128, 2, true, "tile3_gemm_kernel<128, 128, 128, 2, 2, 2>"},
+    // 5: ring, 4 waves (1x4), 4 stages
+    {64, 128, true, 128, 1, true, "tile3_gemm_kernel<64, 128, 128, 1, 4, 4>"},
+    // 6: ring, 8 waves (4x2), 2 stages, the bf16 tile staged in two row
+    // passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs
+    {256, 320, true, 128, 1, false, "tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"},
 };
 constexpr int kNumRingCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
@@ -187,13 +197,14 @@ constexpr int kNumRingCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 // 32-byte k-steps per group and stage, NSTAGE stages.
 struct KsplitCfg {
   int bm, bn, kg, wm, wn, ks, nstage;
+  const char* name;
 };
 constexpr KsplitCfg kKsplitCfgs[] = {
-    {64, 32, 8, 1, 1, 1, 4},    // 0: 256-byte stages, waves of 64 x 32
-    {64, 32, 8, 1, 1, 2, 3},    // 1: 512-byte stages, waves of 64 x 32
-    {64, 64, 8, 1, 1, 1, 4},    // 2: 256-byte stages, waves of 64 x 64
-    {128, 64, 4, 2, 1, 2, 3},   // 3: 256-byte stages, waves of 64 x 64, 2 k-steps per stage
-    {128, 128, 2, 2, 2, 2, 4},  // 4: 128-byte stages, waves of 64 x 64, 2 k-steps
+    {64, 32, 8, 1, 1, 1, 4, "ksplit_gemm_kernel<64, 32, 8, 1, 1, 1, 4>"},      // 0: 256-byte stages, waves of 64 x 32
+    {64, 32, 8, 1, 1, 2, 3, "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>"},      // 1: 512-byte stages, waves of 64 x 32
+    {64, 64, 8, 1, 1, 1, 4, "ksplit_gemm_kernel<64, 64, 8, 1, 1, 1, 4>"},      // 2: 256-byte stages, waves of 64 x 64
+    {128, 64, 4, 2, 1, 2, 3, "ksplit_gemm_kernel<128, 64, 4, 2, 1, 2, 3>"},    // 3: 256-byte stages, 2 k-steps per stage
+    {128, 128, 2, 2, 2, 2, 4, "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"},  // 4: 128-byte stages, 2 k-steps
 };
 constexpr int kNumKsplitCfgs = sizeof(kKsplitCfgs) / sizeof(kKsplitCfgs[0]);
 constexpr int kNumTileCfgs = kNumRingCfgs + kNumKsplitCfgs;
@@ -263,6 +274,7 @@ constexpr ModelCfg kModelCfgs[] = {
     {1, 3.0, 4.6, 5.9},     // 128x128 BK 64, 4 stages, two per CU
     {5, 3.0, 3.36, 3.36},   // 64x128, 4 stages
     {3, 6.0, 8.0, 8.0},     // 256x128, 8 waves, 3 stages (no K split): grids of 129-256 tiles
+    {6, 5.0, 9.0, 9.0},     // 256x320, 8 waves (near-ties go to 256x256)
 };
 
 double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
@@ -395,7 +407,8 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     case 2: rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 3: rc = launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 4: rc = launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
-    default: rc = launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 5: rc = launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    default: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
   if (rc != kOk || !split) return rc;
   switch (c.bm * 1000 + c.bn) {
@@ -635,8 +648,8 @@ const char* gemm_kernel_name(int64_t M, int64_t N, int64_t K) {
     return kDecodeCfgs[cfg].core == 0 ? "decode_gemm_kernel" : "decode3_gemm_kernel";
   }
   const int cfg = select_tile_cfg(M, N, K);
-  if (cfg >= kNumRingCfgs) return "ksplit_gemm_kernel";
-  return kTileCfgs[cfg].dma ? "tile3_gemm_kernel" : "tile_gemm_kernel";
+  if (cfg >= kNumRingCfgs) return kKsplitCfgs[cfg - kNumRingCfgs].name;
+  return kTileCfgs[cfg].name;
 }
 
 int tuning_count(int kind) {

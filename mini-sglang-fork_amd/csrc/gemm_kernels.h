@@ -487,7 +487,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
-  static_assert(kAct < 0 || (Rows::kGrouped && epi_bf16_out(EPI) && BM * BN * 2 <= NSTAGE * kStage && BN >= 128),
+  static_assert(kAct < 0 || (Rows::kGrouped && epi_bf16_out(EPI)),
                 "fused activation: grouped bf16 with the staged epilogue (the host sets staged_out)");
   constexpr int kHalfN = BN / 2;
   const int64_t half = g.N / 2;  // kAct: rows of each of the gate and up halves
@@ -676,100 +676,128 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // ---- staged bf16 epilogue: the tile is assembled in the (now idle) LDS
   // ring and written with 16-byte row stores.  Lanes 2k / 2k+1 swap one
   // value so that each writes two adjacent columns of one row as a 32-bit
-  // word; the staging layout XORs the 16-byte chunk index of row r with
-  // sf(r), which keeps both the word writes (rows R, R+1, R+4, R+5 per
-  // instruction) and the 16-byte row reads on distinct LDS banks.
-  if constexpr (epi_bf16_out(EPI) && BM * BN * 2 <= NSTAGE * kStage && BN >= 128) {
+  // word; the staging layout moves the 16-byte chunk c of row r to
+  // spos(r, c) (an XOR with sf(r) when a row holds a multiple of 16 chunks,
+  // else a rotation by it), which keeps both the word writes (rows R, R+1,
+  // R+4, R+5 per instruction) and the 16-byte row reads on distinct LDS
+  // banks.  A tile whose bf16 image exceeds the ring is staged in row
+  // passes of whole wave rows (kStagePasses).
+  constexpr int kRing = NSTAGE * kStage;
+  constexpr int kStagePasses = (BM * BN * 2 + kRing - 1) / kRing;
+  constexpr int kPassRows = BM / kStagePasses;
+  constexpr bool kStaged = epi_bf16_out(EPI) && BN >= 128 && kStagePasses <= 2 &&
+                           kPassRows * kStagePasses == BM && kPassRows % kWaveM == 0;
+  static_assert(kAct < 0 || (kStaged && kStagePasses == 1), "fused activation: one staging pass");
+  if constexpr (kStaged) {
     if (g.staged_out) {
       constexpr int kRowBytes = BN * 2;
+      constexpr int kChunksRow = BN / 8;
       auto sf = [](int r) { return 4 * ((r & 1) | (((r >> 2) & 1) << 1)); };
-      __syncthreads();  // every wave is past its last LDS fragment read
+      auto spos = [&](int r, int c) {
+        if constexpr (kChunksRow % 16 == 0) {
+          return c ^ sf(r);
+        } else {
+          const int q = c + sf(r);
+          return q >= kChunksRow ? q - kChunksRow : q;
+        }
+      };
       const bool odd = (lane & 1) != 0;
+      constexpr int kThreads = 64 * kWaves;
 #pragma unroll
-      for (int i = 0; i < kFM; ++i) {
+      for (int pass = 0; pass < kStagePasses; ++pass) {
+        const int prow0 = pass * kPassRows;
+        // every wave is past its last LDS fragment read (pass 0) or its
+        // reads of the previous pass's rows
+        __syncthreads();
+        if (wm * kWaveM >= prow0 && wm * kWaveM < prow0 + kPassRows) {  // wave-uniform
 #pragma unroll
-        for (int vp = 0; vp < 8; ++vp) {
-          const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
-          const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
-          float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
-          if constexpr (Rows::kGrouped) {
-            sa0 = meta_sa[r0];
-            sa1 = meta_sa[r0 + 1];
-            rt0 = meta_rt[r0];
-            rt1 = meta_rt[r0 + 1];
-          } else {
-            sa0 = meta_sa[r0];
-            sa1 = meta_sa[r0 + 1];
-          }
+          for (int i = 0; i < kFM; ++i) {
 #pragma unroll
-          for (int j = 0; j < kFN; ++j) {
-            const int c = wn * kWaveN + 32 * j + frow;
-            const float swv = meta_sw[c];
-            float t0 = epi_scale(acc[i][j][v0], sa0, swv);
-            float t1 = epi_scale(acc[i][j][v0 + 1], sa1, swv);
-            if constexpr (!Rows::kGrouped) {
-              if (g.bias) {
-                t0 = t0 + meta_bias[c];
-                t1 = t1 + meta_bias[c];
+            for (int vp = 0; vp < 8; ++vp) {
+              const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
+              const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
+              float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
+              if constexpr (Rows::kGrouped) {
+                sa0 = meta_sa[r0];
+                sa1 = meta_sa[r0 + 1];
+                rt0 = meta_rt[r0];
+                rt1 = meta_rt[r0 + 1];
+              } else {
+                sa0 = meta_sa[r0];
+                sa1 = meta_sa[r0 + 1];
+              }
+#pragma unroll
+              for (int j = 0; j < kFN; ++j) {
+                const int c = wn * kWaveN + 32 * j + frow;
+                const float swv = meta_sw[c];
+                float t0 = epi_scale(acc[i][j][v0], sa0, swv);
+                float t1 = epi_scale(acc[i][j][v0 + 1], sa1, swv);
+                if constexpr (!Rows::kGrouped) {
+                  if (g.bias) {
+                    t0 = t0 + meta_bias[c];
+                    t1 = t1 + meta_bias[c];
+                  }
+                }
+                if (Rows::kGrouped && g.topk_w) {
+                  t0 = t0 * rt0;
+                  t1 = t1 * rt1;
+                }
+                // even lane: row r0, columns (c, c+1); odd lane: row r0+1, columns (c-1, c)
+                const float send = odd ? t0 : t1;
+                const float got = __builtin_bit_cast(
+                    float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+                const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
+                const int rr = (odd ? r0 + 1 : r0) - prow0, cc = odd ? c - 1 : c;
+                *reinterpret_cast<bf16x2*>(lds + rr * kRowBytes + (spos(rr, cc >> 3) << 4) + (cc & 7) * 2) = pr;
               }
             }
-            if (Rows::kGrouped && g.topk_w) {
-              t0 = t0 * rt0;
-              t1 = t1 * rt1;
-            }
-            // even lane: row r0, columns (c, c+1); odd lane: row r0+1, columns (c-1, c)
-            const float send = odd ? t0 : t1;
-            const float got = __builtin_bit_cast(
-                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-            const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
-            const int rr = odd ? r0 + 1 : r0, cc = odd ? c - 1 : c;
-            *reinterpret_cast<bf16x2*>(lds + rr * kRowBytes + (((cc >> 3) ^ sf(rr)) << 4) + (cc & 7) * 2) = pr;
           }
         }
-      }
-      __syncthreads();
-      constexpr int kThreads = 64 * kWaves;
-      if constexpr (kAct >= 0) {  // act chunk ch of row r: gate chunk ch, up chunk ch + BN/16
-        constexpr int kActChunks = BN / 16;
+        __syncthreads();
+        if constexpr (kAct >= 0) {  // act chunk ch of row r: gate chunk ch, up chunk ch + BN/16
+          constexpr int kActChunks = BN / 16;
 #pragma unroll
-        for (int q0 = 0; q0 < BM * kActChunks; q0 += kThreads) {
-          const int q = q0 + tid, r = q / kActChunks, ch = q % kActChunks;
-          const int64_t orow = meta_p[r];
-          const int64_t n = n0 + ch * 8;
-          if (orow >= 0 && n < half) {
-            const v4i gv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
-            const v4i uv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (((ch + kActChunks) ^ sf(r)) << 4));
-            v4i o;
+          for (int q0 = 0; q0 < BM * kActChunks; q0 += kThreads) {
+            const int q = q0 + tid, r = q / kActChunks, ch = q % kActChunks;
+            const int64_t orow = meta_p[r];
+            const int64_t n = n0 + ch * 8;
+            if (orow >= 0 && n < half) {
+              const v4i gv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (spos(r, ch) << 4));
+              const v4i uv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (spos(r, ch + kActChunks) << 4));
+              v4i o;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const uint32_t gw = static_cast<uint32_t>(gv[w]), uw = static_cast<uint32_t>(uv[w]);
-              const float a0 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw & 0xFFFFu))) *
-                               bf16_to_f32(static_cast<uint16_t>(uw & 0xFFFFu));
-              const float a1 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw >> 16))) *
-                               bf16_to_f32(static_cast<uint16_t>(uw >> 16));
-              o[w] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(a0)) |
-                                      (static_cast<uint32_t>(f32_to_bf16(a1)) << 16));
+              for (int w = 0; w < 4; ++w) {
+                const uint32_t gw = static_cast<uint32_t>(gv[w]), uw = static_cast<uint32_t>(uv[w]);
+                const float a0 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw & 0xFFFFu))) *
+                                 bf16_to_f32(static_cast<uint16_t>(uw & 0xFFFFu));
+                const float a1 = act_fn<kAct>(bf16_to_f32(static_cast<uint16_t>(gw >> 16))) *
+                                 bf16_to_f32(static_cast<uint16_t>(uw >> 16));
+                o[w] = static_cast<int>(static_cast<uint32_t>(f32_to_bf16(a0)) |
+                                        (static_cast<uint32_t>(f32_to_bf16(a1)) << 16));
+              }
+              __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n));
             }
-            __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + orow * g.ldo + n));
           }
-        }
-        return;
-      }
-      constexpr int kChunksRow = BN / 8;
-#pragma unroll
-      for (int q0 = 0; q0 < BM * kChunksRow; q0 += kThreads) {
-        const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
-        int64_t orow;
-        if constexpr (Rows::kGrouped) {
-          orow = meta_p[r];
+          return;
         } else {
-          orow = m0 + r < g.M ? m0 + r : -1;
-        }
-        const int64_t n = n0 + ch * 8;
-        if (orow >= 0 && n < g.N) {
-          const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + ((ch ^ sf(r)) << 4));
-          store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d);
+#pragma unroll
+          for (int q0 = 0; q0 < kPassRows * kChunksRow; q0 += kThreads) {
+            const int q = q0 + tid, r = q / kChunksRow, ch = q % kChunksRow;
+            if (q < kPassRows * kChunksRow) {
+              int64_t orow;
+              if constexpr (Rows::kGrouped) {
+                orow = meta_p[prow0 + r];
+              } else {
+                orow = m0 + prow0 + r < g.M ? m0 + prow0 + r : -1;
+              }
+              const int64_t n = n0 + ch * 8;
+              if (orow >= 0 && n < g.N) {
+                const v4i d = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (spos(r, ch) << 4));
+                store_out16(static_cast<uint16_t*>(g.out) + orow * g.ldo + n, d);
+              }
+            }
+          }
         }
       }
       return;

@@ -51,10 +51,18 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_moe_align_max_padded(12, 5, 4) == 27
     assert lib.mw8_moe_align_max_padded(128, 129, 16) == 128 + 129 * 15
     assert lib.mw8_gemm_workspace_bytes(1, 5120, 5120) == 0
-    # tail split of 256x256 tilings: r = T mod 256 tail tiles, sp = min(256 // r, K / 128, 16)
-    # K ranges each, one int32 256x256 partial tile per (tile, range)
-    assert lib.mw8_gemm_workspace_bytes(1024, 34816, 5120) == 32 * 8 * 256 * 256 * 4
-    assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 64 * 4 * 256 * 256 * 4
+    # tail split of 256x256 tilings (forced): r = T mod 256 tail tiles, sp = min(256 // r,
+    # K / 128, 16) K ranges each, one int32 256x256 partial tile per (tile, range)
+    lib.mw8_set_tuning(-1, 2, -1)
+    try:
+        assert lib.mw8_gemm_workspace_bytes(1024, 34816, 5120) == 32 * 8 * 256 * 256 * 4
+        assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 64 * 4 * 256 * 256 * 4
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+    # automatic: N = 5120 at 4096 rows runs 256x320 tiles, 256 of them (no split)
+    assert lib.mw8_gemm_kernel_name(4096, 5120, 5120) == b"tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"
+    assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 0
+    assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) == b"tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"
     assert lib.mw8_gemm_workspace_bytes(8192, 34816, 5120) == 0  # 4352 tiles: whole waves
     assert lib.mw8_gemm_workspace_bytes(4096, 7168, 5120) == 0   # 192 tail tiles: no split
     assert lib.mw8_gemm_workspace_bytes(512, 5120, 5120 + 64) == 0  # K % 128 != 0
@@ -77,7 +85,7 @@ def test_workspace_bound_and_tuning_counts(lib):
     mx = lib.mw8_gemm_workspace_max_bytes()
     assert mx == 256 * 256 * 256 * 4
     counts = [lib.mw8_tuning_count(k) for k in range(4)]
-    assert counts == [8, 11, 2, 3] and lib.mw8_tuning_count(9) == 0
+    assert counts == [8, 12, 2, 3] and lib.mw8_tuning_count(9) == 0
     worst = 0
     try:
         for tile in range(-1, counts[1]):

@@ -36,11 +36,11 @@ def _both(lib, q, s, w, sw, M, N, K):
 
 def test_noalloc_gemm_equals_workspace_gemm():
     lib = load()
-    # (M, N, K): o_proj at M=4096 (320 tiles of 256x256, 64 split into 4 K
-    # ranges: 64 MiB of partial tiles, the whole scratch), then a smaller
-    # input that splits (gate_up at 64 tokens: 272 tiles of 64x128, 16 of
-    # them split 16 ways), then a decode shape (no split)
-    for M, N, K, seed in ((4096, 5120, 5120, 1), (64, 34816, 5120, 2), (8, 2048, 1024, 3)):
+    # (M, N, K): down at M=512 (40 tiles of 256x256, each split into 6 K
+    # ranges: 60 MiB of partial tiles, nearly the whole scratch), then a
+    # smaller input that splits (gate_up at 64 tokens: 272 tiles of 64x128,
+    # 16 of them split 16 ways), then a decode shape (no split)
+    for M, N, K, seed in ((512, 5120, 17408, 1), (64, 34816, 5120, 2), (8, 2048, 1024, 3)):
         announce(f"noalloc gemm M={M} N={N} K={K}")
         c = linear_case(M, K, N, seed=seed)
         q, s = quant_per_token(c["x"].to(DEV))
