@@ -231,8 +231,14 @@ int64_t ksplit_ranges(int64_t M, int64_t N, const KsplitCfg& c, int64_t& gm) {
 // K split of a ring tiling.  With T tiles and S = CUs * per_cu resident
 // slots: T >= S cuts the r = T mod S tiles of the last, partial wave into
 // sp = min(S / r, K / bk, 16) K ranges; T < S cuts every tile into
-// sp = min(S / T, K / bk, 16) ranges.  No split when sp < 2.  r * sp <= S,
-// so the workspace never exceeds S * bm * bn int32 values.
+// sp = min(S / T, K / bk, 16) ranges.  No split when sp < 2, nor for a tail
+// of more than a third of a wave (sp < 3): a partial last wave costs about
+// one tile time whatever its occupancy, while two K ranges add the partial
+// tiles' round trip and the reduction launch (256x256 tiles on MI355X,
+// with / without the split: gate_up M=4096 729 / 669 us, o_proj M=8192
+// 220 / 206, qkv M=8192 296 / 278; with sp >= 4 the split wins: o_proj
+// M=4096 124 / 126, gate_up M=1024 213 / 229).  r * sp <= S, so the
+// workspace never exceeds S * bm * bn int32 values.
 struct SplitPlan {
   int64_t full = 0, tail = 0;
   int sp = 1;
@@ -250,7 +256,7 @@ SplitPlan plan_split(int64_t M, int64_t N, int64_t K, const TileCfg& c) {
   const int64_t nkt = K / c.bk;
   if (sp > nkt) sp = nkt;
   if (sp > 16) sp = 16;
-  if (sp < 2) return p;
+  if (sp < 2 || (T >= slots && sp < 3)) return p;
   p.full = T - r;
   p.tail = r;
   p.sp = static_cast<int>(sp);
