@@ -248,3 +248,26 @@ def test_backend_requires_scales():
     with pytest.raises(ValueError, match="scale"):
         create_moe_backend("fused_w8a8").forward(torch.zeros(1, 16), torch.zeros(4, 16, 16), torch.zeros(4, 16, 8),
                                                  torch.zeros(1, 4), 2, True)
+
+
+def test_default_tiling_of_the_benchmark_shapes(lib):
+    """The tiling the library picks for each Qwen3-14B benchmark shape (the
+    time model plus the split-K rules, planned for 256 CUs without a GPU):
+    decode cores up to 8 rows, in-block split-K for qkv / o_proj at 64 and
+    512 rows, the 64x128 ring for the wide / deep shapes at 64 rows, and
+    the 256x256 or 256x320 rings (whichever fills whole waves) above."""
+    t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
+    sq, wide = t3.format(256, 256, 4, 2, 2), t3.format(256, 320, 4, 2, 2)
+    ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"
+    r64 = t3.format(64, 128, 1, 4, 4)
+    expect = {
+        (5120, 7168): [ks64, ks512, sq, wide],
+        (5120, 5120): [ks64, ks512, wide, wide],
+        (5120, 34816): [r64, wide, wide, sq],
+        (17408, 5120): [r64, sq, wide, wide],
+    }
+    for (K, N), names in expect.items():
+        for M in (1, 8):
+            assert lib.mw8_gemm_kernel_name(M, N, K) == b"decode3_gemm_kernel", (M, N, K)
+        for M, name in zip((64, 512, 4096, 8192), names):
+            assert lib.mw8_gemm_kernel_name(M, N, K).decode() == name, (M, N, K)
