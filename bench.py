@@ -365,13 +365,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
-    ap.add_argument("--mode", choices=["bench", "gemm", "copy", "moe", "vendor", "ceilings"], default="bench",
-                    help="bench: the contract line; gemm / copy / moe: one workload for rocprofv3 passes "
-                         "(moe: the config-3 MoE layer at --tokens); vendor: this library against "
+    ap.add_argument("--mode", choices=["bench", "gemm", "quant", "copy", "moe", "vendor", "ceilings"],
+                    default="bench",
+                    help="bench: the contract line; gemm / quant / copy / moe: one workload for rocprofv3 "
+                         "passes (quant: the per-token quantizer at --shape M,K; moe: the config-3 MoE "
+                         "layer at --tokens); vendor: this library against "
                          "hipBLASLt int8 (torch._int_mm) at the config-1 shapes with M >= 512; ceilings: "
                          "the device's measured data-path ceilings and the decode-size floors")
     ap.add_argument("--tokens", type=int, default=4096, help="--mode moe: tokens per layer call")
-    ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm")
+    ap.add_argument("--shape", default="8192,34816,5120", help="M,N,K for --mode gemm (M,K for --mode quant)")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copies", type=int, default=1,
                     help="--mode gemm: distinct weight copies the launches rotate through (the timed "
@@ -614,6 +616,21 @@ def profile_mode(args) -> int:
         torch.cuda.synchronize()
         reset_global_ctx()
         print(json.dumps({"mode": "moe", "tokens": args.tokens, "reps": args.reps, "tuning": args.tuning}))
+        return 0
+    if args.mode == "quant":
+        from minisgl_amd.kernel import quant_per_token
+
+        M, K = (int(v) for v in args.shape.split(",")[:2])
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        big = torch.rand(M, K, generator=gen, device=dev) < 1e-3  # 0.1% outliers x20, as config 2
+        x = torch.where(big, x * 20, x)
+        q = torch.empty(M, K, dtype=torch.int8, device=dev)
+        s = torch.empty(M, dtype=torch.float32, device=dev)
+        for _ in range(args.reps):
+            quant_per_token(x, out=q, scale=s)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "quant", "M": M, "K": K, "reps": args.reps,
+                          "algorithmic_bytes": 3 * M * K + 4 * M}))
         return 0
     if args.mode == "copy":
         nbytes = 1 << 30
