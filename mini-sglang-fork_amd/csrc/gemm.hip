@@ -204,7 +204,7 @@ constexpr KsplitCfg kKsplitCfgs[] = {
     {64, 32, 8, 1, 1, 2, 3, "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>"},      // 1: 512-byte stages, waves of 64 x 32
     {64, 64, 8, 1, 1, 1, 4, "ksplit_gemm_kernel<64, 64, 8, 1, 1, 1, 4>"},      // 2: 256-byte stages, waves of 64 x 64
     {128, 64, 4, 2, 1, 2, 3, "ksplit_gemm_kernel<128, 64, 4, 2, 1, 2, 3>"},    // 3: 256-byte stages, 2 k-steps per stage
-    {128, 128, 2, 2, 2, 2, 4, "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"},  // 4: 128-byte stages, 2 k-steps
+    {128, 128, 2, 2, 2, 2, 3, "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"},  // 4: 128-byte stages, 2 k-steps
 };
 constexpr int kNumKsplitCfgs = sizeof(kKsplitCfgs) / sizeof(kKsplitCfgs[0]);
 constexpr int kNumTileCfgs = kNumRingCfgs + kNumKsplitCfgs;
@@ -314,17 +314,33 @@ double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
 //        auto   16.5   16.8   23.6   27.0   38.7   42.9
 //   o    ks     11.8   13.2   16.7   21.8   32.3   62.4
 //        auto   15.9   16.5   19.3   26.1   37.4   40.5
-// (ks: 64 x 32 tiles with 512-byte stages up to 64 rows, 64 x 64 tiles to
-// 128, 128 x 64 to 256-384, 128 x 128 with two K groups above.)  With K >
-// 8192 (down, K = 17408) every block re-reads a long token panel and with
-// N > 16384 (gate_up) the ring already fills the CUs: the ring wins there.
+// With K > 8192 (down, K = 17408) every block re-reads a long token panel
+// and with N > 16384 (gate_up) the ring already fills the CUs: the ring
+// wins there.  Above 64 rows the tile is the smallest of 64 x 64, 128 x 64
+// and 128 x 128 whose fewest column ranges fit one wave of the CUs (a second
+// wave costs nearly a whole launch), and the ring when none does; same box,
+// chosen tile (runner-up in brackets):
+//   qkv M=192  128x64 20.4 (64x64 30.2)    qkv M=384  128x128 31.2 (128x64 38.9)
+//   o   M=192  64x64  17.6 (128x64 19.4)   qkv M=640  ring 256x128 40.9 (128x128 58.2)
+//   o   M=768  128x128 34.7 (ring 39.1)    qkv M=768  ring 256x128 44.3 (128x128 61.0)
+// Split-K stages: the 128 x 128 tile runs 3 stages of 32 KB (64 KB in
+// flight); 4 stages measured 1-4% slower at M = 384-768 (the per-CU operand
+// stream saturates near 48 GB/s, not on the bytes in flight).
+int64_t ksplit_min_waves(int64_t M, int64_t N, const KsplitCfg& c) {
+  const int64_t q = (c.bn - N % 16) / 16;
+  if (q < 1) return INT64_MAX;
+  const int64_t gn = N < 16 ? 1 : (N / 16 + q - 1) / q;
+  const int64_t cus = device_cus();
+  return ((M + c.bm - 1) / c.bm * gn + cus - 1) / cus;
+}
+
 int default_ksplit_cfg(int64_t M, int64_t N, int64_t K) {
   if (M > 768 || N > 16384 || K > 8192) return -1;
   if (M <= 64) return K % 512 == 0 ? 1 : (K % 256 == 0 ? 0 : -1);
   if (K % 256 != 0) return -1;
-  if (M <= 128) return 2;
-  if (M <= 384) return 3;
-  return 4;
+  for (const int c : {2, 3, 4})
+    if (ksplit_min_waves(M, N, kKsplitCfgs[c]) <= 1) return c;
+  return -1;
 }
 
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
@@ -378,7 +394,7 @@ int dispatch_ksplit(int i, const GemmArgs& g, hipStream_t st) {
     case 1: return launch_ksplit<64, 32, 8, 1, 1, 2, 3, EPI>(g, st);
     case 2: return launch_ksplit<64, 64, 8, 1, 1, 1, 4, EPI>(g, st);
     case 3: return launch_ksplit<128, 64, 4, 2, 1, 2, 3, EPI>(g, st);
-    default: return launch_ksplit<128, 128, 2, 2, 2, 2, 4, EPI>(g, st);
+    default: return launch_ksplit<128, 128, 2, 2, 2, 2, 3, EPI>(g, st);
   }
 }
 

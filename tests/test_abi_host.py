@@ -258,7 +258,7 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     the 256x256 or 256x320 rings (whichever fills whole waves) above."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
     sq, wide = t3.format(256, 256, 4, 2, 2), t3.format(256, 320, 4, 2, 2)
-    ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"
+    ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
     r64 = t3.format(64, 128, 1, 4, 4)
     expect = {
         (5120, 7168): [ks64, ks512, sq, wide],
@@ -271,3 +271,21 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
             assert lib.mw8_gemm_kernel_name(M, N, K) == b"decode3_gemm_kernel", (M, N, K)
         for M, name in zip((64, 512, 4096, 8192), names):
             assert lib.mw8_gemm_kernel_name(M, N, K).decode() == name, (M, N, K)
+
+
+def test_mid_m_tiling_fills_one_wave(lib):
+    """Between 65 and 768 rows qkv / o_proj take the smallest split-K tile
+    whose fewest column ranges fit one wave of 256 CUs, and the ring when
+    none does (qkv at 640 / 768 rows)."""
+    k64 = "ksplit_gemm_kernel<64, 64, 8, 1, 1, 1, 4>"
+    k128x64 = "ksplit_gemm_kernel<128, 64, 4, 2, 1, 2, 3>"
+    k128 = "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
+    ring = "tile3_gemm_kernel<256, 128, 128, 4, 2, 3>"
+    expect = {
+        7168: {96: k64, 128: k64, 192: k128x64, 256: k128x64, 320: k128, 384: k128, 512: k128,
+               640: ring, 768: ring},
+        5120: {96: k64, 128: k64, 192: k64, 256: k128x64, 384: k128x64, 512: k128, 768: k128},
+    }
+    for N, by_m in expect.items():
+        for M, name in by_m.items():
+            assert lib.mw8_gemm_kernel_name(M, N, 5120).decode() == name, (M, N)

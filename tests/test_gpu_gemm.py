@@ -86,6 +86,17 @@ def test_gemm_qwen3_14b_large_m_sampled(M, K, N):
     _run_case(M, K, N, seed=0, rows=rows)
 
 
+@pytest.mark.parametrize("M,N", [(192, 7168), (192, 5120), (384, 7168), (640, 7168), (768, 7168), (768, 5120)])
+def test_gemm_mid_m_default_tiling_sampled(M, N):
+    """qkv / o_proj between 192 and 768 rows under the automatic choice
+    (64x64, 128x64 or 128x128 split-K tiles whose grid fits one wave, the
+    256x128 ring where none does): a row sample checked bit-exact."""
+    announce(f"gemm mid M={M} N={N}")
+    rng = np.random.default_rng(M + N)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 30, replace=False)]))
+    _run_case(M, 5120, N, seed=1, rows=rows)
+
+
 def test_gemm_bias():
     announce("gemm bias")
     _run_case(16, 512, 384, seed=3, bias=True)
