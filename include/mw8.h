@@ -133,7 +133,7 @@ int32_t mw8_tuning_count(int32_t kind);
  * tuning: "decode3_gemm_kernel" or "decode_gemm_kernel" for the decode
  * cores, else the tile kernel with its leading template arguments as a
  * kernel trace prints them (e.g. "tile3_gemm_kernel<256, 256, 128, 4, 2,
- * 2>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 4>"); "" for invalid
+ * 2>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"); "" for invalid
  * sizes.  Profiling aid; no reference counterpart.
  */
 const char* mw8_gemm_kernel_name(int64_t M, int64_t N, int64_t K);
