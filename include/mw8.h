@@ -239,6 +239,39 @@ int mw8_moe_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, co
                            int32_t block_size, void* out, mw8_stream_t stream);
 
 /*
+ * The MoE layer's down-projection GEMM with the top-k slot sum fused in, for
+ * decode batches (16-row alignment blocks).  For every token t <
+ * num_valid / top_k and column n < N:
+ *   out[t, n] = bf16(sum over slots i = 0 .. top_k-1, in order, in fp32, of
+ *               bf16(epilogue(A[p] . W[e_p][n], sa[p], sw[e_p][n], routed = topk_w[p])))
+ * with p = t * top_k + i and e_p the expert of p's alignment block -- the
+ * bits of mw8_moe_gemm_w8a8_bf16 (top_k = 1, block_size 16) followed by
+ * mw8_moe_sum_reduce_bf16 over [num_valid / top_k, top_k, N].  topk_w null:
+ * no routed weight (routed on GEMM1's input).  A pair whose expert lies
+ * outside [0, E) contributes +0.  Each block owns 8 output columns of every
+ * token and keeps its pairs' values in LDS, so no workspace and no second
+ * launch.  A int8 [num_valid, K], sa fp32 [num_valid], W int8 [E, N, K], sw
+ * fp32 [E, N], sorted_ids / expert_ids / num_post_pad from
+ * mw8_moe_align_block_size with block_size 16 (max_sorted = length of
+ * sorted_ids), out bf16 [num_valid / top_k, N]; K % 16 ==
+ * 0, num_valid % top_k == 0, 16-byte aligned A and W, and
+ * mw8_moe_gemm_sum_supported(max_sorted, num_valid, E) (E <= 256,
+ * num_valid <= 2048, max_sorted <= 6144, and the LDS tables fit: every
+ * decode batch of 128 experts x top-8, up to 1024 pairs at 256 experts).
+ * Replaces fused_moe_kernel
+ * (GEMM2, MUL_ROUTED_WEIGHT) + moe_sum_reduce
+ * (python/minisgl/moe/fused.py:212-226, python/minisgl/kernel/moe_impl.py:65-98).
+ */
+int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const int32_t* sorted_ids, const int32_t* expert_ids,
+                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
+                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E, void* out,
+                               mw8_stream_t stream);
+
+/* 1 if mw8_moe_gemm_sum_w8a8_bf16 accepts these routing sizes (its LDS tables fit), else 0.  Host only. */
+int32_t mw8_moe_gemm_sum_supported(int64_t max_sorted, int64_t num_valid, int32_t E);
+
+/*
  * Gate|up grouped GEMM with the gated activation fused into its epilogue:
  * W int8 [E, N = 2I, K] holds the gate rows then the up rows of each expert;
  * out bf16 [num_valid, I] receives act(g) * u with g, u the bf16 outputs the

@@ -53,6 +53,10 @@ int moe_prepare_small(const void*, int, int64_t, int, int, int, const void*, int
 int moe_gemm_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
                   const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                   int64_t, int, int, void*, int, hipStream_t);
+int moe_gemm_sum_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*,
+                      const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
+                      int64_t, int, void*, hipStream_t);
+int moe_gemm_sum_lds_bytes(int64_t, int64_t, int);
 int rmsnorm_quant_bf16(const void*, void*, const void*, float, int64_t, int64_t, int8_t*, float*, void*,
                        hipStream_t);
 int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, float, int64_t, int64_t, int64_t,
@@ -171,6 +175,19 @@ int mw8_moe_gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W
                                int32_t block_size, int32_t act, void* out, mw8_stream_t stream) {
   MW8_ENTRY(mw8::moe_gemm_act_w8a8(A, sa, W, sw, sorted_ids, expert_ids, num_post_pad, max_sorted, topk_w,
                                    top_k, num_valid, N, K, E, block_size, act, out, S(stream)));
+}
+
+int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                               const int32_t* sorted_ids, const int32_t* expert_ids,
+                               const int32_t* num_post_pad, int64_t max_sorted, const float* topk_w,
+                               int32_t top_k, int64_t num_valid, int64_t N, int64_t K, int32_t E, void* out,
+                               mw8_stream_t stream) {
+  MW8_ENTRY(mw8::moe_gemm_sum_w8a8(A, sa, W, sw, sorted_ids, expert_ids, num_post_pad, max_sorted, topk_w,
+                                   top_k, num_valid, N, K, E, out, S(stream)));
+}
+
+int32_t mw8_moe_gemm_sum_supported(int64_t max_sorted, int64_t num_valid, int32_t E) {
+  return mw8::moe_gemm_sum_lds_bytes(max_sorted, num_valid, E) > 0 ? 1 : 0;
 }
 
 int mw8_moe_route_quant(const void* logits, int32_t is_bf16, int64_t M, int32_t E, int32_t topk,

@@ -694,6 +694,33 @@ int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_
                          : launch_grouped_small_epi<kEpiI32>(g, blocks, st);
 }
 
+// Decode down-projection with the slot sum fused in: 8 waves with 6-slot
+// rings, one block per 8 output columns (a multiple of the CU count).
+constexpr int kMoeSumWaves = 8, kMoeSumDepth = 6;
+constexpr int kMoeSumRing = kMoeSumWaves * kMoeSumDepth * kMoeSumSlot;
+constexpr int kMoeSumMaxLds = 163840 - 256;  // beside the kernel's static LDS
+
+int moe_gemm_sum_lds_bytes(int64_t max_sorted, int64_t num_valid, int E) {
+  if (max_sorted < 0 || num_valid < 0 || E < 1 || E > kMoeSumMaxExperts || max_sorted > kMoeSumMaxSorted ||
+      num_valid > kMoeSumMaxPairs)
+    return -1;
+  const int total = moe_sum_lds(kMoeSumRing, max_sorted, num_valid, E).total;
+  return total <= kMoeSumMaxLds ? total : -1;
+}
+
+int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st) {
+  constexpr auto kern = moe_gemm_sum_kernel<kMoeSumWaves, kMoeSumDepth>;
+  const int lds = moe_gemm_sum_lds_bytes(max_sorted, g.num_valid, g.num_experts);
+  if (lds < 0)
+    return set_error(kErrShape, "moe_gemm_sum: %lld pairs over %lld sorted rows and %d experts exceed the LDS tables",
+                     (long long)g.num_valid, (long long)max_sorted, g.num_experts);
+  if (const int rc = set_lds_limit<kern>(kMoeSumMaxLds)) return rc;
+  const int64_t cus = device_cus();
+  const int64_t blocks = cus * ((g.N + cus * 8 - 1) / (cus * 8));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kMoeSumWaves), lds, st, g, max_sorted);
+  return kOk;
+}
+
 // Gate|up GEMM with the gated activation fused (persistent chunk walk, the
 // moe cfg 1 tiling): out [rows, N/2] = act(gate) * up, bf16.
 int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st) {

@@ -1387,6 +1387,257 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
+// Decode down-projection with the top-k slot sum fused in
+// ------------------------------------------------------------------------
+// For 16-row alignment blocks (decode batches).  Block b owns output
+// columns [n0, n0 + R) of every token (R <= 8: the N columns cut into
+// gridDim.x equal ranges, as the dense decode grid cuts them) and walks
+// every alignment block whose expert lies in [0, E).  The expert's R
+// weight rows for those columns stream through the waves' private LDS
+// rings (slots of 8 rows x 256 K bytes filled by buffer_load ... lds with
+// the decode ring's chunk swizzle on row & 7; the MFMA's weight rows 8-15
+// read rows 0-7 again and are dropped), the 16 gathered pair rows through
+// the token register ring.  After an alignment block's last K stage its
+// wave applies the GEMM2 epilogue (activation scale, column scale, routed
+// weight: the operations of the grouped decode epilogue) and keeps the
+// bf16 value of each (pair, column) in an LDS table.  A pair sits in one
+// alignment block, so the waves write disjoint entries; after one barrier
+// the block sums each token's top_k entries in slot order in fp32 and
+// writes bf16 -- the operations of moe_sum_reduce_kernel.  A pair whose
+// expert lies outside [0, E) contributes +0.  No workspace, no exchange
+// between blocks.  The tables the loop reads (sorted ids, the list of
+// alignment blocks with their experts, the pairs' activation scales and
+// routed weights, every expert's column scales for this block's columns)
+// are loaded into LDS once, before the weight stream.
+struct MoeSumLds {
+  int sid, exp, list, sa, rw, sw, out, total;
+};
+// Sizes one prologue pass of moe_gemm_sum_kernel loads (the host checks them).
+constexpr int kMoeSumMaxSorted = 6144, kMoeSumMaxPairs = 2048, kMoeSumMaxExperts = 256;
+__host__ __device__ inline int moe_sum_up16(int64_t bytes) { return static_cast<int>((bytes + 15) & ~int64_t{15}); }
+__host__ __device__ inline MoeSumLds moe_sum_lds(int ring_bytes, int64_t max_sorted, int64_t num_valid, int E) {
+  MoeSumLds l;
+  l.sid = ring_bytes;
+  l.exp = l.sid + moe_sum_up16(4 * max_sorted);
+  l.list = l.exp + moe_sum_up16(4 * (max_sorted / 16));
+  l.sa = l.list + moe_sum_up16(4 * (max_sorted / 16));
+  l.rw = l.sa + moe_sum_up16(4 * num_valid);
+  l.sw = l.rw + moe_sum_up16(4 * num_valid);
+  l.out = l.sw + 32 * E;
+  l.total = l.out + moe_sum_up16(16 * num_valid);
+  return l;
+}
+constexpr int kMoeSumSlot = 2048;  // 8 weight rows x 256 K bytes
+
+template <int WAVES, int D>
+__global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, int64_t max_sorted) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kOps = 2 + 4;  // vector memory ops per stage: 2 DMA + 4 token loads
+  static_assert(D >= 2 && D <= 8 && (D - 1) * kOps < 64, "ring depth");
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int s_count;
+  const int nv = static_cast<int>(g.num_valid), E = g.num_experts;
+  const MoeSumLds L = moe_sum_lds(WAVES * D * kMoeSumSlot, max_sorted, nv, E);
+  int32_t* t_sid = reinterpret_cast<int32_t*>(lds + L.sid);
+  int32_t* t_exp = reinterpret_cast<int32_t*>(lds + L.exp);
+  int32_t* t_list = reinterpret_cast<int32_t*>(lds + L.list);
+  float* t_sa = reinterpret_cast<float*>(lds + L.sa);
+  float* t_rw = reinterpret_cast<float*>(lds + L.rw);
+  float* t_sw = reinterpret_cast<float*>(lds + L.sw);
+  uint16_t* t_out = reinterpret_cast<uint16_t*>(lds + L.out);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = g.N * blockIdx.x / gridDim.x;
+  const int R = static_cast<int>(g.N * (blockIdx.x + 1) / gridDim.x - n0);
+  if (R <= 0) return;  // more blocks than columns (uniform per block)
+  const int64_t npp = *g.num_post_pad;
+  const int n_sorted = static_cast<int>(npp < max_sorted ? npp : max_sorted);
+  const int nb = n_sorted / 16;
+  const bool routed = g.topk_w != nullptr;
+
+  // ---- tables, every global load of the prologue issued before the first
+  // LDS store (one round trip; the host bounds the sizes to one pass)
+  constexpr int kT = 64 * WAVES;
+  constexpr int kSidPer = (kMoeSumMaxSorted + kT - 1) / kT, kPairPer = (kMoeSumMaxPairs + kT - 1) / kT;
+  constexpr int kSwPer = (8 * kMoeSumMaxExperts + kT - 1) / kT, kExpPer = (kMoeSumMaxSorted / 16 + kT - 1) / kT;
+  int32_t v_sid[kSidPer], v_exp[kExpPer];
+  float v_sa[kPairPer], v_rw[kPairPer], v_sw[kSwPer];
+#pragma unroll
+  for (int u = 0; u < kSidPer; ++u) {
+    const int i = u * kT + tid;
+    v_sid[u] = i < n_sorted ? g.sorted_ids[i] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < kExpPer; ++u) {
+    const int i = u * kT + tid;
+    v_exp[u] = i < nb ? g.expert_ids[i] : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < kPairPer; ++u) {
+    const int i = u * kT + tid;
+    v_sa[u] = i < nv ? g.sa[i] : 0.0f;
+    v_rw[u] = (routed && i < nv) ? g.topk_w[i] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kSwPer; ++u) {
+    const int i = u * kT + tid, r = i & 7;
+    v_sw[u] = (i < E * 8 && r < R) ? g.sw[static_cast<int64_t>(i >> 3) * g.N + n0 + r] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kSidPer; ++u) {
+    const int i = u * kT + tid;
+    if (i < n_sorted) t_sid[i] = v_sid[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kExpPer; ++u) {
+    const int i = u * kT + tid;
+    if (i < nb) t_exp[i] = v_exp[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kPairPer; ++u) {
+    const int i = u * kT + tid;
+    if (i < nv) {
+      t_sa[i] = v_sa[u];
+      t_rw[i] = v_rw[u];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kSwPer; ++u) {
+    const int i = u * kT + tid;
+    if (i < E * 8) t_sw[i] = v_sw[u];
+  }
+  for (int i = tid; i < 4 * nv; i += kT) reinterpret_cast<uint32_t*>(t_out)[i] = 0u;
+  __syncthreads();
+  if (wave == 0) {  // alignment blocks of an expert in [0, E), packed (expert << 20) | block
+    int cnt = 0;
+    for (int base = 0; base < nb; base += 64) {
+      const int a = base + lane;
+      const int e = a < nb ? t_exp[a] : -1;
+      const bool ok = e >= 0 && e < E;
+      const uint64_t m = __ballot(ok);
+      if (ok) t_list[cnt + __popcll(m & ((uint64_t{1} << lane) - 1))] = (e << 20) | a;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) s_count = cnt;
+  }
+  __syncthreads();
+  const int nlist = s_count;
+
+  // ---- the wave's alignment blocks i = wave, wave + WAVES, ...: S stages of 256 K bytes each
+  const int S = static_cast<int>((g.K + 255) / 256);
+  const int n_mine = nlist > wave ? (nlist - wave + WAVES - 1) / WAVES : 0;
+  const int n_st = n_mine * S;
+  unsigned char* my_ring = lds + wave * (D * kMoeSumSlot);
+  const int r16 = lane & 15, grp = lane >> 4, r8 = lane & 7;
+  // weight DMA: instruction j fills LDS rows 4j .. 4j+3; lane l fills row
+  // 4j + l/16, chunk l%16 from global chunk (l%16) ^ row
+  uint32_t w_off[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    w_off[j] = static_cast<uint32_t>(row * g.K + 16 * ((lane & 15) ^ row));
+  }
+  typedef const v4i __attribute__((address_space(1)))* gv4i_ptr;
+  const uint64_t zero_addr = reinterpret_cast<uint64_t>(kZeroChunk);
+  v4i xr[D][4];
+
+  auto issue = [&](int d, int s) {
+    unsigned char* slot = my_ring + d * kMoeSumSlot;
+    int a = 0, e = 0, st = 0;
+    const bool real = s < n_st;  // wave-uniform
+    if (real) {
+      const int i = s / S;
+      st = s - i * S;
+      const int ent = __builtin_amdgcn_readfirstlane(t_list[wave + WAVES * i]);
+      a = ent & 0xFFFFF;
+      e = ent >> 20;
+    }
+    // a padding stage reads past the buffer range: zeros, no traffic
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        scalar_ptr(const_cast<int8_t*>(g.W + (static_cast<int64_t>(e) * g.N + n0) * g.K)), 0,
+        static_cast<int>(R * g.K), kBufferFlags);
+    const int soff = real ? st * 256 : 0x7fff0000;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0,
+                                               kStreamAux);
+    // the token address is selected bitwise and every load is unconditional:
+    // a branch around a load makes its result a merge that the compiler
+    // waits for with vmcnt(0), which would drain the whole ring each stage
+    const int32_t p_raw = t_sid[a * 16 + r16];  // a = 0 on a padding stage (nlist > 0 there)
+    const int32_t p = real ? p_raw : nv;
+    const bool pok = p < nv;
+    const uint64_t xrow = reinterpret_cast<uint64_t>(g.A) + static_cast<uint64_t>(pok ? p : 0) * g.lda;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
+      const uint64_t m = (pok && k < g.K) ? ~uint64_t{0} : uint64_t{0};
+      const uint64_t addr = ((xrow + static_cast<uint64_t>(k)) & m) | (zero_addr & ~m);
+      xr[d][kb] = *reinterpret_cast<gv4i_ptr>(addr);
+    }
+  };
+
+  v4i acc = v4i{0};
+  auto consume = [&](int d, int s) {
+    const unsigned char* slot = my_ring + d * kMoeSumSlot;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const v4i w = *reinterpret_cast<const v4i*>(slot + r8 * 256 + 16 * ((4 * kb + grp) ^ r8));
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, xr[d][kb], acc, 0, 0, 0);
+    }
+    if (s >= n_st) return;
+    const int i = s / S;
+    if (s - i * S != S - 1) return;  // not the alignment block's last stage (uniform)
+    // epilogue: lane holds weight row 4 * grp + v (rows 0-7 in lanes 0-31)
+    // of token column r16 of the alignment block
+    const int ent = __builtin_amdgcn_readfirstlane(t_list[wave + WAVES * i]);
+    const int a = ent & 0xFFFFF, e = ent >> 20;
+    const int32_t p = t_sid[a * 16 + r16];
+    if (grp < 2 && p < nv) {
+      const float sa = t_sa[p], rw = t_rw[p];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 4 * grp + v;
+        if (row >= R) continue;
+        float t = epi_scale(acc[v], sa, t_sw[e * 8 + row]);
+        if (routed) t = t * rw;
+        t_out[p * 8 + row] = f32_to_bf16(t);
+      }
+    }
+    acc = v4i{0};
+  };
+
+  if (n_st > 0) {
+    const int n_pad = ((n_st + D - 1) / D) * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+    for (int s0 = 0; s0 < n_pad - D; s0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        wait_vmcnt<(D - 1) * kOps>();
+        consume(d, s0 + d);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): fragments read before the refill
+        issue(d, s0 + d + D);
+      }
+    }
+    auto drain = [&](int d) { consume(d, n_pad - D + d); };
+    RingDrain<D, kOps, 0>::run(drain);
+  }
+  __syncthreads();
+
+  // ---- slot sum in slot order (fp32), one (token, column) per thread
+  const int tk = g.top_k, T = nv / tk;
+  uint16_t* out = static_cast<uint16_t*>(g.out);
+  for (int idx = tid; idx < T * R; idx += 64 * WAVES) {
+    const int t = idx / R, r = idx - t * R;
+    float sum = 0.0f;
+    for (int i = 0; i < tk; ++i) sum = sum + bf16_to_f32(t_out[(t * tk + i) * 8 + r]);
+    out[static_cast<int64_t>(t) * g.ldo + n0 + r] = f32_to_bf16(sum);
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// ------------------------------------------------------------------------
 // K-split reduction: out[tile rows, tile cols] = epilogue(sum_s part[u0 + s])
 // with the partials summed in split order (exact int32).  One thread per 8
 // consecutive columns of one tile row.

@@ -10,6 +10,8 @@ namespace mw8 {
 int launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
 int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
 int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
+int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st);
+int moe_gemm_sum_lds_bytes(int64_t max_sorted, int64_t num_valid, int E);
 
 namespace {
 
@@ -547,6 +549,32 @@ int moe_gemm_act_w8a8(const int8_t* A, const float* sa, const int8_t* W, const f
   g.align_bsz = bsz;
   if (const int rc = launch_grouped_act(g, act, st)) return rc;
   return check_launch("moe_gemm_act");
+}
+
+int moe_gemm_sum_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* npp,
+                      int64_t max_sorted, const float* topk_w, int top_k, int64_t num_valid, int64_t N,
+                      int64_t K, int E, void* out, hipStream_t st) {
+  MW8_REQUIRE(A && sa && W && sw && sorted_ids && expert_ids && npp && out, kErrArg, "moe_gemm_sum: null pointer");
+  MW8_REQUIRE(N > 0 && K > 0 && K % 16 == 0 && K <= (1ll << 17), kErrShape,
+              "moe_gemm_sum: need K %% 16 == 0 and K <= 131072 (N=%lld K=%lld)", (long long)N, (long long)K);
+  MW8_REQUIRE(top_k >= 1 && num_valid >= 0 && num_valid % top_k == 0 && max_sorted >= 0,
+              kErrShape, "moe_gemm_sum: bad routing sizes (top_k=%d num_valid=%lld max_sorted=%lld)", top_k,
+              (long long)num_valid, (long long)max_sorted);
+  MW8_REQUIRE(moe_gemm_sum_lds_bytes(max_sorted, num_valid, E) > 0, kErrShape,
+              "moe_gemm_sum: %lld pairs over %lld sorted rows and %d experts exceed the LDS tables "
+              "(mw8_moe_gemm_sum_supported)",
+              (long long)num_valid, (long long)max_sorted, E);
+  MW8_REQUIRE(aligned16(A) && aligned16(W), kErrAlign, "moe_gemm_sum: A and W need 16-byte alignment");
+  if (num_valid == 0) return kOk;
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
+  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
+  g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
+  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.align_bsz = 16;
+  if (const int rc = launch_moe_gemm_sum(g, max_sorted, st)) return rc;
+  return check_launch("moe_gemm_sum");
 }
 
 }  // namespace mw8

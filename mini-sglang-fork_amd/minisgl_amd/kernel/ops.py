@@ -493,6 +493,51 @@ def fused_moe_kernel_w8a8_i32(
     return out
 
 
+def moe_gemm_sum_supported(max_sorted: int, num_valid: int, num_experts: int) -> bool:
+    """Whether fused_moe_kernel_sum_w8a8 takes these routing sizes (its LDS
+    tables fit one block); host only."""
+    return bool(load().mw8_moe_gemm_sum_supported(max_sorted, num_valid, num_experts))
+
+
+def fused_moe_kernel_sum_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    output: torch.Tensor,
+    topk_weights: Optional[torch.Tensor],
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    top_k: int,
+    num_valid_tokens: int,
+) -> None:
+    """Down-projection grouped GEMM with the top-k slot sum fused in, for
+    16-row alignment blocks: output bf16 [M, N] receives, bit for bit, what
+    fused_moe_kernel_w8a8 (pair rows, routed weight from ``topk_weights``
+    unless None) followed by moe_sum_reduce writes (python/minisgl/moe/fused.py:212-226)."""
+    _on_gpu(A, A_scale, B, B_scale, output)
+    _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [M*k, K]")
+    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
+    E, N, K = B.shape
+    _need(A.shape == (num_valid_tokens, K), "A: int8 [M*k, K]")
+    _need(A_scale.dtype == torch.float32 and A_scale.shape == (num_valid_tokens,), "A_scale: fp32 [M*k]")
+    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
+    _need(num_valid_tokens % top_k == 0, "num_valid_tokens: a multiple of top_k")
+    _need(output.dtype == torch.bfloat16 and output.is_contiguous() and output.shape == (num_valid_tokens // top_k, N),
+          "output: bf16 [M, N]")
+    _need(topk_weights is None or (topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()
+                                   and topk_weights.numel() == num_valid_tokens), "topk_weights: fp32 [M, k]")
+    _need(sorted_token_ids.dtype == torch.int32 and sorted_token_ids.stride(0) == 1, "sorted_token_ids: int32")
+    check(
+        load().mw8_moe_gemm_sum_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(sorted_token_ids), _ptr(expert_ids),
+            _ptr(num_tokens_post_padded), sorted_token_ids.shape[0], _ptr(topk_weights), top_k,
+            num_valid_tokens, N, K, E, _ptr(output), _stream(A),
+        )
+    )
+
+
 def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
     """out[t] = bf16(sum_i in[t, i]) (python/minisgl/kernel/moe_impl.py:65-98)."""
     _on_gpu(input, output)
@@ -508,6 +553,8 @@ def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
 
 
 __all__ = [
+    "moe_gemm_sum_supported",
+    "fused_moe_kernel_sum_w8a8",
     "gemm_workspace",
     "reserve_gemm_workspace",
     "quant_per_token",

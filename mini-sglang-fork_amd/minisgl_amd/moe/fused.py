@@ -13,7 +13,9 @@ w2 int8 [E, H, I]:
 5. activation + requant -> int8 [M*k, I] + fp32 scales (prefill batches:
    the activation runs in GEMM1's epilogue, then the plain quantizer)
 6. GEMM2 (top_k = 1) -> bf16 cache [M*k, H], routed weight otherwise (:217)
-7. slot sum, written into ``hidden_states`` in place (:175, :223-226)
+7. slot sum, written into ``hidden_states`` in place (:175, :223-226);
+   decode batches (16-row blocks) run 6 and 7 as one kernel
+   (``fused_moe_kernel_sum_w8a8``), the same bits without the cache
 
 All counts stay on the device (no host sync), so the call can be captured
 in a HIP graph.  For the smallest decode batches (M * k <= 32) the backend
@@ -31,8 +33,10 @@ import torch
 from ..kernel import (
     act_and_mul_quant,
     fused_moe_kernel_act_w8a8,
+    fused_moe_kernel_sum_w8a8,
     fused_moe_kernel_w8a8,
     moe_align_block_size,
+    moe_gemm_sum_supported,
     moe_prepare_small,
     moe_route_quant,
     moe_sum_reduce,
@@ -127,9 +131,22 @@ def _experts_from_routing(
     """Steps 4-7: GEMM1, activation + requant, GEMM2, slot sum in place.
     Prefill batches (>= 32 pairs per expert, 64/128-row blocks) run the
     activation in GEMM1's epilogue, writing [M*k, I] instead of [M*k, 2I];
-    the values are the same bit for bit."""
+    decode batches (16-row blocks) run the slot sum inside GEMM2, which
+    writes hidden_states directly; the values are the same bit for bit."""
     M, H = hidden_states.shape
     E, N, K = w1.shape
+    if bsz == 16 and moe_gemm_sum_supported(sorted_ids.shape[0], M * k, E):
+        cache1 = torch.empty((M * k, N), dtype=torch.bfloat16, device=hidden_states.device)
+        fused_moe_kernel_w8a8(
+            q_h, s_h, w1, w1_scale, cache1, topk_weights, sorted_ids, expert_ids, num_post_pad,
+            apply_router_weight_on_input, k, bsz, M * k,
+        )
+        q_a, s_a = act_and_mul_quant(cache1, activation)
+        fused_moe_kernel_sum_w8a8(
+            q_a, s_a, w2, w2_scale, hidden_states, None if apply_router_weight_on_input else topk_weights,
+            sorted_ids, expert_ids, num_post_pad, k, M * k,
+        )
+        return hidden_states
     # one buffer backs both bf16 caches, as in the reference (:157-172)
     cache = torch.empty(M * k * max(N, H), dtype=torch.bfloat16, device=hidden_states.device)
     if bsz in (64, 128) and M * k >= 32 * E and N % 16 == 0 and K % 64 == 0 and E < 512:

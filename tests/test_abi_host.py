@@ -77,6 +77,24 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_gemm_workspace_bytes(32, 34816, 5120) == 0  # decode core
 
 
+def test_moe_gemm_sum_supported_sizes(lib):
+    """The fused down-projection + slot sum keeps its routing tables in LDS:
+    every decode batch of config 3 (up to E = 128 tokens x top-8, sorted
+    positions numel + (E + 1) * 15) fits, and so does E = 256 at 1024 pairs;
+    more pairs, more sorted positions than one prologue pass loads, more than
+    256 experts or negative sizes do not."""
+    sup = lib.mw8_moe_gemm_sum_supported
+    for m in (1, 16, 64, 128):
+        P = m * 8
+        assert sup(lib.mw8_moe_align_max_padded(P, 128, 16), P, 128) == 1
+    assert sup(lib.mw8_moe_align_max_padded(1024, 256, 16), 1024, 256) == 1
+    assert sup(lib.mw8_moe_align_max_padded(2048, 256, 16), 2048, 256) == 0
+    assert sup(6160, 64, 8) == 0
+    assert sup(lib.mw8_moe_align_max_padded(4096, 128, 16), 4096, 128) == 0
+    assert sup(1024, 64, 257) == 0
+    assert sup(-16, 8, 8) == 0 and sup(16, -8, 8) == 0
+
+
 def test_workspace_bound_and_tuning_counts(lib):
     """mw8_gemm_workspace_max_bytes bounds every plan (r * sp <= S slots of
     the largest split tile), so one reservation never has to grow; the
@@ -141,6 +159,16 @@ def test_argument_errors_return_codes(lib):
     assert lib.mw8_rmsnorm_strided_bf16(FAKE_A, 64, FAKE_A, 64, FAKE_B, 1e-6, 4, 8, 16, None) == E["MW8_ERR_SHAPE"]
     assert lib.mw8_rmsnorm_strided_bf16(FAKE_A, 256, FAKE_A, 256, None, 1e-6, 4, 8, 16, None) == E["MW8_ERR_ARG"]
     assert lib.mw8_rmsnorm_strided_bf16(FAKE_A + 2, 256, FAKE_A, 256, FAKE_B, 1e-6, 4, 8, 16, None) == E["MW8_ERR_ALIGN"]
+    # down-projection with the slot sum: null operand, pairs not a multiple of top_k, LDS tables too large
+    gs = lib.mw8_moe_gemm_sum_w8a8_bf16
+    assert gs(None, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 2944, None, 8, 1024, 2048, 768, 128,
+              FAKE_A, None) == E["MW8_ERR_ARG"]
+    assert gs(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 2944, None, 8, 1020, 2048, 768, 128,
+              FAKE_A, None) == E["MW8_ERR_SHAPE"]
+    assert gs(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 8000, None, 8, 4000, 2048, 768, 128,
+              FAKE_A, None) == E["MW8_ERR_SHAPE"] and b"LDS" in lib.mw8_last_error()
+    assert gs(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 2944, None, 8, 1024, 2048, 760, 128,
+              FAKE_A, None) == E["MW8_ERR_SHAPE"]  # K % 16 != 0
     # empty problems are no-ops
     assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0
 

@@ -14,9 +14,11 @@ from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
 from minisgl_amd.kernel import (
     act_and_mul_quant,
     fused_moe_kernel_act_w8a8,
+    fused_moe_kernel_sum_w8a8,
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
+    moe_gemm_sum_supported,
     moe_prepare_small,
     moe_route_quant,
     moe_sum_reduce,
@@ -419,6 +421,72 @@ def test_sum_reduce():
     o2 = torch.empty(1, 8, dtype=torch.bfloat16, device=DEV)
     moe_sum_reduce(y.to(DEV), o2)
     assert o2.float().abs().max().item() == 0.0
+
+
+def _gemm2_sum_check(ids_ref, w_ref, W, SW, K, k, routed, seed, invalid=None):
+    """Down-projection with the slot sum fused in against (a) the grouped
+    GEMM into pair rows followed by moe_sum_reduce on the GPU and (b) the
+    oracle's grouped GEMM + slot sum; bit for bit.  ``invalid``: pairs whose
+    expert id is E (skipped), which contribute +0 to their token's sum."""
+    E, N, _ = W.shape
+    P = ids_ref.size
+    M = P // k
+    gen = torch.Generator().manual_seed(seed)
+    act = torch.randn(P, K, generator=gen).to(torch.bfloat16)
+    q, s = quant_per_token(act.to(DEV))
+    ids = torch.from_numpy(ids_ref.astype(np.int32)).to(DEV)
+    tw = torch.from_numpy(w_ref.astype(np.float32)).to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, 16, E)
+    assert moe_gemm_sum_supported(sorted_ids.shape[0], P, E)
+    Wd, SWd = W.to(DEV), SW.to(DEV)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_sum_w8a8(q, s, Wd, SWd, out, tw if routed else None, sorted_ids, expert_ids, npp, k, P)
+    # oracle: the pairs' rows (zero for skipped pairs), summed in slot order
+    ok = ids_ref.reshape(-1) < E
+    rows = orc.grouped_gemm_w8a8(q.cpu().numpy(), s.cpu().numpy(), W.numpy(), SW.numpy(),
+                                 np.where(ok, ids_ref.reshape(-1), 0), 1,
+                                 routed=w_ref.reshape(-1) if routed else None)
+    rows[~ok] = 0.0
+    ref = orc.moe_sum_reduce(rows.reshape(M, k, N))
+    eq = bf16_bits_equal(out, ref)
+    assert eq.all(), f"{(~eq).sum()} of {eq.size} outputs differ"
+    if invalid is None:  # the two-kernel path writes the same bits
+        c3 = torch.empty(P, N, dtype=torch.bfloat16, device=DEV)
+        fused_moe_kernel_w8a8(q, s, Wd, SWd, c3, tw, sorted_ids, expert_ids, npp, routed, 1, 16, P)
+        o = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        moe_sum_reduce(c3.view(M, k, N), o)
+        assert torch.equal(out.view(torch.int16), o.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 64, 128])
+@pytest.mark.parametrize("routed", [True, False])
+def test_gemm2_sum_fused_config3(M, routed):
+    """Config 3 (E 128, top-8, H 2048, I 768) at decode sizes, routed weight
+    in GEMM2 or not (applied on GEMM1's input)."""
+    announce(f"gemm2+sum fused M={M} routed={routed}")
+    c = moe_case(M, seed=M + 11)
+    w_ref, ids_ref = orc.topk_softmax(f32(c["logits"]), 8, True)
+    _gemm2_sum_check(ids_ref, w_ref, c["w2"], c["s_w2"], 768, 8, routed, seed=M)
+
+
+@pytest.mark.parametrize("N,K,E,k,M", [(208, 384, 8, 2, 50), (4096, 256, 4, 4, 33), (24, 1040, 3, 3, 7)])
+def test_gemm2_sum_fused_ragged(N, K, E, k, M):
+    """Column ranges of 0-1 columns per block (N = 24, 208), more blocks than
+    CUs (N = 4096: 8 columns each over 512 blocks), K not a multiple of the
+    256-byte stage, skewed routing, and top-k other than 8; then pairs routed
+    to expert E (skipped) contribute +0."""
+    announce(f"gemm2+sum fused ragged N={N} K={K} E={E} k={k} M={M}")
+    gen = torch.Generator().manual_seed(N + K)
+    W = torch.randint(-127, 128, (E, N, K), generator=gen, dtype=torch.int8)
+    SW = torch.rand(E, N, generator=gen) * 1e-2 + 1e-4
+    rng = np.random.default_rng(N)
+    ids_ref = np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int64)
+    ids_ref[: M // 3] = np.minimum(ids_ref[: M // 3], 1)  # skew: a third of the tokens on experts 0-1
+    w_ref = rng.random((M, k)).astype(np.float32)
+    _gemm2_sum_check(ids_ref, w_ref, W, SW, K, k, True, seed=K)
+    bad = ids_ref.copy()
+    bad[::4, -1] = E
+    _gemm2_sum_check(bad, w_ref, W, SW, K, k, True, seed=K + 1, invalid=True)
 
 
 @pytest.mark.parametrize("M", [4, 16, 256, 4096])
