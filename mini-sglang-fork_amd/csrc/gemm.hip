@@ -694,9 +694,13 @@ int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_
                          : launch_grouped_small_epi<kEpiI32>(g, blocks, st);
 }
 
-// Decode down-projection with the slot sum fused in: 8 waves with 6-slot
+// Decode down-projection with the slot sum fused in: 16 waves with 3-slot
 // rings, one block per 8 output columns (a multiple of the CU count).
-constexpr int kMoeSumWaves = 8, kMoeSumDepth = 6;
+// Measured on MI355X, config 3 (kernel alone, us, 16 / 64 tokens): 16 x 3
+// 26.8-27.3 / 37.6-38.0; 8 x 4 28.2-29.3 / 37.8-38.7; 8 x 6 28.8-29.7 /
+// 38.5-39.3; 8 x 8 30.6-31.4 / 39.2-39.8 (GEMM2 26.5-27.4 + slot sum 3.2
+// / 40.0-40.5 + 3.1 as two kernels).
+constexpr int kMoeSumWaves = 16, kMoeSumDepth = 3;
 constexpr int kMoeSumRing = kMoeSumWaves * kMoeSumDepth * kMoeSumSlot;
 constexpr int kMoeSumMaxLds = 163840 - 256;  // beside the kernel's static LDS
 
