@@ -469,6 +469,48 @@ def test_gemm2_sum_fused_config3(M, routed):
     _gemm2_sum_check(ids_ref, w_ref, c["w2"], c["s_w2"], 768, 8, routed, seed=M)
 
 
+@pytest.mark.parametrize(
+    "M,E,k,H,I,on_input",
+    [(3, 8, 2, 4096, 1792, False),    # Mixtral-like routing (8 experts, top-2), wide hidden
+     (40, 64, 6, 2048, 1408, False),  # DeepSeek-like (64 experts, top-6), I off the 256-byte stage
+     (100, 128, 8, 2048, 768, True),  # config 3, routed weight on GEMM1's input
+     (7, 256, 8, 1024, 512, False)],  # 256 experts
+)
+def test_moe_layer_decode_fused_sum_equals_two_kernels(M, E, k, H, I, on_input):
+    """Decode batches (M <= E: 16-row blocks) through MoELayer: the layer's
+    output with GEMM2 and the slot sum fused is bit-identical to the same
+    layer run with GEMM2 into pair rows + moe_sum_reduce (whose stages the
+    oracle pins); the all-CPU chain end to end as an informational bound."""
+    import minisgl_amd.moe.fused as fused_mod
+
+    announce(f"moe decode fused sum M={M} E={E} k={k} H={H} I={I} on_input={on_input}")
+    c = moe_case(M, hidden=H, num_experts=E, inter=I, seed=M + E)
+    layer = _moe_layer(c, apply_router_weight_on_input=on_input, E=E, k=k, H=H, I=I)
+    set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+    outs = []
+    orig = fused_mod.moe_gemm_sum_supported
+    try:
+        for fused_on in (True, False):
+            fused_mod.moe_gemm_sum_supported = orig if fused_on else (lambda *a: False)
+            h = c["hidden"].to(DEV)
+            outs.append(layer.forward(h, c["logits"].to(DEV)).clone())
+        torch.cuda.synchronize()
+    finally:
+        fused_mod.moe_gemm_sum_supported = orig
+        reset_global_ctx()
+    from minisgl_amd.kernel.lib import load
+
+    assert orig(load().mw8_moe_align_max_padded(M * k, E, 16), M * k, E), "the fused path applies here"
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    # end to end against the all-CPU chain: informational beside the bit-identity above (a requant
+    # rounding flip between the stages moves a chain, as in test_moe_layer_stagewise)
+    ref = orc.fused_moe_w8a8(f32(c["hidden"]), c["w1"].numpy(), c["s_w1"].numpy(), c["w2"].numpy(),
+                             c["s_w2"].numpy(), f32(c["logits"]), k, apply_router_weight_on_input=on_input)
+    e2e = rel_l2(f32(outs[0]), ref)
+    print(f"end-to-end rel-L2 vs CPU chain: {e2e:.3e}")
+    assert e2e <= 2e-2
+
+
 @pytest.mark.parametrize("N,K,E,k,M", [(208, 384, 8, 2, 50), (4096, 256, 4, 4, 33), (24, 1040, 3, 3, 7)])
 def test_gemm2_sum_fused_ragged(N, K, E, k, M):
     """Column ranges of 0-1 columns per block (N = 24, 208), more blocks than
