@@ -112,19 +112,20 @@ int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
 // N = 4096).  The balanced grid (256 blocks of 20 rows, two MFMA row
 // groups sharing the token fragments) takes 18.1 us, and 21.6 us instead
 // of 28.8 us at 16 tokens.  Narrow N (<= 16384): 4 waves x 3 slots of 32
-// rows at one token, 8 waves x 2 slots up to 8 and from 17 tokens, 4
-// waves x 2 slots at 9-16.  Wide N (gate_up, 2176 row groups): 16-row
-// blocks, 2 waves x 2 slots at one token (30.6 us, 5.8 TB/s), one wave x
-// 4 slots up to 8, 32-row blocks of one wave x 4 slots at 17-32 tokens.
+// rows at one token (and at 2-8 tokens for K > 8192: down M=2 / 8 17.0-17.2
+// / 17.6-17.8 us against 17.4 / 17.9-18.2 for 8 waves x 2), 8 waves x 2
+// slots up to 8 and from 17 tokens, 4 waves x 2 slots at 9-16.  Wide N
+// (gate_up, 2176 row groups): 16-row blocks, 2 waves x 2 slots at one
+// token (30.6 us, 5.8 TB/s), one wave x 4 slots up to 8, 32-row blocks of
+// one wave x 4 slots at 17-32 tokens.
 // From 33 tokens on the token operand, read per wave through the texture
 // path, costs more than the weight stream: the register-streaming core
 // with 32 rows over 8 waves (cfg 0) wins, or 64 rows per block for very
 // wide N (cfg 1), which keeps fewer blocks re-reading the token panel.
 int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
-  (void)K;
   const bool wide = N >= 16384;
   if (M == 1) return wide ? 3 : 6;
-  if (M <= 8) return wide ? 2 : 7;
+  if (M <= 8) return wide ? 2 : (K > 8192 ? 6 : 7);
   if (M <= 16) return 5;
   if (M <= 32) return wide ? 4 : 7;
   if (M > 48 && wide) return 1;
