@@ -66,12 +66,12 @@ __device__ __forceinline__ uint32_t row_max(uint32_t v, uint32_t* red) {
     return wave_max_u32<TPR>(v);
   } else {
     v = wave_max_u32(v);
-    const int wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6, base = (threadIdx.x / TPR) * (TPR / 64);  // the row's first wave
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    uint32_t m = red[0];
+    uint32_t m = red[base];
 #pragma unroll
-    for (int w = 1; w < TPR / 64; ++w) m = red[w] > m ? red[w] : m;
+    for (int w = 1; w < TPR / 64; ++w) m = red[base + w] > m ? red[base + w] : m;
     return m;
   }
 }
@@ -267,12 +267,12 @@ __device__ __forceinline__ double row_sum_f64(double v, double* red) {
   if constexpr (TPR == 64) {
     return v;
   } else {
-    const int wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6, base = (threadIdx.x / TPR) * (TPR / 64);  // the row's first wave
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    double t = red[0];
+    double t = red[base];
 #pragma unroll
-    for (int w = 1; w < TPR / 64; ++w) t += red[w];
+    for (int w = 1; w < TPR / 64; ++w) t += red[base + w];
     return t;
   }
 }
