@@ -839,28 +839,39 @@ def run_secondary(dev, peak_tops):
         log(f"moe cfg3 M={Mt}: {res['moe_cfg3'][str(Mt)]}")
         del c, layer, h0, h, lg
 
-    # config 4: Qwen3-32B GEMM chain at M = 2080
+    # config 4: Qwen3-32B GEMM chain at M = 2080, whole layer on one GPU and
+    # one GPU's share of it under TP 4 (the reference's serving setup)
+    from minisgl_amd.benchmark.inputs import QWEN3_32B_TP4_SHARE
     Mc = 2080
-    Wc = {n: (torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev),
-              torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3) for n, K, N in QWEN3_32B_CHAIN}
-    xin = torch.randn(Mc, 5120, generator=gen, device=dev).to(torch.bfloat16)
 
-    def chain():
-        q0, s0 = quant_per_token(xin)
-        qkv = gemm_w8a8(q0, s0, *Wc["qkv"])
-        q1, s1 = quant_per_token(qkv[:, :8192])  # q-slice stands in for the attention output
-        o = gemm_w8a8(q1, s1, *Wc["o_proj"])
-        q2, s2 = quant_per_token(o)
-        gu = gemm_w8a8(q2, s2, *Wc["gate_up"])
-        q3, s3 = act_and_mul_quant(gu)
-        return gemm_w8a8(q3, s3, *Wc["down"])
+    def time_chain(table, q_cols):
+        Wc = {n: (torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8, device=dev),
+                  torch.rand(N, generator=gen, device=dev) * 9e-3 + 1e-3) for n, K, N in table}
+        xin = torch.randn(Mc, 5120, generator=gen, device=dev).to(torch.bfloat16)
 
-    t = perf_hip(chain, graph_calls=4) * 1e-3
-    ops = sum(2.0 * Mc * K * N for _, K, N in QWEN3_32B_CHAIN)
-    res["chain_cfg4"] = {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 2),
-                         "mfma_frac": round(ops / t / 1e12 / peak_tops, 4),
-                         "note": "quant + 4 GEMMs + act/requant, attention replaced by the q-slice"}
+        def chain():
+            q0, s0 = quant_per_token(xin)
+            qkv = gemm_w8a8(q0, s0, *Wc["qkv"])
+            q1, s1 = quant_per_token(qkv[:, :q_cols])  # q-slice stands in for the attention output
+            o = gemm_w8a8(q1, s1, *Wc["o_proj"])
+            q2, s2 = quant_per_token(o)
+            gu = gemm_w8a8(q2, s2, *Wc["gate_up"])
+            q3, s3 = act_and_mul_quant(gu)
+            return gemm_w8a8(q3, s3, *Wc["down"])
+
+        t = perf_hip(chain, graph_calls=4) * 1e-3
+        ops = sum(2.0 * Mc * K * N for _, K, N in table)
+        del Wc, xin
+        return {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 2),
+                "mfma_frac": round(ops / t / 1e12 / peak_tops, 4),
+                "gemms": {n: [K, N] for n, K, N in table},
+                "note": "quant + 4 GEMMs + act/requant, attention replaced by the q-slice"}
+
+    res["chain_cfg4"] = time_chain(QWEN3_32B_CHAIN, 8192)
     log(f"chain cfg4: {res['chain_cfg4']}")
+    res["chain_cfg4_tp4_share"] = time_chain(QWEN3_32B_TP4_SHARE, 2048)
+    res["chain_cfg4_tp4_share"]["note"] += "; one rank's GEMMs under TP 4, all-reduce not included"
+    log(f"chain cfg4 TP4 share: {res['chain_cfg4_tp4_share']}")
     return res
 
 

@@ -34,6 +34,19 @@ QWEN3_32B_CHAIN: List[Tuple[str, int, int]] = [
     ("down", 25600, 5120),
 ]
 
+# One GPU's share of the same layer under tensor parallelism 4 (the
+# reference README's Qwen3-32B TP4 serving setup): column-parallel qkv
+# (16 q + 2 kv heads of 128) and gate_up shard N, row-parallel o_proj and
+# down shard K (each rank quantizes its own K shard; the bf16 partial
+# outputs would then be summed by the all-reduce of
+# python/minisgl/layers/linear.py:123-127).
+QWEN3_32B_TP4_SHARE: List[Tuple[str, int, int]] = [
+    ("qkv", 5120, 2560),
+    ("o_proj", 2048, 5120),
+    ("gate_up", 5120, 12800),
+    ("down", 6400, 5120),
+]
+
 
 def activations(M: int, K: int, gen: torch.Generator) -> torch.Tensor:
     x = torch.randn(M, K, generator=gen)

@@ -64,42 +64,41 @@ def _check_gemm(q, s, q_ref, s_ref, layer, rows, what):
     return y
 
 
-def test_qwen3_32b_chain_m2080_stagewise():
-    """Config 4: hidden 5120, 64 q / 8 kv heads of 128, intermediate 25600,
-    M = 2080 (32 decode tokens + a 2048-token prefill chunk as one GEMM
-    batch).  GEMM shapes qkv 5120->10240, o 8192->5120, gate_up
-    5120->51200, down 25600->5120."""
-    announce("cfg4 chain M=2080")
-    M = 2080
-    gen = torch.Generator().manual_seed(4)
-    qkv_proj = _load(LinearQKVMerged(5120, 128, 64, 8, has_bias=False), gen)
-    o_proj = _load(LinearOProj(64 * 128, 5120, has_bias=False), gen)
-    mlp = GatedMLPW8A8(5120, 25600)
+def _chain_stagewise(tag, M, q_heads, kv_heads, inter, seed):
+    """One decoder layer's GEMM chain (hidden 5120, heads of 128) at M rows:
+    the drop-in layers as a decoder layer calls them, then every stage
+    against the oracle on the GPU's own stage input."""
+    qc = q_heads * 128
+    gen = torch.Generator().manual_seed(seed)
+    qkv_proj = _load(LinearQKVMerged(5120, 128, q_heads, kv_heads, has_bias=False), gen)
+    o_proj = _load(LinearOProj(qc, 5120, has_bias=False), gen)
+    mlp = GatedMLPW8A8(5120, inter)
     _load(mlp.gate_up_proj, gen)
     _load(mlp.down_proj, gen)
-    assert qkv_proj.weight.shape == (10240, 5120) and mlp.gate_up_proj.weight.shape == (51200, 5120)
+    assert qkv_proj.weight.shape == ((q_heads + 2 * kv_heads) * 128, 5120)
+    assert mlp.gate_up_proj.weight.shape == (2 * inter, 5120) and mlp.down_proj.weight.shape == (5120, inter)
     x = activations(M, 5120, gen).to(DEV)
-    rows = _rows(M, 30, 2080)
+    rows = _rows(M, 30, M + seed)
 
     # the drop-in layers, as a decoder layer calls them
     qkv = qkv_proj.forward(x)
-    o = o_proj.forward(qkv[:, : 64 * 128])
+    o = o_proj.forward(qkv[:, :qc])
     out = mlp.forward(o)
     torch.cuda.synchronize()
 
     # staged, against the oracle
-    announce("cfg4 stage qkv")
+    announce(f"{tag} stage qkv")
     q, s, q_ref, s_ref = _check_quant(x, rows)
     y1 = _check_gemm(q, s, q_ref, s_ref, qkv_proj, rows, "qkv")
     assert torch.equal(y1.view(torch.int16), qkv.view(torch.int16))
-    announce("cfg4 stage o_proj")
-    q, s, q_ref, s_ref = _check_quant(y1[:, : 64 * 128], rows)
+    announce(f"{tag} stage o_proj")
+    q, s, q_ref, s_ref = _check_quant(y1[:, :qc], rows)
     y2 = _check_gemm(q, s, q_ref, s_ref, o_proj, rows, "o_proj")
     assert torch.equal(y2.view(torch.int16), o.view(torch.int16))
-    announce("cfg4 stage gate_up")
+    announce(f"{tag} stage gate_up")
     q, s, q_ref, s_ref = _check_quant(y2, rows)
     y3 = _check_gemm(q, s, q_ref, s_ref, mlp.gate_up_proj, rows, "gate_up")
-    announce("cfg4 stage act + down")
+    announce(f"{tag} stage act + down")
     qa, sa, a = act_and_mul_quant(y3, "silu", return_act=True)
     ridx = torch.as_tensor(rows, device=DEV)
     assert rel_l2(f32(a[ridx]), orc.silu_and_mul(f32(y3[ridx]))) <= 1e-3
@@ -109,6 +108,26 @@ def test_qwen3_32b_chain_m2080_stagewise():
     del y3, a
     y4 = _check_gemm(qa, sa, qa_ref, sa_ref, mlp.down_proj, rows, "down")
     assert torch.equal(y4.view(torch.int16), out.view(torch.int16))
+
+
+def test_qwen3_32b_chain_m2080_stagewise():
+    """Config 4: hidden 5120, 64 q / 8 kv heads of 128, intermediate 25600,
+    M = 2080 (32 decode tokens + a 2048-token prefill chunk as one GEMM
+    batch).  GEMM shapes qkv 5120->10240, o 8192->5120, gate_up
+    5120->51200, down 25600->5120."""
+    announce("cfg4 chain M=2080")
+    _chain_stagewise("cfg4", 2080, 64, 8, 25600, 4)
+
+
+def test_qwen3_32b_tp4_share_m2080_stagewise():
+    """One GPU's share of the config-4 layer under tensor parallelism 4 (the
+    reference README's Qwen3-32B TP4 setup), at its real shape: 16 q / 2 kv
+    heads (qkv 5120->2560), o_proj over the rank's 2048-wide K shard
+    (2048->5120), gate_up 5120->12800, down over the 6400-wide K shard
+    (6400->5120).  The row-parallel layers quantize their own K shard, which
+    is what a rank computes before the all-reduce of the bf16 partials."""
+    announce("cfg4 TP4 share chain M=2080")
+    _chain_stagewise("cfg4-tp4", 2080, 16, 2, 6400, 44)
 
 
 @pytest.mark.parametrize("M", [1, 16, 100])
