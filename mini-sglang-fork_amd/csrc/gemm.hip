@@ -155,10 +155,10 @@ int launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
   return kOk;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0>
 int launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
   constexpr int kLds = NSTAGE * (BM + BN) * BK;
-  constexpr auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>;
+  constexpr auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kWAux>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), kLds, st, g);
   return kOk;
@@ -423,14 +423,28 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
     g.tail_split = sp.sp;
     tiles = static_cast<unsigned>(sp.full + sp.tail * sp.sp);
   }
+  // One row tile: every weight tile is read by one block only, so the
+  // 128- and 64-row rings stream the weights with the non-temporal policy.
+  // Measured on MI355X (graph-timed, rotating weight copies, us, default ->
+  // streaming): 64x128 gate_up M=40 48.9 -> 46.0, M=64 48.9-51.3 ->
+  // 46.8-49.7, down M=64 28.0 -> 27.6; 128x128 gate_up M=128 67.6 -> 66.4.
+  // With more row tiles the weight tiles are re-read from L2 and the policy
+  // loses (down M=256 on two 128-row tiles: 50.9 -> 58.3).
+  const bool one_row = g.M <= c.bm;
   int rc;
   switch (cfg) {
     case 0: rc = launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 1: rc = launch_tile3<128, 128, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 2: rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 3: rc = launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 4: rc = launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 5: rc = launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 4:
+      rc = one_row ? launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows, kStreamAux>(g, dim3(tiles), st)
+                   : launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st);
+      break;
+    case 5:
+      rc = one_row ? launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, kStreamAux>(g, dim3(tiles), st)
+                   : launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st);
+      break;
     default: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
   }
   if (rc != kOk || !split) return rc;

@@ -432,7 +432,9 @@ struct TileJob {
 // weight [N = 2I, K]; the epilogue writes act = bf16(act_fn(g) * u) for act
 // columns [n0, n0 + BN/2) of an [rows, I] output (g.ldo = I), g and u the
 // bf16-rounded GEMM outputs, as the separate activation kernel computes it.
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1>
+// kWAux: cache policy of the weight DMA (0, or kStreamAux for weights that
+// only one block reads: a dense grid with a single row tile).
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1, int kWAux = 0>
 __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds, const TileJob& job) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kWaves = WM * WN;
@@ -551,7 +553,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 #pragma unroll
     for (int j = 0; j < kLB; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(base + kStageA + (j * kWaves + wave) * 1024), 16,
-                                               w_doff[j], k0, 0, 0);
+                                               w_doff[j], k0, 0, kWAux);
   };
 
   const int frow = lane & 31, fgrp = lane >> 5;
@@ -868,7 +870,7 @@ __device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, int64_t b) 
   return TileJob{pm * BM, pn * BN, g.W, g.sw, kt_begin, kt_end, BM, split_unit};
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0>
 __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
   // pass only needs the launch stub.
@@ -887,7 +889,7 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
                       0, static_cast<int>(g.K / BK), BM, -1};
     tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
   } else {
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, dense_tile_job<BM, BN, BK>(g, blockIdx.x));
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, kWAux>(g, lds, dense_tile_job<BM, BN, BK>(g, blockIdx.x));
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
