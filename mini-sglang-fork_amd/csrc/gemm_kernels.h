@@ -30,6 +30,8 @@
 // and B use the same mapping, which both cores do by construction.
 #pragma once
 
+#include <type_traits>
+
 #include "mw8_common.h"
 
 namespace mw8 {
@@ -705,6 +707,62 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       };
       const bool odd = (lane & 1) != 0;
       constexpr int kThreads = 64 * kWaves;
+      // The lane's column scales (and bias) are read from the LDS tables
+      // into registers once, its row scales once per fragment row group:
+      // read inside the staging loop, every table read would follow a
+      // staging store to LDS that the compiler cannot prove disjoint from
+      // the tables, and each output pair would wait on its own LDS round
+      // trip.  The bias and routed-weight choices are made outside the loop.
+      float r_sw[kFN], r_bias[kFN];
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        const int c = wn * kWaveN + 32 * j + frow;
+        r_sw[j] = meta_sw[c];
+        r_bias[j] = 0.0f;
+        if constexpr (!Rows::kGrouped) r_bias[j] = meta_bias[c];
+      }
+      auto stage_rows = [&](auto bias_tag, auto routed_tag, int prow0) {
+        constexpr bool kBias = decltype(bias_tag)::value, kRouted = decltype(routed_tag)::value;
+#pragma unroll
+        for (int i = 0; i < kFM; ++i) {
+          float r_sa[16], r_rt[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+            r_sa[v] = meta_sa[r];
+            r_rt[v] = kRouted ? meta_rt[r] : 1.0f;
+          }
+#pragma unroll
+          for (int vp = 0; vp < 8; ++vp) {
+            const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
+            const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
+#pragma unroll
+            for (int j = 0; j < kFN; ++j) {
+              const int c = wn * kWaveN + 32 * j + frow;
+              float t0 = epi_scale(acc[i][j][v0], r_sa[v0], r_sw[j]);
+              float t1 = epi_scale(acc[i][j][v0 + 1], r_sa[v0 + 1], r_sw[j]);
+              if constexpr (kBias) {
+                t0 = t0 + r_bias[j];
+                t1 = t1 + r_bias[j];
+              }
+              if constexpr (kRouted) {
+                t0 = t0 * r_rt[v0];
+                t1 = t1 * r_rt[v0 + 1];
+              }
+              // even lane: row r0, columns (c, c+1); odd lane: row r0+1, columns (c-1, c)
+              const float send = odd ? t0 : t1;
+              const float got = __builtin_bit_cast(
+                  float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+              typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+              const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
+              const int rr = (odd ? r0 + 1 : r0) - prow0, cc = odd ? c - 1 : c;
+              *reinterpret_cast<bf16x2*>(lds + rr * kRowBytes + (spos(rr, cc >> 3) << 4) + (cc & 7) * 2) = pr;
+            }
+          }
+        }
+      };
+      using kYes = std::integral_constant<bool, true>;
+      using kNo = std::integral_constant<bool, false>;
 #pragma unroll
       for (int pass = 0; pass < kStagePasses; ++pass) {
         const int prow0 = pass * kPassRows;
@@ -712,48 +770,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         // reads of the previous pass's rows
         __syncthreads();
         if (wm * kWaveM >= prow0 && wm * kWaveM < prow0 + kPassRows) {  // wave-uniform
-#pragma unroll
-          for (int i = 0; i < kFM; ++i) {
-#pragma unroll
-            for (int vp = 0; vp < 8; ++vp) {
-              const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
-              const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
-              float sa0, sa1, rt0 = 1.0f, rt1 = 1.0f;
-              if constexpr (Rows::kGrouped) {
-                sa0 = meta_sa[r0];
-                sa1 = meta_sa[r0 + 1];
-                rt0 = meta_rt[r0];
-                rt1 = meta_rt[r0 + 1];
-              } else {
-                sa0 = meta_sa[r0];
-                sa1 = meta_sa[r0 + 1];
-              }
-#pragma unroll
-              for (int j = 0; j < kFN; ++j) {
-                const int c = wn * kWaveN + 32 * j + frow;
-                const float swv = meta_sw[c];
-                float t0 = epi_scale(acc[i][j][v0], sa0, swv);
-                float t1 = epi_scale(acc[i][j][v0 + 1], sa1, swv);
-                if constexpr (!Rows::kGrouped) {
-                  if (g.bias) {
-                    t0 = t0 + meta_bias[c];
-                    t1 = t1 + meta_bias[c];
-                  }
-                }
-                if (Rows::kGrouped && g.topk_w) {
-                  t0 = t0 * rt0;
-                  t1 = t1 * rt1;
-                }
-                // even lane: row r0, columns (c, c+1); odd lane: row r0+1, columns (c-1, c)
-                const float send = odd ? t0 : t1;
-                const float got = __builtin_bit_cast(
-                    float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
-                const int rr = (odd ? r0 + 1 : r0) - prow0, cc = odd ? c - 1 : c;
-                *reinterpret_cast<bf16x2*>(lds + rr * kRowBytes + (spos(rr, cc >> 3) << 4) + (cc & 7) * 2) = pr;
-              }
-            }
+          if constexpr (Rows::kGrouped) {
+            if (g.topk_w) stage_rows(kNo{}, kYes{}, prow0);
+            else stage_rows(kNo{}, kNo{}, prow0);
+          } else {
+            if (g.bias) stage_rows(kYes{}, kNo{}, prow0);
+            else stage_rows(kNo{}, kNo{}, prow0);
           }
         }
         __syncthreads();
