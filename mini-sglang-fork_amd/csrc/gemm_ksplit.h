@@ -289,6 +289,12 @@ __global__ __launch_bounds__(64 * KG * WM * WN) void ksplit_gemm_kernel(GemmArgs
       };
       const bool odd = (lane & 1) != 0;
       typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      // Scales and bias of the owned chunks are read from the LDS tables
+      // into registers before the first staging store: read between the
+      // stores, each would wait on its own LDS round trip (the compiler
+      // cannot prove the staging area and the tables disjoint).  The bias
+      // choice is made outside the loop.
+      float r_sa[kQo * 4], r_sw[kQo], r_bias[kQo];
 #pragma unroll
       for (int i = 0; i < kFM; ++i)
 #pragma unroll
@@ -297,25 +303,45 @@ __global__ __launch_bounds__(64 * KG * WM * WN) void ksplit_gemm_kernel(GemmArgs
           for (int h = 0; h < 4; ++h) {
             const int q = (i * kFN + j) * 4 + h;
             if (q / kQo != grp) continue;
+            const int o = q % kQo;
             const int r0 = wm * S::kWaveM + 32 * i + 8 * h + 4 * fgrp, c = wn * S::kWaveN + 32 * j + frow;
-            const float swv = t_sw[c], bv = t_bias[c];
-            float tv[4];
+            r_sw[o] = t_sw[c];
+            r_bias[o] = t_bias[c];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              tv[u] = epi_scale(acc[i][j][4 * h + u], t_sa[r0 + u], swv);
-              if (g.bias) tv[u] = tv[u] + bv;
-            }
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-              const float t0 = tv[2 * p], t1 = tv[2 * p + 1];
-              const float send = odd ? t0 : t1;
-              const float got = __builtin_bit_cast(
-                  float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-              const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
-              const int rr = r0 + 2 * p + (odd ? 1 : 0), cc = odd ? c - 1 : c;
-              *reinterpret_cast<bf16x2*>(stg + rr * kRowB + (((cc >> 3) ^ sf(rr)) << 4) + (cc & 7) * 2) = pr;
-            }
+            for (int u = 0; u < 4; ++u) r_sa[4 * o + u] = t_sa[r0 + u];
           }
+      auto stage = [&](auto bias_tag) {
+        constexpr bool kBias = decltype(bias_tag)::value;
+#pragma unroll
+        for (int i = 0; i < kFM; ++i)
+#pragma unroll
+          for (int j = 0; j < kFN; ++j)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              const int q = (i * kFN + j) * 4 + h;
+              if (q / kQo != grp) continue;
+              const int o = q % kQo;
+              const int r0 = wm * S::kWaveM + 32 * i + 8 * h + 4 * fgrp, c = wn * S::kWaveN + 32 * j + frow;
+              float tv[4];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                tv[u] = epi_scale(acc[i][j][4 * h + u], r_sa[4 * o + u], r_sw[o]);
+                if constexpr (kBias) tv[u] = tv[u] + r_bias[o];
+              }
+#pragma unroll
+              for (int p = 0; p < 2; ++p) {
+                const float t0 = tv[2 * p], t1 = tv[2 * p + 1];
+                const float send = odd ? t0 : t1;
+                const float got = __builtin_bit_cast(
+                    float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+                const bf16x2 pr = odd ? bf16x2{(__bf16)got, (__bf16)t1} : bf16x2{(__bf16)t0, (__bf16)got};
+                const int rr = r0 + 2 * p + (odd ? 1 : 0), cc = odd ? c - 1 : c;
+                *reinterpret_cast<bf16x2*>(stg + rr * kRowB + (((cc >> 3) ^ sf(rr)) << 4) + (cc & 7) * 2) = pr;
+              }
+            }
+      };
+      if (g.bias) stage(std::integral_constant<bool, true>{});
+      else stage(std::integral_constant<bool, false>{});
       __syncthreads();
       // N % 8 == 0 (staged_out), so every column range is whole 8-column chunks
       for (int it = tid; it < BM * kOC; it += S::kThreads) {
