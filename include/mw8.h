@@ -272,6 +272,31 @@ int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W
 int32_t mw8_moe_gemm_sum_supported(int64_t max_sorted, int64_t num_valid, int32_t E);
 
 /*
+ * The two grouped GEMMs of a decode batch without the alignment pass: the
+ * expert rows come straight from the router's topk_ids [num_valid] (one
+ * block per expert lists the pairs routed to it), for batches of at most 16
+ * tokens (num_valid / top_k <= 16) whose top_k experts per token are
+ * distinct, as topk_softmax produces them -- every expert then holds at
+ * most 16 pairs.  Ids outside [0, E) are skipped, as the alignment skips
+ * them.  Results are bit-identical to the aligned forms with 16-row blocks.
+ *
+ * mw8_moe_gemm_topk_w8a8_bf16: GEMM1 as mw8_moe_gemm_w8a8_bf16 (out bf16
+ * [num_valid, N], pair rows; topk_w null or the routed weights).
+ * mw8_moe_gemm_sum_topk_w8a8_bf16: GEMM2 + slot sum as
+ * mw8_moe_gemm_sum_w8a8_bf16 (out bf16 [num_valid / top_k, N]; E <= 256).
+ * Replace moe_align_block_size + fused_moe_kernel (GEMM1), and
+ * fused_moe_kernel (GEMM2) + moe_sum_reduce, for decode batches
+ * (python/minisgl/moe/fused.py:71-89, :192-226).
+ */
+int mw8_moe_gemm_topk_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                                const int32_t* topk_ids, const float* topk_w, int32_t top_k, int64_t num_valid,
+                                int64_t N, int64_t K, int32_t E, void* out, mw8_stream_t stream);
+int mw8_moe_gemm_sum_topk_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                                    const int32_t* topk_ids, const float* topk_w, int32_t top_k,
+                                    int64_t num_valid, int64_t N, int64_t K, int32_t E, void* out,
+                                    mw8_stream_t stream);
+
+/*
  * Gate|up grouped GEMM with the gated activation fused into its epilogue:
  * W int8 [E, N = 2I, K] holds the gate rows then the up rows of each expert;
  * out bf16 [num_valid, I] receives act(g) * u with g, u the bf16 outputs the

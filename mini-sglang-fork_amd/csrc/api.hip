@@ -57,6 +57,10 @@ int moe_gemm_sum_w8a8(const int8_t*, const float*, const int8_t*, const float*, 
                       const int32_t*, const int32_t*, int64_t, const float*, int, int64_t, int64_t,
                       int64_t, int, void*, hipStream_t);
 int moe_gemm_sum_lds_bytes(int64_t, int64_t, int);
+int moe_gemm_topk_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*, const float*, int,
+                       int64_t, int64_t, int64_t, int, void*, int, hipStream_t);
+int moe_gemm_sum_topk_w8a8(const int8_t*, const float*, const int8_t*, const float*, const int32_t*, const float*,
+                           int, int64_t, int64_t, int64_t, int, void*, hipStream_t);
 int rmsnorm_quant_bf16(const void*, void*, const void*, float, int64_t, int64_t, int8_t*, float*, void*,
                        hipStream_t);
 int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, float, int64_t, int64_t, int64_t,
@@ -184,6 +188,21 @@ int mw8_moe_gemm_sum_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W
                                mw8_stream_t stream) {
   MW8_ENTRY(mw8::moe_gemm_sum_w8a8(A, sa, W, sw, sorted_ids, expert_ids, num_post_pad, max_sorted, topk_w,
                                    top_k, num_valid, N, K, E, out, S(stream)));
+}
+
+int mw8_moe_gemm_topk_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                                const int32_t* topk_ids, const float* topk_w, int32_t top_k, int64_t num_valid,
+                                int64_t N, int64_t K, int32_t E, void* out, mw8_stream_t stream) {
+  MW8_ENTRY(mw8::moe_gemm_topk_w8a8(A, sa, W, sw, topk_ids, topk_w, top_k, num_valid, N, K, E, out,
+                                    0 /* bf16 epilogue */, S(stream)));
+}
+
+int mw8_moe_gemm_sum_topk_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                                    const int32_t* topk_ids, const float* topk_w, int32_t top_k,
+                                    int64_t num_valid, int64_t N, int64_t K, int32_t E, void* out,
+                                    mw8_stream_t stream) {
+  MW8_ENTRY(mw8::moe_gemm_sum_topk_w8a8(A, sa, W, sw, topk_ids, topk_w, top_k, num_valid, N, K, E, out,
+                                        S(stream)));
 }
 
 int32_t mw8_moe_gemm_sum_supported(int64_t max_sorted, int64_t num_valid, int32_t E) {

@@ -704,6 +704,23 @@ int launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hip
                          : launch_grouped_epi<kEpiI32>(g, blocks, bm, st);
 }
 
+// Router-id rows (TopkRows): one block per (16 weight rows, expert), the
+// 16-row ring configuration (1 wave, 3 slots).
+int launch_grouped_topk(const GemmArgs& g, int epi, hipStream_t st) {
+  constexpr int kLds = DecodeRing<1, 1, 3>::kLds;
+  const dim3 grid(static_cast<unsigned>((g.N + 15) / 16), static_cast<unsigned>(g.num_experts));
+  if (epi == kEpiBf16) {
+    constexpr auto kern = decode3_gemm_kernel<1, 1, 3, kEpiBf16, TopkRows, 1>;
+    if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(64), kLds, st, g);
+  } else {
+    constexpr auto kern = decode3_gemm_kernel<1, 1, 3, kEpiI32, TopkRows, 1>;
+    if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(64), kLds, st, g);
+  }
+  return kOk;
+}
+
 int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st) {
   return epi == kEpiBf16 ? launch_grouped_small_epi<kEpiBf16>(g, blocks, st)
                          : launch_grouped_small_epi<kEpiI32>(g, blocks, st);
@@ -727,16 +744,23 @@ int moe_gemm_sum_lds_bytes(int64_t max_sorted, int64_t num_valid, int E) {
   return total <= kMoeSumMaxLds ? total : -1;
 }
 
-int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st) {
-  constexpr auto kern = moe_gemm_sum_kernel<kMoeSumWaves, kMoeSumDepth>;
+// topk: units are the experts, listed from the router ids (max_sorted = 16 E).
+int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st, bool topk) {
   const int lds = moe_gemm_sum_lds_bytes(max_sorted, g.num_valid, g.num_experts);
   if (lds < 0)
     return set_error(kErrShape, "moe_gemm_sum: %lld pairs over %lld sorted rows and %d experts exceed the LDS tables",
                      (long long)g.num_valid, (long long)max_sorted, g.num_experts);
-  if (const int rc = set_lds_limit<kern>(kMoeSumMaxLds)) return rc;
   const int64_t cus = device_cus();
-  const int64_t blocks = cus * ((g.N + cus * 8 - 1) / (cus * 8));
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kMoeSumWaves), lds, st, g, max_sorted);
+  const dim3 grid(static_cast<unsigned>(cus * ((g.N + cus * 8 - 1) / (cus * 8))));
+  if (topk) {
+    constexpr auto kern = moe_gemm_sum_kernel<kMoeSumWaves, kMoeSumDepth, true>;
+    if (const int rc = set_lds_limit<kern>(kMoeSumMaxLds)) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kMoeSumWaves), lds, st, g, max_sorted);
+  } else {
+    constexpr auto kern = moe_gemm_sum_kernel<kMoeSumWaves, kMoeSumDepth, false>;
+    if (const int rc = set_lds_limit<kern>(kMoeSumMaxLds)) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kMoeSumWaves), lds, st, g, max_sorted);
+  }
   return kOk;
 }
 

@@ -110,6 +110,15 @@ struct SortedRunRows {
   static constexpr bool kGrouped = true;
   static constexpr bool kRuns = true;
 };
+// An expert's rows taken straight from the router's ids (decode batches of
+// at most 16 tokens whose top-k experts are distinct, so an expert holds at
+// most 16 pairs): block y is expert y, its rows the pairs p with
+// topk_ids[p] == y in ascending order (GemmArgs::sorted_ids carries
+// topk_ids).  No alignment pass.  Decode core only.
+struct TopkRows {
+  static constexpr bool kGrouped = true;
+  static constexpr bool kRuns = false;
+};
 
 // ------------------------------------------------------------------------
 // Large-M tile core
@@ -1203,12 +1212,41 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   static_assert(!Rows::kRuns, "grouped rows: one alignment block per block");
   extern __shared__ __align__(16) unsigned char ring[];
   __shared__ int32_t red[kAcc][64];
+  constexpr bool kTopk = std::is_same<Rows, TopkRows>::value;
+  static_assert(!kTopk || TG == 1, "router-id rows: one 16-row token group");
+  __shared__ int32_t t_pair[kTopk ? 16 : 1];  // router-id rows: the block's pairs
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int8_t* W = g.W;
   const float* sw = g.sw;
   int64_t m0 = 0;  // grouped: first sorted position of the alignment block
-  if constexpr (Rows::kGrouped) {
+  // grouped: pair of row r of token group tg (num_valid for a padding row)
+  auto pair_of = [&](int tg, int r) -> int32_t {
+    if constexpr (kTopk) return t_pair[r];
+    else return g.sorted_ids[m0 + 16 * tg + r];
+  };
+  if constexpr (kTopk) {
+    // wave 0 lists the pairs routed to this block's expert, in ascending
+    // order, by ballots over the router ids
+    const int e = static_cast<int>(blockIdx.y);
+    const int nv = static_cast<int>(g.num_valid);
+    if (wave == 0) {
+      int before = 0;
+      for (int base = 0; base < nv; base += 64) {
+        const int p = base + lane;
+        const bool hit = p < nv && g.sorted_ids[p] == e;
+        const uint64_t m = __ballot(hit);
+        const int rank = before + static_cast<int>(__popcll(m & ((uint64_t{1} << lane) - 1)));
+        if (hit && rank < 16) t_pair[rank] = p;
+        before += static_cast<int>(__popcll(m));
+      }
+      if (lane < 16 && lane >= before) t_pair[lane] = nv;
+    }
+    __syncthreads();
+    if (t_pair[0] >= nv) return;  // no pair routed here (block-uniform)
+    W += static_cast<int64_t>(e) * g.N * g.K;
+    sw += static_cast<int64_t>(e) * g.N;
+  } else if constexpr (Rows::kGrouped) {
     m0 = static_cast<int64_t>(blockIdx.y) * (16 * TG);
     if (m0 >= static_cast<int64_t>(*g.num_post_pad)) return;
     const int e = g.expert_ids[blockIdx.y];
@@ -1254,7 +1292,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   for (int tg = 0; tg < TG; ++tg) {
     int64_t m;
     if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + 16 * tg + r16];
+      const int32_t p = pair_of(tg, r16);
       mok[tg] = p < g.num_valid;
       m = p / g.top_k;
     } else {
@@ -1308,7 +1346,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     if (e >= kAcc * 64 || nl >= rows) continue;
     int32_t arow;
     if constexpr (Rows::kGrouped) {
-      const int32_t p = g.sorted_ids[m0 + 16 * tg + (l & 15)];
+      const int32_t p = pair_of(tg, l & 15);
       if (p >= g.num_valid) continue;
       e_orow[u] = p;
       arow = p / g.top_k;
@@ -1453,7 +1491,13 @@ __host__ __device__ inline MoeSumLds moe_sum_lds(int ring_bytes, int64_t max_sor
 }
 constexpr int kMoeSumSlot = 2048;  // 8 weight rows x 256 K bytes
 
-template <int WAVES, int D>
+// kTopk: the units are the experts themselves, their pairs listed in the
+// prologue from the router ids (GemmArgs::sorted_ids carries topk_ids; at
+// most 16 tokens with distinct experts each, so a unit holds <= 16 pairs);
+// max_sorted is then 16 * E.  A unit's pairs sit in the order of the LDS
+// atomics that place them, which changes no result: each pair's row is its
+// own dot products, and the slot sum reads the pairs by index.
+template <int WAVES, int D, bool kTopk = false>
 __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, int64_t max_sorted) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kOps = 2 + 4;  // vector memory ops per stage: 2 DMA + 4 token loads
@@ -1474,9 +1518,15 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
   const int64_t n0 = g.N * blockIdx.x / gridDim.x;
   const int R = static_cast<int>(g.N * (blockIdx.x + 1) / gridDim.x - n0);
   if (R <= 0) return;  // more blocks than columns (uniform per block)
-  const int64_t npp = *g.num_post_pad;
-  const int n_sorted = static_cast<int>(npp < max_sorted ? npp : max_sorted);
-  const int nb = n_sorted / 16;
+  int n_sorted, nb;
+  if constexpr (kTopk) {
+    n_sorted = 16 * E;
+    nb = E;
+  } else {
+    const int64_t npp = *g.num_post_pad;
+    n_sorted = static_cast<int>(npp < max_sorted ? npp : max_sorted);
+    nb = n_sorted / 16;
+  }
   const bool routed = g.topk_w != nullptr;
 
   // ---- tables, every global load of the prologue issued before the first
@@ -1486,15 +1536,23 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
   constexpr int kSwPer = (8 * kMoeSumMaxExperts + kT - 1) / kT, kExpPer = (kMoeSumMaxSorted / 16 + kT - 1) / kT;
   int32_t v_sid[kSidPer], v_exp[kExpPer];
   float v_sa[kPairPer], v_rw[kPairPer], v_sw[kSwPer];
+  if constexpr (kTopk) {  // the router ids of the pairs, one per thread
 #pragma unroll
-  for (int u = 0; u < kSidPer; ++u) {
-    const int i = u * kT + tid;
-    v_sid[u] = i < n_sorted ? g.sorted_ids[i] : 0;
-  }
+    for (int u = 0; u < kSidPer; ++u) {
+      const int i = u * kT + tid;
+      v_sid[u] = i < nv ? g.sorted_ids[i] : -1;
+    }
+  } else {
 #pragma unroll
-  for (int u = 0; u < kExpPer; ++u) {
-    const int i = u * kT + tid;
-    v_exp[u] = i < nb ? g.expert_ids[i] : -1;
+    for (int u = 0; u < kSidPer; ++u) {
+      const int i = u * kT + tid;
+      v_sid[u] = i < n_sorted ? g.sorted_ids[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kExpPer; ++u) {
+      const int i = u * kT + tid;
+      v_exp[u] = i < nb ? g.expert_ids[i] : -1;
+    }
   }
 #pragma unroll
   for (int u = 0; u < kPairPer; ++u) {
@@ -1507,15 +1565,33 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
     const int i = u * kT + tid, r = i & 7;
     v_sw[u] = (i < E * 8 && r < R) ? g.sw[static_cast<int64_t>(i >> 3) * g.N + n0 + r] : 0.0f;
   }
+  if constexpr (kTopk) {
+    // unit e lists the pairs routed to expert e: counts in t_exp, slots of
+    // t_sid claimed with LDS atomics, then t_exp[e] = e for used units
+    for (int i = tid; i < n_sorted; i += kT) t_sid[i] = nv;
+    for (int i = tid; i < nb; i += kT) t_exp[i] = 0;
+    __syncthreads();
 #pragma unroll
-  for (int u = 0; u < kSidPer; ++u) {
-    const int i = u * kT + tid;
-    if (i < n_sorted) t_sid[i] = v_sid[u];
-  }
+    for (int u = 0; u < kSidPer; ++u) {
+      const int i = u * kT + tid, e = v_sid[u];
+      if (i < nv && e >= 0 && e < E) {
+        const int pos = atomicAdd(&t_exp[e], 1);
+        if (pos < 16) t_sid[e * 16 + pos] = i;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < nb; i += kT) t_exp[i] = t_exp[i] > 0 ? i : -1;
+  } else {
 #pragma unroll
-  for (int u = 0; u < kExpPer; ++u) {
-    const int i = u * kT + tid;
-    if (i < nb) t_exp[i] = v_exp[u];
+    for (int u = 0; u < kSidPer; ++u) {
+      const int i = u * kT + tid;
+      if (i < n_sorted) t_sid[i] = v_sid[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kExpPer; ++u) {
+      const int i = u * kT + tid;
+      if (i < nb) t_exp[i] = v_exp[u];
+    }
   }
 #pragma unroll
   for (int u = 0; u < kPairPer; ++u) {

@@ -10,7 +10,8 @@ namespace mw8 {
 int launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hipStream_t st);
 int launch_grouped_small(const GemmArgs& g, unsigned blocks, int epi, hipStream_t st);
 int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st);
-int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st);
+int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st, bool topk);
+int launch_grouped_topk(const GemmArgs& g, int epi, hipStream_t st);
 int moe_gemm_sum_lds_bytes(int64_t max_sorted, int64_t num_valid, int E);
 
 namespace {
@@ -573,8 +574,66 @@ int moe_gemm_sum_w8a8(const int8_t* A, const float* sa, const int8_t* W, const f
   g.sorted_ids = sorted_ids; g.expert_ids = expert_ids; g.num_post_pad = npp;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.align_bsz = 16;
-  if (const int rc = launch_moe_gemm_sum(g, max_sorted, st)) return rc;
+  if (const int rc = launch_moe_gemm_sum(g, max_sorted, st, false)) return rc;
   return check_launch("moe_gemm_sum");
+}
+
+// ------------------------------------------- router-id rows (no alignment)
+// Decode batches of at most kTopkMaxTokens tokens whose top-k experts are
+// distinct (what topk_softmax produces): every expert then holds at most 16
+// pairs, so the grouped GEMMs list each expert's pairs from topk_ids
+// themselves and the alignment launch disappears.  Ids outside [0, E) are
+// skipped, as the alignment does.
+constexpr int64_t kTopkMaxTokens = 16;
+
+int moe_topk_check(const int8_t* A, const float* sa, const int8_t* W, const float* sw, const int32_t* topk_ids,
+                   int top_k, int64_t num_valid, int64_t N, int64_t K, int E, const void* out, const char* what) {
+  MW8_REQUIRE(A && W && topk_ids && out && (sa == nullptr) == (sw == nullptr), kErrArg, "%s: null pointer", what);
+  MW8_REQUIRE(N > 0 && K > 0 && K % 16 == 0 && K <= (1ll << 17), kErrShape,
+              "%s: need K %% 16 == 0 and K <= 131072 (N=%lld K=%lld)", what, (long long)N, (long long)K);
+  MW8_REQUIRE(top_k >= 1 && E >= 1 && E < 65536 && num_valid >= 0 && num_valid % top_k == 0 &&
+                  num_valid / top_k <= kTopkMaxTokens,
+              kErrShape, "%s: needs at most %lld tokens (top_k=%d num_valid=%lld E=%d)", what,
+              (long long)kTopkMaxTokens, top_k, (long long)num_valid, E);
+  MW8_REQUIRE(aligned16(A) && aligned16(W), kErrAlign, "%s: A and W need 16-byte alignment", what);
+  MW8_REQUIRE((num_valid / top_k + 1) * K < (1ll << 31) && N * K < (1ll << 31), kErrShape,
+              "%s: operands exceed 32-bit buffer offsets", what);
+  return kOk;
+}
+
+int moe_gemm_topk_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw, const int32_t* topk_ids,
+                       const float* topk_w, int top_k, int64_t num_valid, int64_t N, int64_t K, int E, void* out,
+                       int epi, hipStream_t st) {
+  MW8_REQUIRE(epi == kEpiI32 || (sa && sw), kErrArg, "moe_gemm_topk: null scales");
+  if (const int rc = moe_topk_check(A, sa, W, sw, topk_ids, top_k, num_valid, N, K, E, out, "moe_gemm_topk")) return rc;
+  if (num_valid == 0) return kOk;
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
+  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
+  g.sorted_ids = topk_ids; g.expert_ids = nullptr; g.num_post_pad = nullptr;
+  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.align_bsz = 16;
+  if (const int rc = launch_grouped_topk(g, epi, st)) return rc;
+  return check_launch("moe_gemm_topk");
+}
+
+int moe_gemm_sum_topk_w8a8(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
+                           const int32_t* topk_ids, const float* topk_w, int top_k, int64_t num_valid, int64_t N,
+                           int64_t K, int E, void* out, hipStream_t st) {
+  MW8_REQUIRE(sa && sw, kErrArg, "moe_gemm_sum_topk: null scales");
+  if (const int rc = moe_topk_check(A, sa, W, sw, topk_ids, top_k, num_valid, N, K, E, out, "moe_gemm_sum_topk"))
+    return rc;
+  MW8_REQUIRE(moe_gemm_sum_lds_bytes(16 * static_cast<int64_t>(E), num_valid, E) > 0, kErrShape,
+              "moe_gemm_sum_topk: %lld pairs over %d experts exceed the LDS tables", (long long)num_valid, E);
+  if (num_valid == 0) return kOk;
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
+  g.M = 0; g.N = N; g.K = K; g.lda = K; g.ldo = N;
+  g.sorted_ids = topk_ids; g.expert_ids = nullptr; g.num_post_pad = nullptr;
+  g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
+  g.align_bsz = 16;
+  if (const int rc = launch_moe_gemm_sum(g, 16 * static_cast<int64_t>(E), st, true)) return rc;
+  return check_launch("moe_gemm_sum_topk");
 }
 
 }  // namespace mw8

@@ -62,6 +62,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P, _P],
     ),
     "mw8_moe_gemm_sum_supported": (_I32, [_I64, _I64, _I32]),
+    "mw8_moe_gemm_topk_w8a8_bf16": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _P, _P]
+    ),
+    "mw8_moe_gemm_sum_topk_w8a8_bf16": (
+        ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _P, _P]
+    ),
     "mw8_moe_route_quant": (
         ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64, _P, _P, _P, _P, _P]
     ),

@@ -538,6 +538,71 @@ def fused_moe_kernel_sum_w8a8(
     )
 
 
+TOPK_ROWS_MAX_TOKENS = 16  # batches the router-id grouped GEMMs accept
+
+
+def _check_topk_rows(A, A_scale, B, B_scale, topk_ids, topk_weights, pairs_per_row):
+    _on_gpu(A, A_scale, B, B_scale, topk_ids)
+    _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
+    E, N, K = B.shape
+    _need(topk_ids.dtype == torch.int32 and topk_ids.dim() == 2 and topk_ids.is_contiguous(),
+          "topk_ids: int32 [M, k] contiguous")
+    M, k = topk_ids.shape
+    _need(M <= TOPK_ROWS_MAX_TOKENS, f"router-id rows: at most {TOPK_ROWS_MAX_TOKENS} tokens")
+    _need(A.dtype == torch.int8 and A.is_contiguous() and A.shape == (M * k if pairs_per_row else M, K),
+          "A: int8 [M, K] (GEMM1) or [M*k, K] (GEMM2)")
+    _need(A_scale.dtype == torch.float32 and A_scale.shape == (A.shape[0],), "A_scale: fp32 [rows of A]")
+    _need(B_scale.dtype == torch.float32 and B_scale.shape == (E, N) and B_scale.is_contiguous(), "B_scale: fp32 [E, N]")
+    _need(topk_weights is None or (topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()
+                                   and topk_weights.numel() == M * k), "topk_weights: fp32 [M, k]")
+    return E, N, K, M, k
+
+
+def fused_moe_kernel_topk_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    C: torch.Tensor,
+    topk_ids: torch.Tensor,
+    topk_weights: Optional[torch.Tensor],
+) -> None:
+    """GEMM1 of a decode batch (at most 16 tokens, distinct experts per
+    token) with each expert's rows taken from the router ids: C bf16
+    [M*k, N] pair rows, bit-identical to moe_align_block_size(16) +
+    fused_moe_kernel_w8a8 (python/minisgl/moe/fused.py:71-89, :192-205)."""
+    E, N, K, M, k = _check_topk_rows(A, A_scale, B, B_scale, topk_ids, topk_weights, False)
+    _need(C.dtype == torch.bfloat16 and C.is_contiguous() and C.shape == (M * k, N), "C: bf16 [M*k, N]")
+    check(
+        load().mw8_moe_gemm_topk_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(topk_ids), _ptr(topk_weights), k, M * k,
+            N, K, E, _ptr(C), _stream(A),
+        )
+    )
+
+
+def fused_moe_kernel_sum_topk_w8a8(
+    A: torch.Tensor,
+    A_scale: torch.Tensor,
+    B: torch.Tensor,
+    B_scale: torch.Tensor,
+    output: torch.Tensor,
+    topk_ids: torch.Tensor,
+    topk_weights: Optional[torch.Tensor],
+) -> None:
+    """GEMM2 + top-k slot sum of a decode batch with the expert rows taken
+    from the router ids: output bf16 [M, N], bit-identical to
+    fused_moe_kernel_sum_w8a8 over a 16-row alignment."""
+    E, N, K, M, k = _check_topk_rows(A, A_scale, B, B_scale, topk_ids, topk_weights, True)
+    _need(output.dtype == torch.bfloat16 and output.is_contiguous() and output.shape == (M, N), "output: bf16 [M, N]")
+    check(
+        load().mw8_moe_gemm_sum_topk_w8a8_bf16(
+            _ptr(A), _ptr(A_scale), _ptr(B), _ptr(B_scale), _ptr(topk_ids), _ptr(topk_weights), k, M * k,
+            N, K, E, _ptr(output), _stream(A),
+        )
+    )
+
+
 def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
     """out[t] = bf16(sum_i in[t, i]) (python/minisgl/kernel/moe_impl.py:65-98)."""
     _on_gpu(input, output)
@@ -555,6 +620,9 @@ def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
 __all__ = [
     "moe_gemm_sum_supported",
     "fused_moe_kernel_sum_w8a8",
+    "fused_moe_kernel_topk_w8a8",
+    "fused_moe_kernel_sum_topk_w8a8",
+    "TOPK_ROWS_MAX_TOKENS",
     "gemm_workspace",
     "reserve_gemm_workspace",
     "quant_per_token",

@@ -33,7 +33,9 @@ import torch
 from ..kernel import (
     act_and_mul_quant,
     fused_moe_kernel_act_w8a8,
+    fused_moe_kernel_sum_topk_w8a8,
     fused_moe_kernel_sum_w8a8,
+    fused_moe_kernel_topk_w8a8,
     fused_moe_kernel_w8a8,
     moe_align_block_size,
     moe_gemm_sum_supported,
@@ -45,12 +47,22 @@ from ..kernel import (
 )
 from .base import BaseMoeBackend
 
+# Tokens up to which decode batches skip the alignment pass: the grouped
+# GEMMs take each expert's pairs straight from the router ids (the router
+# picks distinct experts per token, so an expert holds at most one pair per
+# token, at most 16 here).  Measured on MI355X at config 3 (layer, us,
+# router-id rows vs the best aligned path): 1 token 27.5 vs 29.6, 2 tokens
+# 32.7 vs 35.0, 4 tokens 44.2 vs 49.1, 5 tokens 49.8 vs 52.5, 8 tokens 58.6
+# vs 62.6, 16 tokens 84.8 vs 87.2.
+TOPK_ROWS_MAX_TOKENS = 16
+
 # Pairs (tokens x top-k) up to which the backend runs router, alignment and
-# hidden quantization as one launch.  The kernel accepts up to 1024 pairs,
-# but one block serialises what the separate kernels spread over the GPU:
-# measured on MI355X at config 3 (layer, us, one launch vs three): 1 token
-# 30.4 vs 32.0, 4 tokens 52.5 vs 54.0, 8 tokens 70.0 vs 70.1, 16 tokens
-# 97.9 vs 96.4, 64 tokens 159.1 vs 133.7.
+# hidden quantization as one launch, where the router-id rows do not apply
+# (more than 256 experts).  The kernel accepts up to 1024 pairs, but one
+# block serialises what the separate kernels spread over the GPU: measured
+# on MI355X at config 3 (layer, us, one launch vs three): 1 token 30.4 vs
+# 32.0, 4 tokens 52.5 vs 54.0, 8 tokens 70.0 vs 70.1, 16 tokens 97.9 vs
+# 96.4, 64 tokens 159.1 vs 133.7.
 PREPARE_MAX_PAIRS = 32
 
 
@@ -172,6 +184,28 @@ def _experts_from_routing(
     return hidden_states
 
 
+def _experts_from_router_ids(
+    hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, topk_ids, activation,
+    apply_router_weight_on_input,
+) -> torch.Tensor:
+    """Steps 4-7 for a decode batch without the alignment: GEMM1 over each
+    expert's pairs listed from topk_ids, activation + requant, GEMM2 with
+    the slot sum writing hidden_states; bit-identical to
+    _experts_from_routing with 16-row blocks."""
+    M, _ = hidden_states.shape
+    _, N, _ = w1.shape
+    k = topk_ids.shape[1]
+    cache1 = torch.empty((M * k, N), dtype=torch.bfloat16, device=hidden_states.device)
+    fused_moe_kernel_topk_w8a8(
+        q_h, s_h, w1, w1_scale, cache1, topk_ids, topk_weights if apply_router_weight_on_input else None
+    )
+    q_a, s_a = act_and_mul_quant(cache1, activation)
+    fused_moe_kernel_sum_topk_w8a8(
+        q_a, s_a, w2, w2_scale, hidden_states, topk_ids, None if apply_router_weight_on_input else topk_weights
+    )
+    return hidden_states
+
+
 class FusedMoeW8A8(BaseMoeBackend):
     def forward(
         self,
@@ -204,6 +238,22 @@ class FusedMoeW8A8(BaseMoeBackend):
         assert w1.dtype == torch.int8 and w2.dtype == torch.int8, "W8A8 MoE takes int8 weights"
         assert w1.is_contiguous() and w2.is_contiguous(), "Expert weights must be contiguous"
         bsz = try_get_optimal_moe_config(w1.shape, w2.shape, topk, M)["BLOCK_SIZE_M"]
+        contiguous = hidden_states.is_contiguous() and gating_output.is_contiguous()
+        if (
+            contiguous
+            and bsz == 16
+            and 0 < M <= TOPK_ROWS_MAX_TOKENS
+            and E <= 256
+            and moe_gemm_sum_supported(16 * E, M * topk, E)
+        ):
+            # decode batch: router + hidden quantization in one launch, then
+            # the grouped GEMMs list each expert's pairs from the router ids
+            # (no alignment launch)
+            topk_weights, topk_ids, q_h, s_h = moe_route_quant(gating_output, hidden_states, topk, renormalize)
+            return _experts_from_router_ids(
+                hidden_states, q_h, s_h, w1, w1_scale, w2, w2_scale, topk_weights, topk_ids, activation,
+                apply_router_weight_on_input,
+            )
         if (
             bsz == 16
             and 0 < M * topk <= PREPARE_MAX_PAIRS

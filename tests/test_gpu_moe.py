@@ -14,7 +14,9 @@ from minisgl_amd.core import Context, reset_global_ctx, set_global_ctx
 from minisgl_amd.kernel import (
     act_and_mul_quant,
     fused_moe_kernel_act_w8a8,
+    fused_moe_kernel_sum_topk_w8a8,
     fused_moe_kernel_sum_w8a8,
+    fused_moe_kernel_topk_w8a8,
     fused_moe_kernel_w8a8,
     fused_moe_kernel_w8a8_i32,
     moe_align_block_size,
@@ -529,6 +531,94 @@ def test_gemm2_sum_fused_ragged(N, K, E, k, M):
     bad = ids_ref.copy()
     bad[::4, -1] = E
     _gemm2_sum_check(bad, w_ref, W, SW, K, k, True, seed=K + 1, invalid=True)
+
+
+def _router_id_rows_check(ids_ref, w_ref, E, k, N1, K1, N2, K2, routed_on_input, seed):
+    """GEMM1 and GEMM2 + slot sum with each expert's rows listed from the
+    router ids, against the same kernels over a 16-row alignment; bit for
+    bit.  Pairs routed to an id outside [0, E) are skipped by both (their
+    GEMM1 rows are not written; they add +0 to their token's sum)."""
+    P = ids_ref.size
+    M = P // k
+    gen = torch.Generator().manual_seed(seed)
+    W1 = torch.randint(-127, 128, (E, N1, K1), generator=gen, dtype=torch.int8).to(DEV)
+    S1 = (torch.rand(E, N1, generator=gen) * 1e-2 + 1e-4).to(DEV)
+    W2 = torch.randint(-127, 128, (E, N2, K2), generator=gen, dtype=torch.int8).to(DEV)
+    S2 = (torch.rand(E, N2, generator=gen) * 1e-2 + 1e-4).to(DEV)
+    qh, sh = quant_per_token(torch.randn(M, K1, generator=gen).to(torch.bfloat16).to(DEV))
+    qa, sa = quant_per_token(torch.randn(P, K2, generator=gen).to(torch.bfloat16).to(DEV))
+    ids = torch.from_numpy(ids_ref.astype(np.int32)).to(DEV)
+    tw = torch.from_numpy(w_ref.astype(np.float32)).to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids, 16, E)
+    valid = torch.from_numpy((ids_ref.reshape(-1) >= 0) & (ids_ref.reshape(-1) < E)).to(DEV)
+    # GEMM1 (routed weight on its input when routed_on_input)
+    c_ref = torch.zeros(P, N1, dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_w8a8(qh, sh, W1, S1, c_ref, tw, sorted_ids, expert_ids, npp, routed_on_input, k, 16, P)
+    c_new = torch.zeros(P, N1, dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_topk_w8a8(qh, sh, W1, S1, c_new, ids, tw if routed_on_input else None)
+    assert torch.equal(c_new[valid].view(torch.int16), c_ref[valid].view(torch.int16))
+    # GEMM2 + slot sum (routed weight here unless it went on GEMM1's input)
+    rw = None if routed_on_input else tw
+    o_ref = torch.full((M, N2), float("nan"), dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_sum_w8a8(qa, sa, W2, S2, o_ref, rw, sorted_ids, expert_ids, npp, k, P)
+    o_new = torch.full((M, N2), float("nan"), dtype=torch.bfloat16, device=DEV)
+    fused_moe_kernel_sum_topk_w8a8(qa, sa, W2, S2, o_new, ids, rw)
+    assert torch.equal(o_new.view(torch.int16), o_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize(
+    "M,E,k,on_input",
+    [(1, 128, 8, False), (5, 128, 8, False), (16, 128, 8, True), (16, 8, 2, False), (9, 64, 6, False),
+     (16, 256, 8, False), (12, 3, 3, True)],
+)
+def test_router_id_rows_equal_aligned(M, E, k, on_input):
+    """Decode batches (<= 16 tokens, distinct experts per token): the
+    router-id forms of GEMM1 and of GEMM2 + slot sum against the aligned
+    forms, with config-3-like sizes scaled down; then a quarter of the
+    pairs routed outside [0, E); then 16 tokens all routed to expert 0
+    (an expert holding the 16 pairs the router-id rows allow)."""
+    announce(f"router-id rows M={M} E={E} k={k} on_input={on_input}")
+    rng = np.random.default_rng(M * 1000 + E)
+    ids_ref = np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int64)
+    w_ref = rng.random((M, k)).astype(np.float32)
+    _router_id_rows_check(ids_ref, w_ref, E, k, 384, 1024, 512, 192, on_input, seed=M + E)
+    bad = ids_ref.copy()
+    bad[::4, 0] = E
+    bad[1::4, -1] = -1
+    _router_id_rows_check(bad, w_ref, E, k, 384, 1024, 512, 192, on_input, seed=M + E + 1)
+    if E >= k and M == 16:
+        full = ids_ref.copy()
+        for t in range(M):
+            others = [e for e in full[t] if e != 0][: k - 1]
+            full[t] = np.array([0] + others)
+        assert (full == 0).sum() == 16
+        _router_id_rows_check(full, w_ref, E, k, 384, 1024, 512, 192, on_input, seed=M + E + 2)
+
+
+@pytest.mark.parametrize("M", [1, 4, 5, 8, 16])
+@pytest.mark.parametrize("on_input", [False, True])
+def test_moe_layer_router_id_rows_equal_aligned(M, on_input):
+    """MoELayer at config 3 for 1-16 tokens: the default path (router-id
+    rows, no alignment launch) against the same layer forced onto the
+    aligned paths (the one-launch preparation up to 4 tokens, router +
+    alignment above); bit for bit."""
+    import minisgl_amd.moe.fused as fused_mod
+
+    announce(f"moe layer router-id rows M={M} on_input={on_input}")
+    c = moe_case(M, seed=M + 23)
+    layer = _moe_layer(c, apply_router_weight_on_input=on_input)
+    set_global_ctx(Context(moe_backend=create_moe_backend("fused_w8a8")))
+    outs = []
+    orig = fused_mod.TOPK_ROWS_MAX_TOKENS
+    try:
+        for limit in (orig, 0):
+            fused_mod.TOPK_ROWS_MAX_TOKENS = limit
+            outs.append(layer.forward(c["hidden"].to(DEV), c["logits"].to(DEV)).clone())
+        torch.cuda.synchronize()
+    finally:
+        fused_mod.TOPK_ROWS_MAX_TOKENS = orig
+        reset_global_ctx()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
 
 
 @pytest.mark.parametrize("M", [4, 16, 256, 4096])
