@@ -273,17 +273,19 @@ int32_t mw8_moe_gemm_sum_supported(int64_t max_sorted, int64_t num_valid, int32_
 
 /*
  * The two grouped GEMMs of a decode batch without the alignment pass: the
- * expert rows come straight from the router's topk_ids [num_valid] (one
- * block per expert lists the pairs routed to it), for batches of at most 16
- * tokens (num_valid / top_k <= 16) whose top_k experts per token are
- * distinct, as topk_softmax produces them -- every expert then holds at
- * most 16 pairs.  Ids outside [0, E) are skipped, as the alignment skips
- * them.  Results are bit-identical to the aligned forms with 16-row blocks.
+ * expert rows come straight from the router's topk_ids [num_valid] (blocks
+ * list the pairs routed to their expert, in units of 16), for batches of at
+ * most 48 tokens (num_valid / top_k <= 48) whose top_k experts per token
+ * are distinct, as topk_softmax produces them -- every expert then holds at
+ * most one pair per token, ceil(tokens / 16) units.  Ids outside [0, E) are
+ * skipped, as the alignment skips them.  Results are bit-identical to the
+ * aligned forms with 16-row blocks.
  *
  * mw8_moe_gemm_topk_w8a8_bf16: GEMM1 as mw8_moe_gemm_w8a8_bf16 (out bf16
  * [num_valid, N], pair rows; topk_w null or the routed weights).
  * mw8_moe_gemm_sum_topk_w8a8_bf16: GEMM2 + slot sum as
- * mw8_moe_gemm_sum_w8a8_bf16 (out bf16 [num_valid / top_k, N]; E <= 256).
+ * mw8_moe_gemm_sum_w8a8_bf16 (out bf16 [num_valid / top_k, N]; E <= 256 and
+ * E * ceil(tokens / 16) <= 384).
  * Replace moe_align_block_size + fused_moe_kernel (GEMM1), and
  * fused_moe_kernel (GEMM2) + moe_sum_reduce, for decode batches
  * (python/minisgl/moe/fused.py:71-89, :192-226).

@@ -708,7 +708,7 @@ int launch_grouped_tile(const GemmArgs& g, unsigned blocks, int bm, int epi, hip
 // 16-row ring configuration (1 wave, 3 slots).
 int launch_grouped_topk(const GemmArgs& g, int epi, hipStream_t st) {
   constexpr int kLds = DecodeRing<1, 1, 3>::kLds;
-  const dim3 grid(static_cast<unsigned>((g.N + 15) / 16), static_cast<unsigned>(g.num_experts));
+  const dim3 grid(static_cast<unsigned>((g.N + 15) / 16), static_cast<unsigned>(g.num_experts * g.topk_units));
   if (epi == kEpiBf16) {
     constexpr auto kern = decode3_gemm_kernel<1, 1, 3, kEpiBf16, TopkRows, 1>;
     if (const int rc = set_lds_limit<kern>(kLds)) return rc;

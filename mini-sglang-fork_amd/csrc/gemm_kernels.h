@@ -73,6 +73,8 @@ struct GemmArgs {
   // blocks behind expert_ids / num_post_pad (the tile height BM is a
   // multiple of it)
   int32_t align_bsz;
+  // router-id rows (TopkRows): 16-pair units per expert (ceil(tokens / 16))
+  int32_t topk_units;
 };
 
 __device__ __forceinline__ uint16_t epi_bf16(int32_t acc, float sa, float sw, const uint16_t* bias,
@@ -110,10 +112,11 @@ struct SortedRunRows {
   static constexpr bool kGrouped = true;
   static constexpr bool kRuns = true;
 };
-// An expert's rows taken straight from the router's ids (decode batches of
-// at most 16 tokens whose top-k experts are distinct, so an expert holds at
-// most 16 pairs): block y is expert y, its rows the pairs p with
-// topk_ids[p] == y in ascending order (GemmArgs::sorted_ids carries
+// An expert's rows taken straight from the router's ids (decode batches
+// whose top-k experts are distinct per token, so an expert holds at most
+// one pair per token): block y is unit y % U of expert y / U (U =
+// GemmArgs::topk_units), its rows the pairs 16 u .. 16 u + 15 of the pairs
+// p with topk_ids[p] == e in ascending order (GemmArgs::sorted_ids carries
 // topk_ids).  No alignment pass.  Decode core only.
 struct TopkRows {
   static constexpr bool kGrouped = true;
@@ -1226,9 +1229,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     else return g.sorted_ids[m0 + 16 * tg + r];
   };
   if constexpr (kTopk) {
-    // wave 0 lists the pairs routed to this block's expert, in ascending
+    // wave 0 lists this unit's pairs of the block's expert, in ascending
     // order, by ballots over the router ids
-    const int e = static_cast<int>(blockIdx.y);
+    const int U = g.topk_units;
+    const int e = static_cast<int>(blockIdx.y) / U, r0 = 16 * (static_cast<int>(blockIdx.y) % U);
     const int nv = static_cast<int>(g.num_valid);
     if (wave == 0) {
       int before = 0;
@@ -1236,11 +1240,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
         const int p = base + lane;
         const bool hit = p < nv && g.sorted_ids[p] == e;
         const uint64_t m = __ballot(hit);
-        const int rank = before + static_cast<int>(__popcll(m & ((uint64_t{1} << lane) - 1)));
-        if (hit && rank < 16) t_pair[rank] = p;
+        const int rank = before + static_cast<int>(__popcll(m & ((uint64_t{1} << lane) - 1))) - r0;
+        if (hit && rank >= 0 && rank < 16) t_pair[rank] = p;
         before += static_cast<int>(__popcll(m));
       }
-      if (lane < 16 && lane >= before) t_pair[lane] = nv;
+      if (lane < 16 && lane >= before - r0) t_pair[lane] = nv;
     }
     __syncthreads();
     if (t_pair[0] >= nv) return;  // no pair routed here (block-uniform)
@@ -1491,12 +1495,13 @@ __host__ __device__ inline MoeSumLds moe_sum_lds(int ring_bytes, int64_t max_sor
 }
 constexpr int kMoeSumSlot = 2048;  // 8 weight rows x 256 K bytes
 
-// kTopk: the units are the experts themselves, their pairs listed in the
-// prologue from the router ids (GemmArgs::sorted_ids carries topk_ids; at
-// most 16 tokens with distinct experts each, so a unit holds <= 16 pairs);
-// max_sorted is then 16 * E.  A unit's pairs sit in the order of the LDS
-// atomics that place them, which changes no result: each pair's row is its
-// own dot products, and the slot sum reads the pairs by index.
+// kTopk: units of 16 pairs per expert (U = GemmArgs::topk_units of them,
+// unit e * U + u), the pairs listed in the prologue from the router ids
+// (GemmArgs::sorted_ids carries topk_ids; distinct experts per token, so an
+// expert holds at most 16 U pairs); max_sorted is then 16 * E * U.  Pairs
+// sit in the order of the LDS atomics that place them, which changes no
+// result: each pair's row is its own dot products, and the slot sum reads
+// the pairs by index.
 template <int WAVES, int D, bool kTopk = false>
 __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, int64_t max_sorted) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1520,8 +1525,8 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
   if (R <= 0) return;  // more blocks than columns (uniform per block)
   int n_sorted, nb;
   if constexpr (kTopk) {
-    n_sorted = 16 * E;
-    nb = E;
+    nb = E * g.topk_units;
+    n_sorted = 16 * nb;
   } else {
     const int64_t npp = *g.num_post_pad;
     n_sorted = static_cast<int>(npp < max_sorted ? npp : max_sorted);
@@ -1533,6 +1538,7 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
   // LDS store (one round trip; the host bounds the sizes to one pass)
   constexpr int kT = 64 * WAVES;
   constexpr int kSidPer = (kMoeSumMaxSorted + kT - 1) / kT, kPairPer = (kMoeSumMaxPairs + kT - 1) / kT;
+  static_assert(!kTopk || kMoeSumMaxSorted / 16 <= kT, "router-id units: one per thread");
   constexpr int kSwPer = (8 * kMoeSumMaxExperts + kT - 1) / kT, kExpPer = (kMoeSumMaxSorted / 16 + kT - 1) / kT;
   int32_t v_sid[kSidPer], v_exp[kExpPer];
   float v_sa[kPairPer], v_rw[kPairPer], v_sw[kSwPer];
@@ -1566,21 +1572,26 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_sum_kernel(GemmArgs g, in
     v_sw[u] = (i < E * 8 && r < R) ? g.sw[static_cast<int64_t>(i >> 3) * g.N + n0 + r] : 0.0f;
   }
   if constexpr (kTopk) {
-    // unit e lists the pairs routed to expert e: counts in t_exp, slots of
-    // t_sid claimed with LDS atomics, then t_exp[e] = e for used units
+    // the pairs of expert e fill units e * U .. e * U + U - 1: per-expert
+    // counts in t_exp[0, E), slots of t_sid claimed with LDS atomics, then
+    // t_exp[unit] = e for the units that hold pairs (nb <= kT: one unit per
+    // thread, its count read before any unit entry is written)
+    const int U = g.topk_units;
     for (int i = tid; i < n_sorted; i += kT) t_sid[i] = nv;
-    for (int i = tid; i < nb; i += kT) t_exp[i] = 0;
+    for (int i = tid; i < E; i += kT) t_exp[i] = 0;
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kSidPer; ++u) {
       const int i = u * kT + tid, e = v_sid[u];
       if (i < nv && e >= 0 && e < E) {
         const int pos = atomicAdd(&t_exp[e], 1);
-        if (pos < 16) t_sid[e * 16 + pos] = i;
+        if (pos < 16 * U) t_sid[(e * U + pos / 16) * 16 + pos % 16] = i;
       }
     }
     __syncthreads();
-    for (int i = tid; i < nb; i += kT) t_exp[i] = t_exp[i] > 0 ? i : -1;
+    const int cnt = tid < nb ? t_exp[tid / U] : 0;
+    __syncthreads();
+    if (tid < nb) t_exp[tid] = cnt > 16 * (tid % U) ? tid / U : -1;
   } else {
 #pragma unroll
     for (int u = 0; u < kSidPer; ++u) {

@@ -580,18 +580,24 @@ int moe_gemm_sum_w8a8(const int8_t* A, const float* sa, const int8_t* W, const f
 
 // ------------------------------------------- router-id rows (no alignment)
 // Decode batches of at most kTopkMaxTokens tokens whose top-k experts are
-// distinct (what topk_softmax produces): every expert then holds at most 16
-// pairs, so the grouped GEMMs list each expert's pairs from topk_ids
-// themselves and the alignment launch disappears.  Ids outside [0, E) are
-// skipped, as the alignment does.
-constexpr int64_t kTopkMaxTokens = 16;
+// distinct per token (what topk_softmax produces): an expert then holds at
+// most one pair per token, U = ceil(tokens / 16) units of 16, so the grouped
+// GEMMs list each expert's pairs from topk_ids themselves and the
+// alignment launch disappears.  Ids outside [0, E) are skipped, as the
+// alignment does.
+constexpr int64_t kTopkMaxTokens = 48;
+
+int topk_units(int64_t num_valid, int top_k) {
+  const int64_t tokens = num_valid / top_k;
+  return static_cast<int>(tokens <= 16 ? 1 : (tokens + 15) / 16);
+}
 
 int moe_topk_check(const int8_t* A, const float* sa, const int8_t* W, const float* sw, const int32_t* topk_ids,
                    int top_k, int64_t num_valid, int64_t N, int64_t K, int E, const void* out, const char* what) {
   MW8_REQUIRE(A && W && topk_ids && out && (sa == nullptr) == (sw == nullptr), kErrArg, "%s: null pointer", what);
   MW8_REQUIRE(N > 0 && K > 0 && K % 16 == 0 && K <= (1ll << 17), kErrShape,
               "%s: need K %% 16 == 0 and K <= 131072 (N=%lld K=%lld)", what, (long long)N, (long long)K);
-  MW8_REQUIRE(top_k >= 1 && E >= 1 && E < 65536 && num_valid >= 0 && num_valid % top_k == 0 &&
+  MW8_REQUIRE(top_k >= 1 && E >= 1 && E <= 16384 && num_valid >= 0 && num_valid % top_k == 0 &&
                   num_valid / top_k <= kTopkMaxTokens,
               kErrShape, "%s: needs at most %lld tokens (top_k=%d num_valid=%lld E=%d)", what,
               (long long)kTopkMaxTokens, top_k, (long long)num_valid, E);
@@ -613,6 +619,7 @@ int moe_gemm_topk_w8a8(const int8_t* A, const float* sa, const int8_t* W, const 
   g.sorted_ids = topk_ids; g.expert_ids = nullptr; g.num_post_pad = nullptr;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.align_bsz = 16;
+  g.topk_units = topk_units(num_valid, top_k);
   if (const int rc = launch_grouped_topk(g, epi, st)) return rc;
   return check_launch("moe_gemm_topk");
 }
@@ -623,8 +630,10 @@ int moe_gemm_sum_topk_w8a8(const int8_t* A, const float* sa, const int8_t* W, co
   MW8_REQUIRE(sa && sw, kErrArg, "moe_gemm_sum_topk: null scales");
   if (const int rc = moe_topk_check(A, sa, W, sw, topk_ids, top_k, num_valid, N, K, E, out, "moe_gemm_sum_topk"))
     return rc;
-  MW8_REQUIRE(moe_gemm_sum_lds_bytes(16 * static_cast<int64_t>(E), num_valid, E) > 0, kErrShape,
-              "moe_gemm_sum_topk: %lld pairs over %d experts exceed the LDS tables", (long long)num_valid, E);
+  const int U = topk_units(num_valid, top_k);
+  MW8_REQUIRE(moe_gemm_sum_lds_bytes(16 * static_cast<int64_t>(E) * U, num_valid, E) > 0, kErrShape,
+              "moe_gemm_sum_topk: %lld pairs over %d experts (%d units each) exceed the LDS tables",
+              (long long)num_valid, E, U);
   if (num_valid == 0) return kOk;
   GemmArgs g{};
   g.A = A; g.sa = sa; g.W = W; g.sw = sw; g.bias = nullptr; g.out = out;
@@ -632,7 +641,8 @@ int moe_gemm_sum_topk_w8a8(const int8_t* A, const float* sa, const int8_t* W, co
   g.sorted_ids = topk_ids; g.expert_ids = nullptr; g.num_post_pad = nullptr;
   g.topk_w = topk_w; g.num_valid = num_valid; g.top_k = top_k; g.num_experts = E;
   g.align_bsz = 16;
-  if (const int rc = launch_moe_gemm_sum(g, 16 * static_cast<int64_t>(E), st, true)) return rc;
+  g.topk_units = U;
+  if (const int rc = launch_moe_gemm_sum(g, 16 * static_cast<int64_t>(E) * U, st, true)) return rc;
   return check_launch("moe_gemm_sum_topk");
 }
 

@@ -538,7 +538,7 @@ def fused_moe_kernel_sum_w8a8(
     )
 
 
-TOPK_ROWS_MAX_TOKENS = 16  # batches the router-id grouped GEMMs accept
+TOPK_ROWS_MAX_TOKENS = 48  # batches the router-id grouped GEMMs accept
 
 
 def _check_topk_rows(A, A_scale, B, B_scale, topk_ids, topk_weights, pairs_per_row):
@@ -567,7 +567,7 @@ def fused_moe_kernel_topk_w8a8(
     topk_ids: torch.Tensor,
     topk_weights: Optional[torch.Tensor],
 ) -> None:
-    """GEMM1 of a decode batch (at most 16 tokens, distinct experts per
+    """GEMM1 of a decode batch (at most 48 tokens, distinct experts per
     token) with each expert's rows taken from the router ids: C bf16
     [M*k, N] pair rows, bit-identical to moe_align_block_size(16) +
     fused_moe_kernel_w8a8 (python/minisgl/moe/fused.py:71-89, :192-205)."""

@@ -53,7 +53,10 @@ from .base import BaseMoeBackend
 # token, at most 16 here).  Measured on MI355X at config 3 (layer, us,
 # router-id rows vs the best aligned path): 1 token 27.5 vs 29.6, 2 tokens
 # 32.7 vs 35.0, 4 tokens 44.2 vs 49.1, 5 tokens 49.8 vs 52.5, 8 tokens 58.6
-# vs 62.6, 16 tokens 84.8 vs 87.2.
+# vs 62.6, 16 tokens 84.8 vs 87.2.  The kernels take up to 48 tokens (two or
+# three 16-pair units per expert), but there every block's scan of the
+# router ids costs more than the alignment launch: 17 / 32 / 48 tokens 90.6
+# / 111.3 / 131.6 vs 88.6 / 107.3 / 112.3.
 TOPK_ROWS_MAX_TOKENS = 16
 
 # Pairs (tokens x top-k) up to which the backend runs router, alignment and
@@ -244,7 +247,7 @@ class FusedMoeW8A8(BaseMoeBackend):
             and bsz == 16
             and 0 < M <= TOPK_ROWS_MAX_TOKENS
             and E <= 256
-            and moe_gemm_sum_supported(16 * E, M * topk, E)
+            and moe_gemm_sum_supported(16 * E * -(-M // 16), M * topk, E)
         ):
             # decode batch: router + hidden quantization in one launch, then
             # the grouped GEMMs list each expert's pairs from the router ids

@@ -569,14 +569,15 @@ def _router_id_rows_check(ids_ref, w_ref, E, k, N1, K1, N2, K2, routed_on_input,
 @pytest.mark.parametrize(
     "M,E,k,on_input",
     [(1, 128, 8, False), (5, 128, 8, False), (16, 128, 8, True), (16, 8, 2, False), (9, 64, 6, False),
-     (16, 256, 8, False), (12, 3, 3, True)],
+     (16, 256, 8, False), (12, 3, 3, True), (17, 128, 8, False), (32, 128, 8, True), (48, 128, 8, False),
+     (40, 8, 2, False), (32, 192, 6, False)],
 )
 def test_router_id_rows_equal_aligned(M, E, k, on_input):
-    """Decode batches (<= 16 tokens, distinct experts per token): the
-    router-id forms of GEMM1 and of GEMM2 + slot sum against the aligned
-    forms, with config-3-like sizes scaled down; then a quarter of the
-    pairs routed outside [0, E); then 16 tokens all routed to expert 0
-    (an expert holding the 16 pairs the router-id rows allow)."""
+    """Decode batches (<= 48 tokens, distinct experts per token, units of 16
+    pairs per expert): the router-id forms of GEMM1 and of GEMM2 + slot sum
+    against the aligned forms, with config-3-like sizes scaled down; then a
+    quarter of the pairs routed outside [0, E); then every token routed to
+    expert 0 (an expert filling all its units)."""
     announce(f"router-id rows M={M} E={E} k={k} on_input={on_input}")
     rng = np.random.default_rng(M * 1000 + E)
     ids_ref = np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int64)
@@ -586,19 +587,19 @@ def test_router_id_rows_equal_aligned(M, E, k, on_input):
     bad[::4, 0] = E
     bad[1::4, -1] = -1
     _router_id_rows_check(bad, w_ref, E, k, 384, 1024, 512, 192, on_input, seed=M + E + 1)
-    if E >= k and M == 16:
+    if M in (16, 32, 48):
         full = ids_ref.copy()
         for t in range(M):
             others = [e for e in full[t] if e != 0][: k - 1]
             full[t] = np.array([0] + others)
-        assert (full == 0).sum() == 16
+        assert (full == 0).sum() == M
         _router_id_rows_check(full, w_ref, E, k, 384, 1024, 512, 192, on_input, seed=M + E + 2)
 
 
-@pytest.mark.parametrize("M", [1, 4, 5, 8, 16])
+@pytest.mark.parametrize("M", [1, 4, 5, 8, 16, 17, 32, 48])
 @pytest.mark.parametrize("on_input", [False, True])
 def test_moe_layer_router_id_rows_equal_aligned(M, on_input):
-    """MoELayer at config 3 for 1-16 tokens: the default path (router-id
+    """MoELayer at config 3 for 1-48 tokens: the default path (router-id
     rows, no alignment launch) against the same layer forced onto the
     aligned paths (the one-launch preparation up to 4 tokens, router +
     alignment above); bit for bit."""
