@@ -169,11 +169,11 @@ def test_argument_errors_return_codes(lib):
               FAKE_A, None) == E["MW8_ERR_SHAPE"] and b"LDS" in lib.mw8_last_error()
     assert gs(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, FAKE_C, FAKE_C, 2944, None, 8, 1024, 2048, 760, 128,
               FAKE_A, None) == E["MW8_ERR_SHAPE"]  # K % 16 != 0
-    # router-id grouped GEMMs: more than 16 tokens, null ids, pairs not a multiple of top_k,
-    # one scale without the other, K % 16 != 0, more experts than the slot-sum tables hold
+    # router-id grouped GEMMs: more than 48 tokens, null ids, pairs not a multiple of top_k,
+    # one scale without the other, K % 16 != 0, more expert units than the slot-sum tables hold
     for fn in (lib.mw8_moe_gemm_topk_w8a8_bf16, lib.mw8_moe_gemm_sum_topk_w8a8_bf16):
-        assert fn(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 17 * 8, 2048, 768, 128, FAKE_A,
-                  None) == E["MW8_ERR_SHAPE"] and b"16 tokens" in lib.mw8_last_error()
+        assert fn(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 49 * 8, 2048, 768, 128, FAKE_A,
+                  None) == E["MW8_ERR_SHAPE"] and b"48 tokens" in lib.mw8_last_error()
         assert fn(FAKE_A, FAKE_B, FAKE_A, FAKE_B, None, None, 8, 128, 2048, 768, 128, FAKE_A,
                   None) == E["MW8_ERR_ARG"]
         assert fn(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 100, 2048, 768, 128, FAKE_A,
@@ -185,6 +185,8 @@ def test_argument_errors_return_codes(lib):
         assert fn(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 0, 2048, 768, 128, FAKE_A, None) == 0
     assert lib.mw8_moe_gemm_sum_topk_w8a8_bf16(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 128, 2048,
                                               768, 400, FAKE_A, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_moe_gemm_sum_topk_w8a8_bf16(FAKE_A, FAKE_B, FAKE_A, FAKE_B, FAKE_C, None, 8, 48 * 8, 2048,
+                                              768, 129, FAKE_A, None) == E["MW8_ERR_SHAPE"]  # 3 x 129 > 384 units
     # empty problems are no-ops
     assert lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 0, 8, 64, None, 0, None) == 0
 
