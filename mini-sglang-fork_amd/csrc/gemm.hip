@@ -412,7 +412,11 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   const int cfg = select_tile_cfg(g.M, g.N, g.K);
   if (cfg >= kNumRingCfgs) return dispatch_ksplit<EPI>(cfg - kNumRingCfgs, g, st);
   const TileCfg c = kTileCfgs[cfg];
-  unsigned tiles = static_cast<unsigned>(((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn));
+  const int64_t tiles64 = ((g.M + c.bm - 1) / c.bm) * ((g.N + c.bn - 1) / c.bn);
+  // the tile walk computes in 32 bits; a K split multiplies the blocks by at most 16
+  MW8_REQUIRE(tiles64 <= (int64_t{1} << 26), kErrShape, "gemm: %lld output tiles exceed the tile walk's range",
+              (long long)tiles64);
+  unsigned tiles = static_cast<unsigned>(tiles64);
   // K split (ring configurations): needs the caller's workspace
   const SplitPlan sp = plan_split(g.M, g.N, g.K, c);
   const bool split = sp.sp > 1 && ws != nullptr && ws_bytes >= sp.ws;

@@ -160,23 +160,28 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
+// The tile arithmetic below is 32-bit: the host launches at most 2^31
+// blocks and tiles, and a 64-bit division by a runtime value expands into
+// a long scalar routine that every block would run before its first load.
+
 // Tile index t of the grouped raster -> (pid_m, pid_n).
-__device__ __forceinline__ void tile_of_index(int64_t t, int64_t tiles_m, int64_t tiles_n,
+__device__ __forceinline__ void tile_of_index(uint32_t t, uint32_t tiles_m, uint32_t tiles_n,
                                               int64_t& pid_m, int64_t& pid_n) {
-  const int64_t per_group = kGroupM * tiles_n;
-  const int64_t group = t / per_group;
-  const int64_t first_m = group * kGroupM;
-  const int64_t gsize = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
-  const int64_t in_group = t % per_group;
-  pid_m = first_m + in_group % gsize;
-  pid_n = in_group / gsize;
+  const uint32_t per_group = kGroupM * tiles_n;
+  const uint32_t group = t / per_group;
+  const uint32_t first_m = group * kGroupM;
+  const uint32_t gsize = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const uint32_t in_group = t - group * per_group;
+  const uint32_t col = in_group / gsize;
+  pid_m = first_m + (in_group - col * gsize);
+  pid_n = col;
 }
 
 // Block b (b < count) -> tile index in [0, count): XCD b % 8 gets a
 // contiguous range of tile indices.
-__device__ __forceinline__ int64_t xcd_tile_index(int64_t b, int64_t count) {
-  const int64_t xcd = b % kXcds, local = b / kXcds;
-  const int64_t base = count / kXcds, rem = count % kXcds;
+__device__ __forceinline__ uint32_t xcd_tile_index(uint32_t b, uint32_t count) {
+  const uint32_t xcd = b % kXcds, local = b / kXcds;
+  const uint32_t base = count / kXcds, rem = count % kXcds;
   return xcd * base + (xcd < rem ? xcd : rem) + local;
 }
 
@@ -188,15 +193,15 @@ __device__ __forceinline__ int64_t xcd_tile_index(int64_t b, int64_t count) {
 // stay consecutive in the raster.  Measured on MI355X (graph-timed, weights
 // from HBM): gate_up M=8192 1312-1324 -> 1259-1273 us, down M=8192 637 ->
 // 628 us.
-__device__ __forceinline__ int64_t xcd_tile_index_rot(int64_t b, int64_t count) {
-  const int64_t xcd = b % kXcds, local = b / kXcds;
-  const int64_t base = count / kXcds, rem = count % kXcds;
-  const int64_t n_x = base + (xcd < rem ? 1 : 0);  // blocks b with b % 8 == xcd
-  const int64_t start = xcd * base + (xcd < rem ? xcd : rem);
+__device__ __forceinline__ uint32_t xcd_tile_index_rot(uint32_t b, uint32_t count) {
+  const uint32_t xcd = b % kXcds, local = b / kXcds;
+  const uint32_t base = count / kXcds, rem = count % kXcds;
+  const uint32_t n_x = base + (xcd < rem ? 1 : 0);  // blocks b with b % 8 == xcd
+  const uint32_t start = xcd * base + (xcd < rem ? xcd : rem);
   return start + (local + xcd * n_x / kXcds) % n_x;
 }
 
-__device__ __forceinline__ void tile_of_block(int64_t b, int64_t tiles_m, int64_t tiles_n,
+__device__ __forceinline__ void tile_of_block(uint32_t b, uint32_t tiles_m, uint32_t tiles_n,
                                               int64_t& pid_m, int64_t& pid_n) {
   tile_of_index(xcd_tile_index_rot(b, tiles_m * tiles_n), tiles_m, tiles_n, pid_m, pid_n);
 }
@@ -884,19 +889,20 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 // tail tile u / tail_split (an int32 partial tile); without a split, block
 // b owns tile tile_of_block(b).
 template <int BM, int BN, int BK>
-__device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, int64_t b) {
-  const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+__device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, uint32_t b) {
+  const uint32_t tm = static_cast<uint32_t>((g.M + BM - 1) / BM), tn = static_cast<uint32_t>((g.N + BN - 1) / BN);
   int64_t pm, pn, split_unit = -1;
   int kt_begin = 0, kt_end = static_cast<int>(g.K / BK);
   if (g.tail_split > 1) {
-    if (b < g.full_tiles) {
-      tile_of_index(xcd_tile_index_rot(b, g.full_tiles), tm, tn, pm, pn);
+    const uint32_t full = static_cast<uint32_t>(g.full_tiles), ts = static_cast<uint32_t>(g.tail_split);
+    if (b < full) {
+      tile_of_index(xcd_tile_index_rot(b, full), tm, tn, pm, pn);
     } else {
-      split_unit = b - g.full_tiles;
-      tile_of_index(g.full_tiles + split_unit / g.tail_split, tm, tn, pm, pn);
-      const int64_t sp = split_unit % g.tail_split, nkt = g.K / BK;
-      kt_begin = static_cast<int>(nkt * sp / g.tail_split);
-      kt_end = static_cast<int>(nkt * (sp + 1) / g.tail_split);
+      const uint32_t u = b - full, tile = u / ts, sp = u - tile * ts, nkt = static_cast<uint32_t>(g.K / BK);
+      split_unit = u;
+      tile_of_index(full + tile, tm, tn, pm, pn);
+      kt_begin = static_cast<int>(nkt * sp / ts);
+      kt_end = static_cast<int>(nkt * (sp + 1) / ts);
     }
   } else {
     tile_of_block(b, tm, tn, pm, pn);
