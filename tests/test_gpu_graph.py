@@ -116,12 +116,13 @@ def _moe_inputs(bs, gen):
     return activations(bs, 2048, gen), logits
 
 
-@pytest.mark.parametrize("bs", [1, 8, 64, 256])
+@pytest.mark.parametrize("bs", [1, 8, 16, 64, 256])
 def test_moe_layer_graph_replay(bs):
     """MoELayer.forward (config-3 experts: E 128, top-8, H 2048, I 768)
-    captured at a decode batch size: the path for the size (one-launch
-    preparation at bs 1, router + quant at 8, 16-row blocks at 64, 64-row
-    tiles at 256) replayed on fresh router logits and hidden states."""
+    captured at a decode batch size: the path for the size (up to 16 tokens
+    the grouped GEMMs list each expert's pairs from the router ids, GEMM2
+    summing the top-k slots; 16-row alignment blocks at 64; 64-row tiles at
+    256) replayed on fresh router logits and hidden states."""
     announce(f"moe graph replay bs={bs}")
     gen = torch.Generator().manual_seed(1000 + bs)
     E, H, I = 128, 2048, 768
