@@ -155,10 +155,13 @@ int launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
   return kOk;
 }
 
+// 128-byte K stages hold two 64-byte substeps of v_mfma_i32_16x16x64_i8
+// (the int8 MFMA with the higher power-limited rate on MI355X); 64-byte
+// stages run v_mfma_i32_32x32x32_i8 (two 32-byte substeps).
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0>
 int launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
   constexpr int kLds = NSTAGE * (BM + BN) * BK;
-  constexpr auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kWAux>;
+  constexpr auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kWAux, BK == 128 ? 16 : 32>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), kLds, st, g);
   return kOk;

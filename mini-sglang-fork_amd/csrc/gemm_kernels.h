@@ -373,6 +373,12 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 // together by one phase of a fragment load on distinct 16-byte bank groups:
 //   BK = 64 : f(r) = ((r >> 1) ^ (r >> 3)) & 3
 //   BK = 128: f(r) = (r & 7) ^ ((r >> 3) & 1)
+// The 16x16x64 fragments of a 128-byte stage read chunk 2 g + s (lane group
+// g = l / 16, substep s) rather than 4 s + g: with lane groups on chunks
+// c..c+3 the reads of 8 waves per CU moved 136 B/clk per CU through LDS on
+// MI355X, with groups on chunks 0,2,4,6 (or 1,3,5,7) 212-244 B/clk, as the
+// 32x32x32 fragments do (an in-bounds ds_read_b128 probe; the MFMA sums
+// over all of a stage's K bytes, so any chunk order serves A and B alike).
 template <int BK>
 __device__ __forceinline__ int swz_f(int row) {
   if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
@@ -436,6 +442,39 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The int8 MFMA a ring tile is built from (MF = output rows and columns of
+// one instruction).  Both take 16 K-bytes per lane as A and B operands:
+//   MF = 32: v_mfma_i32_32x32x32_i8, lane l feeds row / column l % 32 with
+//            K group l / 32 (2 groups = 32 K bytes per instruction); D reg v
+//            (16) holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.
+//   MF = 16: v_mfma_i32_16x16x64_i8, lane l feeds row / column l % 16 with
+//            K group l / 16 (4 groups = 64 K bytes); D reg v (4) holds row
+//            4 (l / 16) + v, column l % 16.
+// On MI355X the two run at the same nominal rate (4.98 POPS with constant
+// operands), but on random int8 data the part is power-limited and the
+// 16x16x64 form sustains 3.92-3.99 POPS against 3.35-3.41 for 32x32x32
+// (register-only loops, 4 waves per SIMD).
+template <int MF>
+struct MfmaI8;
+template <>
+struct MfmaI8<32> {
+  using Acc = v16i;
+  static constexpr int kK = 32, kV = 16, kGroups = 2;
+  static __device__ __forceinline__ int row(int lane, int v) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaI8<16> {
+  using Acc = v4i;
+  static constexpr int kK = 64, kV = 4, kGroups = 4;
+  static __device__ __forceinline__ int row(int lane, int v) { return 4 * (lane >> 4) + v; }
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+};
+
 // One BM x BN output tile over K stages [kt_begin, kt_end) of the ring core.
 struct TileJob {
   int64_t m0, n0;     // first (sorted) row and first output column
@@ -453,12 +492,16 @@ struct TileJob {
 // bf16-rounded GEMM outputs, as the separate activation kernel computes it.
 // kWAux: cache policy of the weight DMA (0, or kStreamAux for weights that
 // only one block reads: a dense grid with a single row tile).
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1, int kWAux = 0>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1, int kWAux = 0,
+          int MF = 32>
 __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds, const TileJob& job) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  using Mf = MfmaI8<MF>;
+  using Acc = typename Mf::Acc;
   constexpr int kWaves = WM * WN;
   constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
-  constexpr int kFM = kWaveM / 32, kFN = kWaveN / 32;
+  constexpr int kFM = kWaveM / MF, kFN = kWaveN / MF;
+  constexpr int kV = Mf::kV;  // accumulator registers per fragment and lane
   constexpr int kChunks = BK / 16;                 // 16-byte chunks per LDS row
   constexpr int kRowsPerInst = 1024 / BK;           // rows one 1 KB DMA instruction fills
   constexpr int kStageA = BM * BK, kStageB = BN * BK, kStage = kStageA + kStageB;
@@ -466,6 +509,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   constexpr int kL = kLA + kLB;                     // DMA instructions per wave per stage
   static_assert(BK == 64 || BK == 128, "BK");
   static_assert((kWaves == 4 || kWaves == 8 || kWaves == 16) && kFM >= 1 && kFN >= 1, "shape");
+  static_assert(BK / Mf::kK >= 2, "the fragment pipeline runs two k-substeps per stage");
   static_assert(kLA >= 1 && kLB >= 1 && kLA * kRowsPerInst * kWaves == BM &&
                 kLB * kRowsPerInst * kWaves == BN, "DMA split");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
@@ -575,29 +619,29 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
                                                w_doff[j], k0, 0, kWAux);
   };
 
-  const int frow = lane & 31, fgrp = lane >> 5;
-  int a_off[kFM], b_off[kFN];  // row byte offsets of this lane's fragment rows
+  const int frow = lane & (MF - 1), fgrp = lane / MF;
+  int a_off[kFM], b_off[kFN];  // tile rows of this lane's fragment rows
 #pragma unroll
-  for (int i = 0; i < kFM; ++i) a_off[i] = wm * kWaveM + 32 * i + frow;
+  for (int i = 0; i < kFM; ++i) a_off[i] = wm * kWaveM + MF * i + frow;
 #pragma unroll
-  for (int j = 0; j < kFN; ++j) b_off[j] = wn * kWaveN + 32 * j + frow;
+  for (int j = 0; j < kFN; ++j) b_off[j] = wn * kWaveN + MF * j + frow;
   v4i fa[2][kFM], fb[2][kFN];
-  // fragments of k-substep ks (32 K bytes) of stage kt into register set ks & 1
+  // fragments of k-substep ks (Mf::kK K bytes) of stage kt into register set ks & 1
   auto read_frags = [&](int kt, int ks) {
     const unsigned char* la = lds + (kt % NSTAGE) * kStage;
     const unsigned char* lb = la + kStageA;
-    const int ch = 2 * ks + fgrp;
+    const int ch = Mf::kGroups * ks + fgrp;
 #pragma unroll
     for (int i = 0; i < kFM; ++i) fa[ks & 1][i] = *reinterpret_cast<const v4i*>(la + swz_lds<BK>(a_off[i], ch));
 #pragma unroll
     for (int j = 0; j < kFN; ++j) fb[ks & 1][j] = *reinterpret_cast<const v4i*>(lb + swz_lds<BK>(b_off[j], ch));
   };
 
-  v16i acc[kFM][kFN];
+  Acc acc[kFM][kFN];
 #pragma unroll
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < kFN; ++j) acc[i][j] = Acc{0};
   // Run tiles: the sorted positions of a run are real pairs up to the
   // expert's padding, which ends it, so the real rows of this wave's range
   // form a prefix of length live_w; 32-row fragments past it (padding or
@@ -616,13 +660,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   auto mfmas = [&](int set) {
 #pragma unroll
     for (int i = 0; i < kFM; ++i) {
-      if (Rows::kRuns && 32 * i >= live_w) break;
+      if (Rows::kRuns && MF * i >= live_w) break;
 #pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < kFN; ++j) acc[i][j] = Mf::mma(fa[set][i], fb[set][j], acc[i][j]);
     }
   };
-  constexpr int kSub = BK / 32;  // k-substeps per stage (2 or 4)
+  constexpr int kSub = BK / Mf::kK;  // k-substeps per stage (2 or 4)
 
   // prologue: stages 0 .. NSTAGE-1 in flight, stage 0 landed, its fragments read
 #pragma unroll
@@ -646,6 +689,71 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   }
   wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
   raw_barrier();
+  if constexpr (MF == 16) {
+    // Two 64-byte substeps per stage.  The B fragments roll: fragment j of
+    // the next substep is read as soon as the kFM MFMAs of column block j
+    // have been issued.  The A fragments are double-buffered by substep
+    // (2 kFM + kFN registers of 16 bytes instead of 2 (kFM + kFN)), or,
+    // where that would not fit beside the accumulators (kASets == 1), held
+    // once and re-read during the last column block, each right after its
+    // last MFMA.  The next stage's fragments are read after the barrier
+    // that follows its landing, in the middle of the stage's substep-1
+    // MFMAs.
+    static_assert(kSub == 2, "16x16x64 ring: 128-byte stages");
+    constexpr int kASets = 4 * (2 * kFM + kFN) + 4 * kFM * kFN > 200 ? 1 : 2;
+    auto read_a1 = [&](int kt, int ks, int set, int i) {
+      const unsigned char* la = lds + (kt % NSTAGE) * kStage;
+      fa[set][i] = *reinterpret_cast<const v4i*>(la + swz_lds<BK>(a_off[i], 2 * fgrp + ks));
+    };
+    auto read_a = [&](int kt, int ks, int set) {
+#pragma unroll
+      for (int i = 0; i < kFM; ++i) read_a1(kt, ks, set, i);
+    };
+    auto read_b = [&](int kt, int ks, int j) {
+      const unsigned char* lb = lds + (kt % NSTAGE) * kStage + kStageA;
+      fb[0][j] = *reinterpret_cast<const v4i*>(lb + swz_lds<BK>(b_off[j], 2 * fgrp + ks));
+    };
+    // MFMAs of column block j on A set `set`; with one A set, the last
+    // column block re-reads A fragment i of substep (nkt, nks) after its
+    // MFMA (nkt < 0: no re-read)
+    auto col = [&](int set, int j, int nkt, int nks) {
+#pragma unroll
+      for (int i = 0; i < kFM; ++i) {
+        if (Rows::kRuns && MF * i >= live_w) break;
+        acc[i][j] = Mf::mma(fa[kASets == 1 ? 0 : set][i], fb[0][j], acc[i][j]);
+        if (kASets == 1 && j == kFN - 1 && nkt >= 0) read_a1(nkt, nks, 0, i);
+      }
+    };
+    read_a(0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) read_b(0, 0, j);
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      if constexpr (kASets == 2) read_a(kt, 1, 1);
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        col(0, j, kt, 1);
+        read_b(kt, 1, j);
+      }
+      const int later = nk - 2 - kt;  // stages after kt+1 already issued
+      wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
+      raw_barrier();
+      if constexpr (kASets == 2) read_a(kt + 1, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        col(1, j, kt + 1, 0);
+        read_b(kt + 1, 0, j);
+      }
+      if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+    }
+    if constexpr (kASets == 2) read_a(nk - 1, 1, 1);
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      col(0, j, nk - 1, 1);
+      read_b(nk - 1, 1, j);
+    }
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) col(1, j, -1, 0);
+  } else {
   read_frags(0, 0);
   read_frags(0, 1);
 
@@ -678,6 +786,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   }
   mfmas(kSub & 1);
   mfmas((kSub - 1) & 1);
+  }  // MF == 32
 
   if constexpr (!Rows::kGrouped) {
     if (split_unit >= 0) {  // split-tail unit: raw int32 partial tile, rows/cols unmasked
@@ -685,10 +794,10 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 #pragma unroll
       for (int i = 0; i < kFM; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+        for (int v = 0; v < kV; ++v) {
+          const int r = wm * kWaveM + MF * i + Mf::row(lane, v);
 #pragma unroll
-          for (int j = 0; j < kFN; ++j) pt[r * BN + wn * kWaveN + 32 * j + frow] = acc[i][j][v];
+          for (int j = 0; j < kFN; ++j) pt[r * BN + wn * kWaveN + MF * j + frow] = acc[i][j][v];
         }
       return;
     }
@@ -713,7 +822,13 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
     if (g.staged_out) {
       constexpr int kRowBytes = BN * 2;
       constexpr int kChunksRow = BN / 8;
-      auto sf = [](int r) { return 4 * ((r & 1) | (((r >> 2) & 1) << 1)); };
+      // MF = 32: one word-store instruction covers rows R, R+1, R+4, R+5 (64
+      // bytes each); MF = 16: rows R, R+1, R+4, R+5, R+8, R+9, R+12, R+13
+      // (32 bytes each).  sf spreads them over the 256 bytes of the banks.
+      auto sf = [](int r) {
+        if constexpr (MF == 32) return 4 * ((r & 1) | (((r >> 2) & 1) << 1));
+        else return 2 * ((r & 1) | (((r >> 2) & 3) << 1));
+      };
       auto spos = [&](int r, int c) {
         if constexpr (kChunksRow % 16 == 0) {
           return c ^ sf(r);
@@ -733,7 +848,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       float r_sw[kFN], r_bias[kFN];
 #pragma unroll
       for (int j = 0; j < kFN; ++j) {
-        const int c = wn * kWaveN + 32 * j + frow;
+        const int c = wn * kWaveN + MF * j + frow;
         r_sw[j] = meta_sw[c];
         r_bias[j] = 0.0f;
         if constexpr (!Rows::kGrouped) r_bias[j] = meta_bias[c];
@@ -742,20 +857,20 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         constexpr bool kBias = decltype(bias_tag)::value, kRouted = decltype(routed_tag)::value;
 #pragma unroll
         for (int i = 0; i < kFM; ++i) {
-          float r_sa[16], r_rt[16];
+          float r_sa[kV], r_rt[kV];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+          for (int v = 0; v < kV; ++v) {
+            const int r = wm * kWaveM + MF * i + Mf::row(lane, v);
             r_sa[v] = meta_sa[r];
             r_rt[v] = kRouted ? meta_rt[r] : 1.0f;
           }
 #pragma unroll
-          for (int vp = 0; vp < 8; ++vp) {
-            const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's 16
-            const int r0 = wm * kWaveM + 32 * i + 8 * (v0 >> 2) + 4 * fgrp + (v0 & 3);
+          for (int vp = 0; vp < kV / 2; ++vp) {
+            const int v0 = 2 * vp;  // rows v0, v0 + 1 of this lane's kV (adjacent rows)
+            const int r0 = wm * kWaveM + MF * i + Mf::row(lane, v0);
 #pragma unroll
             for (int j = 0; j < kFN; ++j) {
-              const int c = wn * kWaveN + 32 * j + frow;
+              const int c = wn * kWaveN + MF * j + frow;
               float t0 = epi_scale(acc[i][j][v0], r_sa[v0], r_sw[j]);
               float t1 = epi_scale(acc[i][j][v0 + 1], r_sa[v0 + 1], r_sw[j]);
               if constexpr (kBias) {
@@ -845,12 +960,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
     }
   }
 
-  // ---- epilogue: lane holds column (lane & 31) of each 32x32 block
+  // ---- epilogue: lane holds column frow of each MF x MF fragment
 #pragma unroll
   for (int i = 0; i < kFM; ++i) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = wm * kWaveM + 32 * i + 8 * (v >> 2) + 4 * fgrp + (v & 3);
+    for (int v = 0; v < kV; ++v) {
+      const int r = wm * kWaveM + MF * i + Mf::row(lane, v);
       int64_t orow, arow;
       bool rvalid;
       float routed = 1.0f;
@@ -869,7 +984,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       const float sa = epi_bf16_out(EPI) ? g.sa[arow] : 0.0f;
 #pragma unroll
       for (int j = 0; j < kFN; ++j) {
-        const int64_t n = n0 + wn * kWaveN + 32 * j + frow;
+        const int64_t n = n0 + wn * kWaveN + MF * j + frow;
         if (n >= g.N) continue;
         const int32_t a = acc[i][j][v];
         if constexpr (epi_bf16_out(EPI)) {
@@ -910,7 +1025,7 @@ __device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, uint32_t b)
   return TileJob{pm * BM, pn * BN, g.W, g.sw, kt_begin, kt_end, BM, split_unit};
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0, int MF = 32>
 __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
   // pass only needs the launch stub.
@@ -927,9 +1042,10 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
     if (e < 0 || e >= g.num_experts) return;
     const TileJob job{m0, n0, g.W + static_cast<int64_t>(e) * g.N * g.K, g.sw + static_cast<int64_t>(e) * g.N,
                       0, static_cast<int>(g.K / BK), BM, -1};
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows>(g, lds, job);
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, 0, MF>(g, lds, job);
   } else {
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, kWAux>(g, lds, dense_tile_job<BM, BN, BK>(g, blockIdx.x));
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, kWAux, MF>(g, lds,
+                                                                 dense_tile_job<BM, BN, BK>(g, blockIdx.x));
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
