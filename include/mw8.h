@@ -178,8 +178,10 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
  * loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference.  The K split's partial tiles go to a static 64 MiB device
  * array of the library (held on every device it runs on until the process
- * ends); a shape whose split would need more returns MW8_ERR_WORKSPACE
- * (none does on a 256-CU MI355X: the bound is mw8_gemm_workspace_max_bytes).
+ * ends, whether or not this entry is called); a split that would need more
+ * is not taken and those tiles run whole, as mw8_gemm_w8a8_bf16 does with a
+ * short workspace (none needs more on a 256-CU MI355X: the bound is
+ * mw8_gemm_workspace_max_bytes).
  * Calls on one device share that array: calls that overlap on one device
  * (concurrent streams) race.  Allocates nothing; results equal
  * mw8_gemm_w8a8_bf16's bit for bit.

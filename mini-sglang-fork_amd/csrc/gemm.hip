@@ -551,7 +551,8 @@ int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int
 // The K split's int32 partial tiles live in a file-scope device array of
 // kScratchBytes (64 MiB: the workspace bound of a 256-CU MI355X, 256 slots
 // x one 256x256 int32 tile), held by every device the library runs on
-// until the process ends.  Host code never passes the array's name to a
+// until the process ends.  A split that would need more (a part with more
+// CUs) is not taken: those tiles run whole, as with a short workspace.  Host code never passes the array's name to a
 // kernel (on the host it is only a stand-in for the symbol): the device
 // address comes from hipGetSymbolAddress, taken once per device with that
 // device current, and only that address is used.  Every call on a device
@@ -584,12 +585,6 @@ int gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W, co
                            const void* bias, void* y, int64_t M, int64_t N, int64_t K, hipStream_t st) {
   void* ws = nullptr;
   if (const int rc = scratch_of_current_device(&ws)) return rc;
-  if (M > 0 && N > 0 && K > 0) {
-    const size_t need = gemm_workspace_bytes(M, N, K);
-    MW8_REQUIRE(need <= kScratchBytes, kErrWorkspace,
-                "gemm_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of scratch, above the static %zu",
-                (long long)M, (long long)N, (long long)K, need, kScratchBytes);
-  }
   return gemm_common(A, sa, W, sw, bias, y, M, N, K, ws, kScratchBytes, st, kEpiBf16);
 }
 

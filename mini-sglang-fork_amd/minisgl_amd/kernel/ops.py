@@ -36,6 +36,12 @@ def _on_gpu(*ts: Optional[torch.Tensor]) -> None:
             raise ValueError("the W8A8 HIP path needs GPU tensors (no CPU fallback)")
 
 
+def _same_device(*ts: Optional[torch.Tensor]) -> None:
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) > 1:
+        raise ValueError(f"the W8A8 HIP path needs every tensor on one device, got {sorted(map(str, devs))}")
+
+
 # ----------------------------------------------------------------- workspace
 _WORKSPACE: Dict[torch.device, torch.Tensor] = {}
 
@@ -193,6 +199,9 @@ def rmsnorm_strided(x: torch.Tensor, weight: torch.Tensor, eps: float, out: Opti
     H = x.shape[-1]
     _need(weight.dtype == torch.bfloat16 and weight.shape == (H,) and weight.is_contiguous(), "weight: bf16 [H]")
     gx, go = _row_groups(x), _row_groups(out)
+    if gx is not None and out.is_contiguous():
+        # a contiguous out holds x's row groups back to back: g * (inner * H) + i * H
+        go = (gx[0], gx[1], gx[1] * H)
     if gx is None or go is None or gx[:2] != go[:2] or H % 8 or gx[2] % 8 or go[2] % 8:
         return False
     if x.data_ptr() % 16 or out.data_ptr() % 16:
@@ -516,7 +525,8 @@ def fused_moe_kernel_sum_w8a8(
     16-row alignment blocks: output bf16 [M, N] receives, bit for bit, what
     fused_moe_kernel_w8a8 (pair rows, routed weight from ``topk_weights``
     unless None) followed by moe_sum_reduce writes (python/minisgl/moe/fused.py:212-226)."""
-    _on_gpu(A, A_scale, B, B_scale, output)
+    _on_gpu(A, A_scale, B, B_scale, output, topk_weights, sorted_token_ids, expert_ids, num_tokens_post_padded)
+    _same_device(A, A_scale, B, B_scale, output, topk_weights, sorted_token_ids, expert_ids, num_tokens_post_padded)
     _need(A.dtype == torch.int8 and A.dim() == 2 and A.is_contiguous(), "A: int8 [M*k, K]")
     _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
     E, N, K = B.shape
@@ -538,17 +548,18 @@ def fused_moe_kernel_sum_w8a8(
     )
 
 
-TOPK_ROWS_MAX_TOKENS = 48  # batches the router-id grouped GEMMs accept
+TOPK_ROWS_KERNEL_MAX_TOKENS = 48  # batches the router-id grouped GEMM kernels accept
 
 
 def _check_topk_rows(A, A_scale, B, B_scale, topk_ids, topk_weights, pairs_per_row):
-    _on_gpu(A, A_scale, B, B_scale, topk_ids)
+    _on_gpu(A, A_scale, B, B_scale, topk_ids, topk_weights)
+    _same_device(A, A_scale, B, B_scale, topk_ids, topk_weights)
     _need(B.dtype == torch.int8 and B.dim() == 3 and B.is_contiguous(), "B: int8 [E, N, K]")
     E, N, K = B.shape
     _need(topk_ids.dtype == torch.int32 and topk_ids.dim() == 2 and topk_ids.is_contiguous(),
           "topk_ids: int32 [M, k] contiguous")
     M, k = topk_ids.shape
-    _need(M <= TOPK_ROWS_MAX_TOKENS, f"router-id rows: at most {TOPK_ROWS_MAX_TOKENS} tokens")
+    _need(M <= TOPK_ROWS_KERNEL_MAX_TOKENS, f"router-id rows: at most {TOPK_ROWS_KERNEL_MAX_TOKENS} tokens")
     _need(A.dtype == torch.int8 and A.is_contiguous() and A.shape == (M * k if pairs_per_row else M, K),
           "A: int8 [M, K] (GEMM1) or [M*k, K] (GEMM2)")
     _need(A_scale.dtype == torch.float32 and A_scale.shape == (A.shape[0],), "A_scale: fp32 [rows of A]")
@@ -622,7 +633,7 @@ __all__ = [
     "fused_moe_kernel_sum_w8a8",
     "fused_moe_kernel_topk_w8a8",
     "fused_moe_kernel_sum_topk_w8a8",
-    "TOPK_ROWS_MAX_TOKENS",
+    "TOPK_ROWS_KERNEL_MAX_TOKENS",
     "gemm_workspace",
     "reserve_gemm_workspace",
     "quant_per_token",

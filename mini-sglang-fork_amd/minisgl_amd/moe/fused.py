@@ -44,6 +44,7 @@ from ..kernel import (
     moe_sum_reduce,
     quant_per_token,
     topk_softmax,
+    TOPK_ROWS_KERNEL_MAX_TOKENS,
 )
 from .base import BaseMoeBackend
 
@@ -58,6 +59,7 @@ from .base import BaseMoeBackend
 # router ids costs more than the alignment launch: 17 / 32 / 48 tokens 90.6
 # / 111.3 / 131.6 vs 88.6 / 107.3 / 112.3.
 TOPK_ROWS_MAX_TOKENS = 16
+assert TOPK_ROWS_MAX_TOKENS <= TOPK_ROWS_KERNEL_MAX_TOKENS, "the dispatch limit stays within the kernels' limit"
 
 # Pairs (tokens x top-k) up to which the backend runs router, alignment and
 # hidden quantization as one launch, where the router-id rows do not apply

@@ -102,6 +102,8 @@ def test_workspace_bound_and_tuning_counts(lib):
     plans for 256 CUs."""
     mx = lib.mw8_gemm_workspace_max_bytes()
     assert mx == 256 * 256 * 256 * 4
+    # the allocation-free entry's static scratch (64 MiB) holds every plan on 256 CUs
+    assert mx <= 64 << 20
     counts = [lib.mw8_tuning_count(k) for k in range(4)]
     assert counts == [8, 12, 2, 3] and lib.mw8_tuning_count(9) == 0
     worst = 0

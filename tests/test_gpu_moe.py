@@ -26,6 +26,7 @@ from minisgl_amd.kernel import (
     moe_sum_reduce,
     quant_per_token,
     topk_softmax,
+    TOPK_ROWS_KERNEL_MAX_TOKENS,
 )
 from minisgl_amd.layers import MoELayer
 from minisgl_amd.moe import create_moe_backend
@@ -533,6 +534,33 @@ def test_gemm2_sum_fused_ragged(N, K, E, k, M):
     _gemm2_sum_check(bad, w_ref, W, SW, K, k, True, seed=K + 1, invalid=True)
 
 
+def test_moe_gemm_sum_rejects_host_tensors():
+    """Every tensor argument of the fused GEMM2 + slot sum is checked for the
+    device before any launch: a host (CPU) routed weight, sorted-id list,
+    block-expert list or padded count raises ValueError (its host pointer
+    never reaches a kernel)."""
+    E, N, K, k, M = 8, 64, 256, 2, 4
+    P = M * k
+    gen = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, E, (M, k), generator=gen, dtype=torch.int32)
+    q, s = quant_per_token(torch.randn(P, K, generator=gen).to(torch.bfloat16).to(DEV))
+    W = torch.randint(-127, 128, (E, N, K), generator=gen, dtype=torch.int8).to(DEV)
+    SW = torch.rand(E, N, generator=gen).to(DEV)
+    tw = torch.rand(M, k, generator=gen).to(DEV)
+    sorted_ids, expert_ids, npp = moe_align_block_size(ids.to(DEV), 16, E)
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device=DEV)
+    args = dict(topk_weights=tw, sorted_token_ids=sorted_ids, expert_ids=expert_ids, num_tokens_post_padded=npp)
+    fused_moe_kernel_sum_w8a8(q, s, W, SW, out, top_k=k, num_valid_tokens=P, **args)
+    torch.cuda.synchronize()
+    for name in args:
+        bad = dict(args, **{name: args[name].cpu()})
+        with pytest.raises(ValueError):
+            fused_moe_kernel_sum_w8a8(q, s, W, SW, out, top_k=k, num_valid_tokens=P, **bad)
+    with pytest.raises(ValueError):
+        fused_moe_kernel_topk_w8a8(q[:M], s[:M], W, SW, torch.zeros(P, N, dtype=torch.bfloat16, device=DEV),
+                                   ids.to(DEV), tw.cpu())
+
+
 def _router_id_rows_check(ids_ref, w_ref, E, k, N1, K1, N2, K2, routed_on_input, seed):
     """GEMM1 and GEMM2 + slot sum with each expert's rows listed from the
     router ids, against the same kernels over a 16-row alignment; bit for
@@ -599,10 +627,11 @@ def test_router_id_rows_equal_aligned(M, E, k, on_input):
 @pytest.mark.parametrize("M", [1, 4, 5, 8, 16, 17, 32, 48])
 @pytest.mark.parametrize("on_input", [False, True])
 def test_moe_layer_router_id_rows_equal_aligned(M, on_input):
-    """MoELayer at config 3 for 1-48 tokens: the default path (router-id
-    rows, no alignment launch) against the same layer forced onto the
-    aligned paths (the one-launch preparation up to 4 tokens, router +
-    alignment above); bit for bit."""
+    """MoELayer at config 3 for 1-48 tokens: the router-id rows (no
+    alignment launch; the dispatch limit raised to the kernels' limit of 48
+    tokens, so that 17-48 tokens take them too) against the same layer
+    forced onto the aligned paths (the one-launch preparation up to 4
+    tokens, router + alignment above); bit for bit."""
     import minisgl_amd.moe.fused as fused_mod
 
     announce(f"moe layer router-id rows M={M} on_input={on_input}")
@@ -612,7 +641,7 @@ def test_moe_layer_router_id_rows_equal_aligned(M, on_input):
     outs = []
     orig = fused_mod.TOPK_ROWS_MAX_TOKENS
     try:
-        for limit in (orig, 0):
+        for limit in (TOPK_ROWS_KERNEL_MAX_TOKENS, 0):
             fused_mod.TOPK_ROWS_MAX_TOKENS = limit
             outs.append(layer.forward(c["hidden"].to(DEV), c["logits"].to(DEV)).clone())
         torch.cuda.synchronize()

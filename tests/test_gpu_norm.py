@@ -133,8 +133,20 @@ def test_rmsnorm_inplace_on_qkv_head_views(M):
     q, k, v = qkv.split([nq * D, nkv * D, nkv * D], dim=-1)
     qn, kn = RMSNorm(D, eps), RMSNorm(D, eps)
     qn.weight, kn.weight = wq.to(DEV), wk.to(DEV)
-    # out-of-place forward on the view returns the normalized heads
-    y = qn.forward(q.view(-1, nq, D))
+    # out-of-place forward on the view returns the normalized heads through
+    # the strided kernel (the copy-and-normalize path would call rmsnorm_quant)
+    import minisgl_amd.layers.norm as norm_mod
+
+    def _no_copy_path(*a, **kw):
+        raise AssertionError("RMSNorm.forward took the copy path on a head view")
+
+    orig = norm_mod.rmsnorm_quant
+    if not q.view(-1, nq, D).is_contiguous():  # one token: the view is contiguous, no copy either way
+        norm_mod.rmsnorm_quant = _no_copy_path
+    try:
+        y = qn.forward(q.view(-1, nq, D))
+    finally:
+        norm_mod.rmsnorm_quant = orig
     qn.forward_inplace(q.view(-1, nq, D))
     kn.forward_inplace(k.view(-1, nkv, D))
     torch.cuda.synchronize()
