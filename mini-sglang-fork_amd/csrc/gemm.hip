@@ -6,6 +6,7 @@
 
 #include "gemm_kernels.h"
 #include "gemm_ksplit.h"
+#include "gemm_stream.h"
 
 namespace mw8 {
 
@@ -193,6 +194,9 @@ constexpr TileCfg kTileCfgs[] = {
     // 6: ring, 8 waves (4x2), 2 stages, the bf16 tile staged in two row
     // passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs
     {256, 320, true, 128, 1, false, "tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"},
+    // 7: the pipelined persistent walk over 256x256 tiles (bf16 output, at
+    // least 6 K stages and one tile per CU; else as cfg 2)
+    {256, 256, true, 128, 1, false, "stream_gemm_kernel<256, 0, false, -1>"},
 };
 constexpr int kNumRingCfgs = sizeof(kTileCfgs) / sizeof(kTileCfgs[0]);
 
@@ -347,6 +351,15 @@ int default_ksplit_cfg(int64_t M, int64_t N, int64_t K) {
   return -1;
 }
 
+// The stream walk (cfg 7) replaces the one-tile 256 x 256 ring (cfg 2)
+// where its tiles are short: fewer than 16 K stages of 128 bytes, at least
+// one tile per CU.  Measured on MI355X (graph-timed, rotating weights, us,
+// cfg 2 -> cfg 7, bit-identical): 32768 x 2048 x 768 71.9 -> 64.2, 32768 x
+// 1536 x 2048 101.9 -> 100.1; with 40 or more stages the walk's static tile
+// lists lose to the hardware's dynamic block dispatch (gate_up M=8192 1160
+// -> 1228, down M=8192 591 -> 635, qkv M=8192 263 -> 283).
+constexpr int64_t kStreamMaxStages = 15;
+
 int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
   if (K % 64 != 0) return 0;
   const int ks = default_ksplit_cfg(M, N, K);
@@ -361,6 +374,10 @@ int default_tile_cfg(int64_t M, int64_t N, int64_t K) {
       best = mc.cfg;
     }
   }
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  if (best == 2 && K % kStreamBK == 0 && K / kStreamBK >= kStreamMinStages && K / kStreamBK <= kStreamMaxStages &&
+      tiles >= device_cus() && plan_split(M, N, K, kTileCfgs[2]).sp <= 1)
+    return 7;
   return best;
 }
 
@@ -410,6 +427,24 @@ int launch_split_reduce(const GemmArgs& g, const SplitPlan& sp, hipStream_t st) 
   return kOk;
 }
 
+// The stream walk (gemm_stream.h) over 256 x 256 tiles: one block per CU.
+template <bool kGrouped, int kAct = -1>
+int launch_stream(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  constexpr int kLds = stream_lds_bytes<256, kAct>();
+  constexpr auto kern = stream_gemm_kernel<256, kEpiBf16, kGrouped, kAct>;
+  if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(512), kLds, st, g);
+  return kOk;
+}
+
+// Whether the stream walk takes a bf16 GEMM: whole 128-byte K stages, at
+// least kStreamMinStages of them, 16-byte output rows, and an output the
+// 32-bit buffer offsets reach.
+bool stream_fits(const GemmArgs& g, int64_t out_rows, int64_t out_cols) {
+  return g.staged_out && g.K % kStreamBK == 0 && g.K / kStreamBK >= kStreamMinStages && out_cols % 8 == 0 &&
+         out_rows * g.ldo * 2 < (int64_t{1} << 31);
+}
+
 template <int EPI>
 int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   const int cfg = select_tile_cfg(g.M, g.N, g.K);
@@ -452,7 +487,15 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
       rc = one_row ? launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, kStreamAux>(g, dim3(tiles), st)
                    : launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st);
       break;
-    default: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 6: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    default: {
+      const int64_t cus = device_cus();
+      if (EPI == kEpiBf16 && tiles >= cus && stream_fits(g, g.M, g.N))
+        rc = launch_stream<false>(g, static_cast<unsigned>(cus), st);
+      else
+        rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st);
+      break;
+    }
   }
   if (rc != kOk || !split) return rc;
   switch (c.bm * 1000 + c.bn) {
@@ -463,6 +506,7 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 
 // Decode core up to 32 tokens, the tile core above 64.  In between the
 // tile core when K % 128 == 0 (its 64-row rings stream 1.2-2x faster than
@@ -604,7 +648,8 @@ int launch_grouped3(const GemmArgs& g, unsigned blocks, hipStream_t st) {
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, int kPerCu, int kAct = -1>
 int launch_grouped_persist(const GemmArgs& g, hipStream_t st) {
   constexpr int kLds = NSTAGE * (BM + BN) * BK;
-  constexpr auto kern = grouped_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, true, kPerCu, kAct>;
+  constexpr auto kern =
+      grouped_persist_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, true, kPerCu, kAct, BK == 128 ? 16 : 32>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   const unsigned grid = static_cast<unsigned>(device_cus() * kPerCu);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * WM * WN), kLds, st, g);
@@ -621,7 +666,7 @@ int launch_grouped_persist(const GemmArgs& g, hipStream_t st) {
 // persistent chunk walk (cfg 1): 1024 tokens 237 -> 215 us, 4096 tokens
 // 536 -> 459 us against cfg 0; at 16 pairs per expert (256 tokens) cfg 0
 // (167 us against 177).
-constexpr int kNumMoeCfgs = 2;
+constexpr int kNumMoeCfgs = 3;
 int default_moe_cfg(const GemmArgs& g) {
   if (g.K % 64 == 0 && g.num_experts < kPersistMaxSlots &&
       g.num_valid >= 32 * static_cast<int64_t>(g.num_experts))
@@ -640,6 +685,9 @@ int launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t s
   if (cfg < 0 || cfg >= kNumMoeCfgs) cfg = default_moe_cfg(g);
   if (cfg == 1 && g.num_experts < kPersistMaxSlots)
     return launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, 2>(g, st);
+  if (cfg == 2 && EPI == kEpiBf16 && g.num_experts < kPersistMaxSlots && 256 % g.align_bsz == 0 &&
+      stream_fits(g, g.num_valid, g.N))
+    return launch_stream<true>(g, static_cast<unsigned>(device_cus()), st);
   if (bm == 64) return launch_grouped3<64, 128, 64, 2, 2, 4, EPI>(g, blocks, st);
   return launch_grouped3<128, 128, 64, 2, 2, 4, EPI>(g, blocks, st);
 }
@@ -769,6 +817,11 @@ int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st, b
 // Gate|up GEMM with the gated activation fused (persistent chunk walk, the
 // moe cfg 1 tiling): out [rows, N/2] = act(gate) * up, bf16.
 int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st) {
+  const int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  if (cfg == 2 && 256 % g.align_bsz == 0 && stream_fits(g, g.num_valid, g.N / 2)) {
+    if (act == 0) return launch_stream<true, 0>(g, static_cast<unsigned>(device_cus()), st);
+    return launch_stream<true, 1>(g, static_cast<unsigned>(device_cus()), st);
+  }
   if (act == 0) return launch_grouped_persist<128, 256, 64, 2, 2, 3, kEpiBf16, 2, 0>(g, st);
   return launch_grouped_persist<128, 256, 64, 2, 2, 3, kEpiBf16, 2, 1>(g, st);
 }

@@ -1077,18 +1077,17 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems, int kPerCu,
-          int kAct = -1>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(kPerCu * WM * WN / 4)))
-void grouped_persist_kernel(GemmArgs g) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
-  extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ int run_start[kPersistMaxSlots + 1];  // first alignment block of expert e
-  __shared__ int act_base[kPersistMaxSlots + 1];   // units (experts or chunks) before e
-  __shared__ int wave_tot[kWaves];
+// Run tables of a grouped walk, built by every block from expert_ids:
+// run_start[e] = first alignment block of expert e (run_start[E] = blocks
+// in use) and act_base[e] = units (experts with blocks, or chunks of up to
+// per_tile blocks with kChunkItems) before e; returns the unit total.
+// Ends with a __syncthreads: the tables are visible to the whole block.
+template <int kThreads, bool kChunkItems>
+__device__ __forceinline__ int build_run_tables(const GemmArgs& g, int per_tile, int* run_start, int* act_base,
+                                                int* wave_tot) {
+  constexpr int kWaves = kThreads / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int E = g.num_experts, ab = g.align_bsz, per_tile = BM / ab;
+  const int E = g.num_experts, ab = g.align_bsz;
   const int used = *g.num_post_pad / ab;  // alignment blocks in use
   // run starts: the block b where expert_ids steps from p to c starts the
   // runs of experts p+1 .. c (a virtual block `used` starts every later one)
@@ -1119,6 +1118,22 @@ void grouped_persist_kernel(GemmArgs g) {
   }
   if (tid == 0) act_base[E] = carry;
   __syncthreads();
+  return carry;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, bool kChunkItems, int kPerCu,
+          int kAct = -1, int MF = 32>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(kPerCu * WM * WN / 4)))
+void grouped_persist_kernel(GemmArgs g) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kThreads = 64 * WM * WN, kWaves = WM * WN;
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int run_start[kPersistMaxSlots + 1];  // first alignment block of expert e
+  __shared__ int act_base[kPersistMaxSlots + 1];   // units (experts or chunks) before e
+  __shared__ int wave_tot[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = g.num_experts, ab = g.align_bsz, per_tile = BM / ab;
+  const int carry = build_run_tables<kThreads, kChunkItems>(g, per_tile, run_start, act_base, wave_tot);
   // column tiles: BN output columns, or BN / 2 activation columns (kAct)
   constexpr int kTileCols = kAct >= 0 ? BN / 2 : BN;
   const int64_t out_cols = kAct >= 0 ? g.N / 2 : g.N;
@@ -1164,7 +1179,7 @@ void grouped_persist_kernel(GemmArgs g) {
                   (c1 - c0) * ab,
                   -1};
       __syncthreads();  // the previous tile's LDS staging has been read out
-      tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows, kAct>(g, lds, job);
+      tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, SortedRunRows, kAct, 0, MF>(g, lds, job);
     }
   }
 #endif  // __HIP_DEVICE_COMPILE__

@@ -275,3 +275,38 @@ def test_gemm_every_decode_config(M, K, N):
             assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w), y_ref).all(), f"cfg {cfg}"
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
+
+
+@pytest.mark.parametrize(
+    "M,K,N,bias",
+    [(4100, 768, 4104, True), (2080, 1024, 8200, False), (4096, 5120, 7168, False), (8192, 896, 2056, True)],
+)
+def test_gemm_stream_walk(M, K, N, bias):
+    """The pipelined persistent walk (tile configuration 7, forced) on shapes
+    it takes (at least one 256 x 256 tile per CU, K >= 768), ragged in M and
+    N, with and without bias: bit-identical to the one-tile 256 x 256 ring
+    (configuration 2) on every output, and bit-exact against the oracle on a
+    row sample (first and last rows, rows of the last partial tile)."""
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm stream walk M={M} K={K} N={N} bias={bias}")
+    c = linear_case(M, K, N, seed=M + N, bias=bias)
+    q, s = quant_per_token(c["x"].to(DEV))
+    w, s_w = c["w"].to(DEV), c["s_w"].to(DEV)
+    b = c["bias"].to(DEV) if bias else None
+    lib = load()
+    try:
+        lib.mw8_set_tuning(-1, 7, -1)
+        assert lib.mw8_gemm_kernel_name(M, N, K).decode().startswith("stream_gemm_kernel")
+        y_stream = gemm_w8a8(q, s, w, s_w, b)
+        lib.mw8_set_tuning(-1, 2, -1)
+        y_tile = gemm_w8a8(q, s, w, s_w, b)
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+    torch.cuda.synchronize()
+    assert torch.equal(y_stream.view(torch.int16), y_tile.view(torch.int16))
+    rows = np.unique(np.r_[0, 1, M - 1, np.arange(M - 40, M, 3), np.linspace(0, M - 1, 24).astype(int)])
+    q_ref, s_ref = orc.quant_per_token(f32(c["x"][rows]))
+    y_ref = orc.epilogue(orc.gemm_i32(q_ref, c["w"].numpy()), s_ref, c["s_w"].numpy(),
+                         f32(c["bias"]) if bias else None)
+    assert bf16_bits_equal(y_stream[torch.as_tensor(rows, device=DEV)], y_ref).all()
