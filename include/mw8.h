@@ -191,6 +191,23 @@ int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W
                                mw8_stream_t stream);
 
 /*
+ * F.linear of a decode batch in one launch: y bf16 [M, N] = the W8A8
+ * linear of the bf16 activations x [M, K] (row stride ldx elements, a
+ * multiple of 8; x 16-byte aligned): per-token quantization (the
+ * mw8_quant_per_token_bf16 arithmetic), int8 GEMM and epilogue, bit for
+ * bit what the two calls write.  Each block of the decode core quantizes
+ * the few token rows itself, so there is no quantizer launch and no int8
+ * copy of x.  Takes M <= 4 where the decode core streams at most 6 K
+ * stages of 256 bytes per wave (mw8_linear_bf16_supported); returns
+ * MW8_ERR_SHAPE otherwise.  Replaces _LinearTPImpl.forward -> F.linear
+ * (python/minisgl/layers/linear.py:31-32) for an input with no quantizing
+ * producer (the attention output into o_proj, python/minisgl/models/utils.py:123).
+ */
+int mw8_linear_bf16_w8a8(const void* x, int64_t ldx, const int8_t* W, const float* sw, const void* bias,
+                         void* y, int64_t M, int64_t N, int64_t K, mw8_stream_t stream);
+int32_t mw8_linear_bf16_supported(int64_t M, int64_t N, int64_t K);
+
+/*
  * Same GEMM, raw int32 accumulators acc [M, N] (parity hook; no scales).
  * Test hook for the A4 int32 contract; no reference counterpart.
  */

@@ -65,6 +65,9 @@ int rmsnorm_quant_bf16(const void*, void*, const void*, float, int64_t, int64_t,
                        hipStream_t);
 int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, float, int64_t, int64_t, int64_t,
                          hipStream_t);
+int linear_bf16_w8a8(const void*, int64_t, const int8_t*, const float*, const void*, void*, int64_t, int64_t,
+                     int64_t, hipStream_t);
+int linear_bf16_supported(int64_t, int64_t, int64_t);
 int64_t calib_sink_len();
 int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
 int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
@@ -113,6 +116,13 @@ int mw8_act_and_mul_quant_bf16(const void* x, int64_t R, int64_t two_d, int32_t 
 void mw8_set_tuning(int32_t decode_cfg, int32_t tile_cfg, int32_t moe_cfg) {
   mw8::set_tuning(decode_cfg, tile_cfg, moe_cfg);
 }
+
+int mw8_linear_bf16_w8a8(const void* x, int64_t ldx, const int8_t* W, const float* sw, const void* bias, void* y,
+                         int64_t M, int64_t N, int64_t K, mw8_stream_t st) {
+  MW8_ENTRY(mw8::linear_bf16_w8a8(x, ldx, W, sw, bias, y, M, N, K, S(st)));
+}
+
+int32_t mw8_linear_bf16_supported(int64_t M, int64_t N, int64_t K) { return mw8::linear_bf16_supported(M, N, K); }
 
 size_t mw8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return mw8::gemm_workspace_bytes(M, N, K);

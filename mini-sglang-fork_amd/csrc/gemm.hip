@@ -91,6 +91,19 @@ int launch_decode3_bal(const GemmArgs& g, hipStream_t st) {
   return kOk;
 }
 
+// Fused quantization (bf16 activation rows, kXQ): the decode3
+// configurations with one token group.
+template <int WAVES, int D, int RG>
+int launch_decode3_xq(const GemmArgs& g, hipStream_t st) {
+  constexpr int kLds = RG * DecodeRing<1, WAVES, D>::kLds;
+  constexpr auto kern = decode3_gemm_kernel<1, WAVES, D, kEpiBf16, DenseRows, RG, true>;
+  if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+  const int64_t cus = device_cus();
+  const int64_t blocks = cus * ((g.N + cus * 16 * RG - 1) / (cus * 16 * RG));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), kLds, st, g);
+  return kOk;
+}
+
 template <int TG, int EPI>
 int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
   switch (cfg) {
@@ -507,6 +520,20 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The decode configuration a fused-quantization call at (M, N, K) runs, or
+// -1 if it does not take it: at most kXQMaxTokens rows, a decode3
+// configuration (override first) whose waves each stream at most
+// kXQMaxStages K stages of 256 bytes.
+int xq_decode_cfg(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kXQMaxTokens || N < 1 || K < 16 || K % 16 != 0) return -1;
+  int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+  if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
+  const DecodeCfg& c = kDecodeCfgs[cfg];
+  if (c.core != 1) return -1;
+  const int64_t steps = (K + 255) / 256;
+  return (steps + c.waves - 1) / c.waves <= kXQMaxStages ? cfg : -1;
+}
+
 
 // Decode core up to 32 tokens, the tile core above 64.  In between the
 // tile core when K % 128 == 0 (its 64-row rings stream 1.2-2x faster than
@@ -555,6 +582,38 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
 }
 
 }  // namespace
+
+int linear_bf16_supported(int64_t M, int64_t N, int64_t K) { return xq_decode_cfg(M, N, K) >= 0 ? 1 : 0; }
+
+int linear_bf16_w8a8(const void* x, int64_t ldx, const int8_t* W, const float* sw, const void* bias, void* y,
+                     int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  MW8_REQUIRE(x && W && sw && y, kErrArg, "linear_bf16: null x/W/scales/y");
+  const int cfg = xq_decode_cfg(M, N, K);
+  MW8_REQUIRE(cfg >= 0, kErrShape,
+              "linear_bf16: M=%lld N=%lld K=%lld is not a fused decode shape (M <= %d, at most %d K stages of 256 "
+              "bytes per wave)",
+              (long long)M, (long long)N, (long long)K, kXQMaxTokens, kXQMaxStages);
+  MW8_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned16(x) && aligned16(W), kErrAlign,
+              "linear_bf16: x rows and W need 16-byte alignment (ldx=%lld)", (long long)ldx);
+  MW8_REQUIRE(N < (1ll << 31) && N * K < (1ll << 31), kErrShape, "linear_bf16: W exceeds 2^31 bytes");
+  GemmArgs g{};
+  g.A = static_cast<const int8_t*>(x);  // bf16 rows, quantized in the kernel
+  g.W = W; g.sw = sw;
+  g.bias = static_cast<const uint16_t*>(bias);
+  g.out = y; g.M = M; g.N = N; g.K = K; g.lda = ldx; g.ldo = N;
+  g.top_k = 1;
+  int rc;
+  switch (cfg) {
+    case 2: rc = launch_decode3_xq<1, 4, 1>(g, st); break;
+    case 3: rc = launch_decode3_xq<2, 2, 1>(g, st); break;
+    case 4: rc = launch_decode3_xq<1, 4, 2>(g, st); break;
+    case 5: rc = launch_decode3_xq<4, 2, 2>(g, st); break;
+    case 6: rc = launch_decode3_xq<4, 3, 2>(g, st); break;
+    default: rc = launch_decode3_xq<8, 2, 2>(g, st); break;
+  }
+  if (rc != kOk) return rc;
+  return check_launch("linear_bf16");
+}
 
 void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
   g_decode_cfg.store(decode_cfg, std::memory_order_relaxed);

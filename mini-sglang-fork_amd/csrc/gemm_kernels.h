@@ -1343,11 +1343,21 @@ struct RingDrain<D, OPS, D> {
 // per block), the token rows are gathered through sorted_ids (padding rows
 // read zeros), and the epilogue scatters to pair rows with the routed
 // weight.
-template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1>
+// kXQ (dense, one token group, bf16 output): g.A holds the bf16 activation
+// rows [M <= 16, lda elements], quantized inside the block -- the fused
+// F.linear of a decode batch.  Every block computes the rows' absmax; each
+// wave quantizes its K range of the rows into its (not yet used) ring slots
+// with the quantizer's arithmetic, loads its token fragments of every stage
+// into registers (at most kXQMaxStages stages per wave), and only then
+// starts the weight stream; the epilogue takes the row scales from LDS.
+constexpr int kXQMaxStages = 6, kXQMaxTokens = 4;
+
+template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1, bool kXQ = false>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  static_assert(!kXQ || (TG == 1 && !Rows::kGrouped && epi_bf16_out(EPI)), "fused quantization: dense bf16, <= 16 rows");
   constexpr int kAcc = RG * TG * 4;
-  constexpr int kOps = 4 * RG + 4 * TG;  // vector memory ops per stage (DMA + token loads)
+  constexpr int kOps = 4 * RG + (kXQ ? 0 : 4 * TG);  // vector memory ops per stage (DMA + token loads)
   static_assert(D >= 2 && D <= 6 && (D - 1) * kOps < 64, "ring depth");
   static_assert(!Rows::kRuns, "grouped rows: one alignment block per block");
   extern __shared__ __align__(16) unsigned char ring[];
@@ -1452,14 +1462,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     for (int j = 0; j < 4 * RG; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0,
                                                kStreamAux);
+    if constexpr (!kXQ) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
-      const bool kin = k < g.K;
+      for (int kb = 0; kb < 4; ++kb) {
+        const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
+        const bool kin = k < g.K;
 #pragma unroll
-      for (int tg = 0; tg < TG; ++tg) {
-        const uint64_t a = (mok[tg] & kin) ? xrow[tg] + static_cast<uint64_t>(k) : zero_addr;
-        xr[d][kb][tg] = *reinterpret_cast<gv4i_ptr>(a);
+        for (int tg = 0; tg < TG; ++tg) {
+          const uint64_t a = (mok[tg] & kin) ? xrow[tg] + static_cast<uint64_t>(k) : zero_addr;
+          xr[d][kb][tg] = *reinterpret_cast<gv4i_ptr>(a);
+        }
       }
     }
   };
@@ -1505,6 +1517,71 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     }
   }
 
+  // fused quantization (kXQ): row absmax over the block, the wave's K range
+  // quantized into its ring slots, its token fragments into registers
+  __shared__ uint32_t xq_max[kXQ ? 16 : 1];
+  __shared__ float xq_s[kXQ ? 16 : 1];
+  v4i xq[kXQ ? kXQMaxStages : 1][4];
+  if constexpr (kXQ) {
+    const int M = static_cast<int>(g.M);
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.A);
+    const int64_t ldx = g.lda;
+    if (tid < 16) xq_max[tid] = 0;
+    __syncthreads();
+    for (int m = 0; m < M; ++m) {
+      uint32_t mx = 0;
+      for (int64_t c = tid; c < g.K / 8; c += 64 * WAVES) {
+        const v4i v = *reinterpret_cast<const v4i*>(X + m * ldx + 8 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w = static_cast<uint32_t>(v[j]), lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
+          mx = lo > mx ? lo : mx;
+          mx = hi > mx ? hi : mx;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = __shfl_xor(mx, off, 64);
+        mx = o > mx ? o : mx;
+      }
+      if (lane == 0) atomicMax(&xq_max[m], mx);
+    }
+    __syncthreads();
+    if (tid < 16) xq_s[tid] = tid < M ? row_scale(bf16_to_f32(static_cast<uint16_t>(xq_max[tid]))).s : 0.0f;
+    // this wave's K range [256 s_begin, 256 s_end) of each row, int8, row-major in its ring
+    const int kw = 256 * (s_end - s_begin);
+    for (int m = 0; m < M; ++m) {
+      const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(xq_max[m])));
+      for (int u = lane; u < kw / 16; u += 64) {
+        const int64_t k = 256 * static_cast<int64_t>(s_begin) + 16 * u;
+        v4i q = v4i{0};
+        if (k < g.K) {  // K % 16 == 0: a 16-element chunk is all in or all out
+          const v4i v0 = *reinterpret_cast<const v4i*>(X + m * ldx + k);
+          const v4i v1 = *reinterpret_cast<const v4i*>(X + m * ldx + k + 8);
+          U16x8 a, b;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            a.w[j] = static_cast<uint32_t>(v0[j]);
+            b.w[j] = static_cast<uint32_t>(v1[j]);
+          }
+          const uint2 qa = rs.fast ? quant8<true>(a, rs) : quant8<false>(a, rs);
+          const uint2 qb = rs.fast ? quant8<true>(b, rs) : quant8<false>(b, rs);
+          q = v4i{static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qb.x), static_cast<int>(qb.y)};
+        }
+        *reinterpret_cast<v4i*>(my_ring + m * kw + 16 * u) = q;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's ring writes done (one wave reads them)
+#pragma unroll
+    for (int i = 0; i < kXQMaxStages; ++i)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        xq[i][kb] = r16 < M && i < s_end - s_begin
+                        ? *reinterpret_cast<const v4i*>(my_ring + r16 * kw + 256 * i + 64 * kb + 16 * grp)
+                        : v4i{0};
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // fragments read before the weight DMA reuses the ring
+  }
+
   v4i acc[RG][TG];
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg)
@@ -1528,7 +1605,31 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   // run branch-free: D stages in flight, refill after each consume; the last
   // D stages drain with compile-time waits.
   const int n_st = s_end - s_begin;
-  if (n_st > 0) {
+  if constexpr (kXQ) {
+    // fused quantization: every stage's token fragments are in xq (compile-
+    // time indices), so the wave's stages run fully unrolled
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if (i < n_st) issue(i, s_begin + i);
+#pragma unroll
+    for (int i = 0; i < kXQMaxStages; ++i) {
+      if (i < n_st) {
+        const int later = n_st - 1 - i < D - 1 ? n_st - 1 - i : D - 1;  // stages issued after stage i
+        wait_stages<kOps, (D - 1 < 3 ? D - 1 : 3)>(later);
+        const unsigned char* slot = my_ring + (i % D) * kStage;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg) {
+            const v4i w = *reinterpret_cast<const v4i*>(slot + (16 * rg + r16) * 256 + 16 * ((4 * kb + grp) ^ r16));
+            acc[rg][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, xq[i][kb], acc[rg][0], 0, 0, 0);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): fragments read before the refill
+        if (i + D < n_st) issue(i % D, s_begin + i + D);
+      }
+    }
+  } else if (n_st > 0) {
     const int n_pad = ((n_st + D - 1) / D) * D;
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, s_begin + d);
@@ -1566,7 +1667,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
       if (nl >= rows || m >= g.M) continue;
       e_orow[0] = m;
       if constexpr (epi_bf16_out(EPI)) {
-        e_sa[0] = g.sa[m];
+        e_sa[0] = kXQ ? xq_s[m] : g.sa[m];
         e_sw[0] = sw[n];
         e_x[0] = g.bias ? bf16_to_f32(g.bias[n]) : 0.0f;
       }

@@ -19,15 +19,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// 8 bf16 values packed two per 32-bit register (element j in bits
-// 16*(j&1) .. of word j/2), so a register-resident row costs 4 VGPRs per
-// 16-byte vector.
-struct alignas(16) U16x8 {
-  uint32_t w[4];
-  __device__ __forceinline__ uint32_t get(int j) const {
-    return (j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xFFFFu);
-  }
-};
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -86,29 +77,8 @@ __device__ __forceinline__ uint32_t absmax8(const U16x8& v, uint32_t m) {
   return m;
 }
 
-// bf16 element 2j / 2j+1 of a packed word as fp32 (one shift or one mask)
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 
-// Four integral fp32 values in [-127, 127] -> four int8 bytes of a word.
-__device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d) {
-  const uint32_t lo = (static_cast<uint32_t>(static_cast<int>(a)) & 0xFFu) |
-                      ((static_cast<uint32_t>(static_cast<int>(b)) & 0xFFu) << 8);
-  const uint32_t hi = (static_cast<uint32_t>(static_cast<int>(c)) & 0xFFu) |
-                      ((static_cast<uint32_t>(static_cast<int>(d)) & 0xFFu) << 8);
-  return lo | (hi << 16);
-}
 
-template <bool FAST>
-__device__ __forceinline__ uint2 quant8(const U16x8& v, const RowScale& rs) {
-  float f[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f[2 * j] = quant_div_rne_t<FAST>(bf16_lo(v.w[j]), rs);
-    f[2 * j + 1] = quant_div_rne_t<FAST>(bf16_hi(v.w[j]), rs);
-  }
-  return make_uint2(pack4_i8(f[0], f[1], f[2], f[3]), pack4_i8(f[4], f[5], f[6], f[7]));
-}
 
 // ------------------------------------------------------------ quantizer
 template <int TPR, int VPT>

@@ -41,6 +41,8 @@ SIGNATURES = {
     ),
     "mw8_gemm_w8a8_bf16_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "mw8_gemm_w8a8_i32": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, c_size_t, _P]),
+    "mw8_linear_bf16_w8a8": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "mw8_linear_bf16_supported": (_I32, [_I64, _I64, _I64]),
     "mw8_topk_softmax": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _P, _P]),
     "mw8_moe_align_max_padded": (_I64, [_I64, _I32, _I32]),
     "mw8_moe_align_block_size": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),

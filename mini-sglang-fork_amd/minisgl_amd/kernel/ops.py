@@ -253,6 +253,42 @@ def gemm_w8a8(
     return y
 
 
+def linear_bf16_supported(M: int, N: int, K: int) -> bool:
+    """Whether linear_bf16_w8a8 takes a decode batch of this shape (host
+    only; the answer follows the decode-configuration override)."""
+    return bool(load().mw8_linear_bf16_supported(M, N, K))
+
+
+def linear_bf16_w8a8(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    s_w: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """y bf16 [M, N] = the W8A8 linear of bf16 x [M, K] in one launch
+    (per-token quantization inside the decode GEMM), bit for bit
+    gemm_w8a8(*quant_per_token(x), w, s_w, bias).  Decode batches only
+    (linear_bf16_supported); x rows 16-byte aligned, last dim contiguous."""
+    _on_gpu(x, w, s_w, bias, out)
+    _need(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1, "x: bf16 [M, K], rows contiguous")
+    _need(w.dtype == torch.int8 and w.dim() == 2 and w.is_contiguous() and w.shape[1] == x.shape[1], "W: int8 [N, K]")
+    M, K = x.shape
+    N = w.shape[0]
+    _need(s_w.dtype == torch.float32 and s_w.shape == (N,) and s_w.is_contiguous(), "s_w: fp32 [N]")
+    if bias is not None:
+        _need(bias.dtype == torch.bfloat16 and bias.shape == (N,) and bias.is_contiguous(), "bias: bf16 [N]")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _need(y.dtype == torch.bfloat16 and y.shape == (M, N) and y.is_contiguous(), "bad out buffer")
+    ldx = x.stride(0) if M > 1 else K
+    check(
+        load().mw8_linear_bf16_w8a8(
+            _ptr(x), ldx, _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K, _stream(x),
+        )
+    )
+    return y
+
+
 def gemm_w8a8_i32(q: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """Raw int32 accumulators acc [M, N] = A . W^T (parity hook)."""
     M, N, K = _check_gemm(q, w)
@@ -642,6 +678,8 @@ __all__ = [
     "rmsnorm_strided",
     "gemm_w8a8",
     "gemm_w8a8_i32",
+    "linear_bf16_supported",
+    "linear_bf16_w8a8",
     "topk_softmax",
     "moe_align_block_size",
     "fused_moe_kernel_w8a8",

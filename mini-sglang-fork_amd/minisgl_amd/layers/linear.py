@@ -18,7 +18,7 @@ from typing import List, Optional, Tuple
 
 import torch
 
-from ..kernel import gemm_w8a8, quant_per_token
+from ..kernel import gemm_w8a8, linear_bf16_supported, linear_bf16_w8a8, quant_per_token
 from .base import BaseOP
 
 
@@ -56,8 +56,21 @@ class _LinearW8A8Impl(BaseOP):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1])
-        q, s = quant_per_token(x2)
-        y = self.forward_quantized(q, s)
+        M, K = x2.shape
+        N = self.weight.shape[0]
+        if (
+            0 < M <= 4
+            and x2.dtype == torch.bfloat16
+            and x2.stride(1) == 1
+            and (M == 1 or x2.stride(0) % 8 == 0)
+            and x2.data_ptr() % 16 == 0
+            and linear_bf16_supported(M, N, K)
+        ):
+            # decode batch: quantization inside the GEMM launch (one kernel)
+            y = linear_bf16_w8a8(x2, self.weight, self.weight_scale, self.bias)
+        else:
+            q, s = quant_per_token(x2)
+            y = self.forward_quantized(q, s)
         return y.view(*lead, y.shape[-1])
 
     def load_float_weight(self, w: torch.Tensor, bias: Optional[torch.Tensor] = None) -> None:

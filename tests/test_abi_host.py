@@ -118,6 +118,19 @@ def test_workspace_bound_and_tuning_counts(lib):
     assert 0 < worst <= mx
 
 
+def test_linear_bf16_supported_shapes(lib):
+    """The one-launch decode linear takes 1-4 tokens where the decode core's
+    waves stream at most 6 K stages of 256 bytes (planned for 256 CUs
+    without a GPU): o_proj / qkv of Qwen3-14B at 1-4 tokens, not at 5 tokens,
+    not the K = 17408 down projection, not K % 16 != 0."""
+    sup = lib.mw8_linear_bf16_supported
+    for M in (1, 2, 3, 4):
+        assert sup(M, 5120, 5120) == 1 and sup(M, 7168, 5120) == 1
+    assert sup(5, 5120, 5120) == 0 and sup(0, 5120, 5120) == 0
+    assert sup(1, 5120, 17408) == 0
+    assert sup(1, 5120, 5128) == 0
+
+
 FAKE_A, FAKE_B, FAKE_C = 4096, 8192, 12288  # aligned non-null stand-ins: never dereferenced
 
 
@@ -126,6 +139,11 @@ def test_argument_errors_return_codes(lib):
     assert lib.mw8_quant_per_token_bf16(None, 4, 16, 16, None, 16, None, None) == E["MW8_ERR_ARG"]
     assert b"null" in lib.mw8_last_error()
     assert lib.mw8_quant_per_token_bf16(FAKE_A, 4, 16, 8, FAKE_B, 16, FAKE_C, None) == E["MW8_ERR_SHAPE"]
+    # the one-launch decode linear: null operand, too many tokens, unaligned row stride
+    lin = lib.mw8_linear_bf16_w8a8
+    assert lin(None, 5120, FAKE_B, FAKE_C, None, FAKE_A, 1, 5120, 5120, None) == E["MW8_ERR_ARG"]
+    assert lin(FAKE_A, 5120, FAKE_B, FAKE_C, None, FAKE_A, 5, 5120, 5120, None) == E["MW8_ERR_SHAPE"]
+    assert lin(FAKE_A, 5124, FAKE_B, FAKE_C, None, FAKE_A, 2, 5120, 5120, None) == E["MW8_ERR_ALIGN"]
     # K % 16 != 0
     rc = lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 4, 8, 40, None, 0, None)
     assert rc == E["MW8_ERR_SHAPE"] and b"multiple of 16" in lib.mw8_last_error()

@@ -310,3 +310,73 @@ def test_gemm_stream_walk(M, K, N, bias):
     y_ref = orc.epilogue(orc.gemm_i32(q_ref, c["w"].numpy()), s_ref, c["s_w"].numpy(),
                          f32(c["bias"]) if bias else None)
     assert bf16_bits_equal(y_stream[torch.as_tensor(rows, device=DEV)], y_ref).all()
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 7168), (1024, 6144), (1040, 520), (2048, 2056)])
+def test_linear_bf16_fused_quant(K, N):
+    """The one-launch decode linear (mw8_linear_bf16_w8a8: per-token
+    quantization inside the decode GEMM) equals quant_per_token followed by
+    gemm_w8a8 bit for bit, for 1-4 tokens, under every decode configuration
+    that takes the shape; rows with a stride past K, an all-zero row, x20
+    outliers and a bias; and the oracle on every row."""
+    from minisgl_amd.kernel import linear_bf16_supported, linear_bf16_w8a8
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"linear bf16 fused quant K={K} N={N}")
+    lib = load()
+    gen = torch.Generator().manual_seed(K + N)
+    w = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8)
+    s_w = torch.rand(N, generator=gen) * 9e-3 + 1e-3
+    bias = torch.randn(N, generator=gen).to(torch.bfloat16)
+    wd, swd, bd = w.to(DEV), s_w.to(DEV), bias.to(DEV)
+    for M in (1, 2, 3, 4):
+        buf = torch.randn(M, K + 64, generator=gen) * 2
+        buf[:, :K][torch.rand(M, K, generator=gen) < 1e-3] *= 20
+        if M >= 3:
+            buf[1] = 0.0  # all-zero row: s = 0, q = 0
+        xb = buf.to(torch.bfloat16)
+        x = xb.to(DEV)[:, :K]  # row stride K + 64
+        for b, bref in ((None, None), (bd, f32(bias))):
+            q, s = quant_per_token(x.contiguous())
+            want = gemm_w8a8(q, s, wd, swd, b)
+            q_ref, s_ref = orc.quant_per_token(f32(xb[:, :K]))
+            y_ref = orc.epilogue(orc.gemm_i32(q_ref, w.numpy()), s_ref, s_w.numpy(), bref)
+            assert bf16_bits_equal(want, y_ref).all(), f"reference path M={M}"
+            ran = 0
+            try:
+                for cfg in [-1] + list(range(_tuning_count(0))):
+                    lib.mw8_set_tuning(cfg, -1, -1)
+                    if not linear_bf16_supported(M, N, K):
+                        continue
+                    got = linear_bf16_w8a8(x, wd, swd, b)
+                    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={M} cfg={cfg}"
+                    ran += 1
+            finally:
+                lib.mw8_set_tuning(-1, -1, -1)
+            assert ran >= 2, f"M={M}: the default and at least one forced configuration take the shape"
+
+
+def test_linear_layer_decode_takes_the_fused_path():
+    """LinearOProj.forward on a one-token bf16 input runs the one-launch
+    fused linear (no separate quantizer call) and matches the oracle."""
+    import minisgl_amd.layers.linear as lin
+
+    announce("linear layer fused decode path")
+    gen = torch.Generator().manual_seed(9)
+    layer = LinearOProj(5120, 5120, has_bias=False)
+    sd = {"weight": torch.randint(-127, 128, (5120, 5120), generator=gen, dtype=torch.int8),
+          "weight_scale": torch.rand(5120, generator=gen) * 1e-2}
+    layer.load_state_dict({k: v.to(DEV) for k, v in sd.items()})
+    x = torch.randn(1, 5120, generator=gen).to(torch.bfloat16)
+
+    def _no_quant(*a, **kw):
+        raise AssertionError("the decode forward called the separate quantizer")
+
+    orig = lin.quant_per_token
+    lin.quant_per_token = _no_quant
+    try:
+        y = layer.forward(x.to(DEV))
+    finally:
+        lin.quant_per_token = orig
+    y_ref, *_ = orc.linear_w8a8(f32(x), sd["weight"].numpy(), sd["weight_scale"].numpy())
+    assert bf16_bits_equal(y, y_ref).all()
