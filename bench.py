@@ -82,7 +82,8 @@ def device_ceilings(lib, dev):
     sink = torch.empty(n, dtype=torch.int32, device=dev)
     st = torch.cuda.Stream()
     iters, reps = 4000, 10
-    ops = 256 * 1024 / 64 * iters * 32 * 65536.0
+    # 4096 waves x iters x 64 v_mfma_i32_16x16x64_i8 of 16*16*64*2 ops each
+    ops = 256 * 1024 / 64 * iters * 64 * (16 * 16 * 64 * 2.0)
     res = {}
 
     def timed(launch, reps):

@@ -1,11 +1,13 @@
 // Measurement kernels behind the benchmark's device ceilings (gfx950).
 //
-// calib_mfma_kernel: a register-only loop of v_mfma_i32_32x32x32_i8 on four
-// independent accumulators, no memory traffic.  With constant operands the
-// matrix cores run at the nominal clock; with random operands (eight
-// fragments per operand, cycled) the datapath toggles as it does on real
-// int8 data and the part settles at its power-limited clock -- the
-// practical ceiling a W8A8 GEMM on random data can approach.
+// calib_mfma_kernel: a register-only loop of v_mfma_i32_16x16x64_i8 (the
+// instruction of the large-M tiles) on eight independent accumulators, no
+// memory traffic.  With constant operands the matrix cores run at the
+// nominal clock; with random operands (eight fragments per operand, cycled)
+// the datapath toggles as it does on real int8 data and the part settles at
+// its power-limited clock -- the practical ceiling a W8A8 GEMM on random
+// data can approach.  (On MI355X: 4.98 POPS constant, 3.92-3.99 random; the
+// same loop on v_mfma_i32_32x32x32_i8 reaches 3.35-3.41 random.)
 //
 // calib_read_kernel: a grid-stride streaming read (16 bytes per lane,
 // eight loads in flight, non-temporal) -- the practical HBM read ceiling
@@ -52,19 +54,19 @@ __global__ __launch_bounds__(kCalibThreads) void calib_mfma_kernel(int iters, in
       B[i][j] = RANDOM ? static_cast<int>(mix32(seed * 3 + 29 * i + j + 100)) : 0x01010101;
     }
   }
-  v16i acc[4];
+  v4i acc[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = v16i{0};
+  for (int i = 0; i < 8; ++i) acc[i] = v4i{0};
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[(k + j) & 7], B[(k + 3 * j) & 7], acc[j], 0, 0, 0);
+      for (int j = 0; j < 8; ++j)
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[(k + j) & 7], B[(k + 3 * j) & 7], acc[j], 0, 0, 0);
   }
   int32_t s = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s += acc[i][0] + acc[i][15];
+  for (int i = 0; i < 8; ++i) s += acc[i][0] + acc[i][3];
   sink[blockIdx.x * kCalibThreads + tid] = s;
 }
 

@@ -369,9 +369,11 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 // sets F0/F1), so LDS latency hides behind the MFMAs.  Requires K % BK == 0.
 //
 // LDS rows are BK bytes (4 or 8 chunks of 16 bytes).  Chunk c of row r sits
-// at unit r*BK/16 + (c ^ f(r)); f keeps the 8 (and the 16) rows read
-// together by one phase of a fragment load on distinct 16-byte bank groups:
-//   BK = 64 : f(r) = ((r >> 1) ^ (r >> 3)) & 3
+// at unit r*BK/16 + (c ^ f(r)), with f chosen so that the fragment reads of
+// 8 waves per CU move 207-210 B/clk per CU through LDS on MI355X, the rate
+// of a linear read (measured with an in-bounds ds_read_b128 probe):
+//   BK = 64 : f(r) = (r ^ (r >> 2)) & 3        (32x32x32 fragments, chunks
+//             2 s + g; ((r >> 1) ^ (r >> 3)) & 3 gave 130-139 B/clk here)
 //   BK = 128: f(r) = (r & 7) ^ ((r >> 3) & 1)
 // The 16x16x64 fragments of a 128-byte stage read chunk 2 g + s (lane group
 // g = l / 16, substep s) rather than 4 s + g: with lane groups on chunks
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs g) {
 // over all of a stage's K bytes, so any chunk order serves A and B alike).
 template <int BK>
 __device__ __forceinline__ int swz_f(int row) {
-  if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
+  if constexpr (BK == 64) return (row ^ (row >> 2)) & 3;
   else return (row & 7) ^ ((row >> 3) & 1);
 }
 template <int BK>
