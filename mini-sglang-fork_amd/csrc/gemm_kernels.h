@@ -10,10 +10,14 @@
 // Cores:
 //   tile_gemm_kernel  -- register-staged MFMA tile (any K % 16 == 0).
 //   tile3_gemm_kernel -- the large-M ring: direct-to-LDS DMA of A and W
-//                  tiles, NSTAGE-deep ring, v_mfma_i32_32x32x32_i8, K split
-//                  of the last partial wave of tiles (split_reduce_kernel).
+//                  tiles, NSTAGE-deep ring, v_mfma_i32_16x16x64_i8 on
+//                  128-byte stages (v_mfma_i32_32x32x32_i8 on 64-byte
+//                  ones), K split of the last partial wave of tiles
+//                  (split_reduce_kernel).
 //   grouped_persist_kernel -- the same ring walking (expert chunk, column
 //                  tile) items of the fused-MoE GEMM.
+//   (gemm_ksplit.h: in-block split-K tiles for 33-768 rows; gemm_stream.h:
+//   the pipelined persistent walk over 256x256 tiles.)
 //   decode_gemm_kernel / decode3_gemm_kernel -- dense small M (decode):
 //                  weight streaming with v_mfma_i32_16x16x64_i8, weight rows
 //                  as the MFMA "A" operand, up to 64 tokens as the "B"
