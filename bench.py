@@ -68,7 +68,7 @@ def device_peaks(lib):
             "hbm_peak_gbps": HBM_PEAK_GBPS}
 
 
-def device_ceilings(lib, dev):
+def device_ceilings(dev):
     """Live device ceilings from the library's measurement kernels, timed
     with HIP events on the launch stream: the int8 MFMA rate with constant
     operands (nominal clock) and with random operands (the power-limited
@@ -76,7 +76,9 @@ def device_ceilings(lib, dev):
     (past the 256 MB MALL)."""
     import torch
 
-    from minisgl_amd.kernel.lib import check
+    from minisgl_amd.kernel.lib import check_calib as check, load_calib
+
+    lib = load_calib()  # the measurement kernels' own library
 
     n = int(lib.mw8_calib_sink_len())
     sink = torch.empty(n, dtype=torch.int32, device=dev)
@@ -123,7 +125,7 @@ def device_ceilings(lib, dev):
     return res
 
 
-def data_path_ceilings(lib, dev):
+def data_path_ceilings(dev):
     """The operand path of the GEMM rings (16-byte buffer_load ... lds) in
     three regimes, aggregate TB/s over 256 blocks of 4 waves: an L2-resident
     region per XCD read 64 times; a 64 MB region per XCD streamed once by its
@@ -132,7 +134,9 @@ def data_path_ceilings(lib, dev):
     panels); and a private 4 MB region per block (a plain HBM stream)."""
     import torch
 
-    from minisgl_amd.kernel.lib import check
+    from minisgl_amd.kernel.lib import check_calib as check, load_calib
+
+    lib = load_calib()  # the measurement kernels' own library
 
     n = int(lib.mw8_calib_sink_len())
     sink = torch.empty(n, dtype=torch.int32, device=dev)
@@ -159,7 +163,7 @@ def data_path_ceilings(lib, dev):
     return res
 
 
-def decode_floors(lib, dev):
+def decode_floors(dev):
     """Under the bench's own timing (a HIP graph of launches replayed between
     events): the per-node cost of a trivial kernel, and at each Qwen3-14B
     decode weight size the library's plain streaming read next to the
@@ -170,7 +174,9 @@ def decode_floors(lib, dev):
     from minisgl_amd.benchmark import perf_hip
     from minisgl_amd.benchmark.inputs import QWEN3_14B_SHAPES
     from minisgl_amd.kernel import gemm_w8a8, quant_per_token
-    from minisgl_amd.kernel.lib import check
+    from minisgl_amd.kernel.lib import check_calib as check, load_calib
+
+    lib = load_calib()  # the measurement kernels' own library
 
     n = int(lib.mw8_calib_sink_len())
     sink = torch.empty(n, dtype=torch.int32, device=dev)
@@ -218,9 +224,9 @@ def ceilings_mode(args) -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     out = {"mode": "ceilings", "device": device_peaks(lib)}
-    out["device"]["measured"] = device_ceilings(lib, dev)
-    out["data_path"] = data_path_ceilings(lib, dev)
-    out["decode_floors"] = decode_floors(lib, dev)
+    out["device"]["measured"] = device_ceilings(dev)
+    out["data_path"] = data_path_ceilings(dev)
+    out["decode_floors"] = decode_floors(dev)
     print(json.dumps(out))
     return 0
 
@@ -404,7 +410,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     peaks = device_peaks(lib)
     peak_tops = peaks["int8_peak_tops"]
-    peaks["measured"] = device_ceilings(lib, dev)
+    peaks["measured"] = device_ceilings(dev)
     log(f"device: {peaks}")
 
     gen = torch.Generator(device=dev).manual_seed(0)

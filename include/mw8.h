@@ -381,36 +381,6 @@ int mw8_moe_prepare_small(const void* logits, int32_t is_bf16, int64_t M, int32_
 int mw8_moe_sum_reduce_bf16(const void* in, int64_t M, int32_t k, int64_t H, void* out,
                             mw8_stream_t stream);
 
-/*
- * Measurement kernels behind the benchmark's device ceilings; no reference
- * counterpart (the reference times only its own kernels,
- * python/minisgl/benchmark/perf.py:10-51).  Launch-only like every entry
- * point: the caller times them with events on the same stream.  `sink`
- * (device int32 [mw8_calib_sink_len()]) receives one value per thread.
- *
- * mw8_calib_mfma_i8: 256 x 1024 threads, each running iters x 32
- *   v_mfma_i32_32x32x32_i8 on registers only (65536 int8 ops each):
- *   random_operands = 0 uses constant operands (the nominal-clock rate),
- *   1 random ones (the power-limited rate int8 GEMMs on real data see).
- * mw8_calib_read: grid-stride streaming read of `bytes` (multiple of 16,
- *   16-byte aligned) -- the practical HBM read rate at that size.
- * mw8_calib_stream_lds: 256 blocks x 4 waves moving region_bytes (a
- *   multiple of 32 KiB, at most 1 GiB) per block, `passes` times, from
- *   global memory into LDS with 16-byte buffer_load ... lds, 8-16 KB in
- *   flight per wave.  shared = 1: block b reads region b % 8, so the 32
- *   blocks of an XCD share one region (L2-resident for a small region read
- *   several times; for a large one a lockstep stream in which each line is
- *   fetched once and requested 32 times together); shared = 0: block b
- *   reads region b.  buf holds region_bytes x (shared ? 8 : 256) bytes.
- */
-int64_t mw8_calib_sink_len(void);
-int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int64_t sink_len,
-                      mw8_stream_t stream);
-int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len,
-                   mw8_stream_t stream);
-int mw8_calib_stream_lds(const void* buf, int64_t region_bytes, int32_t passes, int32_t shared,
-                         int32_t* sink, int64_t sink_len, mw8_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -68,10 +68,6 @@ int rmsnorm_strided_bf16(const void*, int64_t, void*, int64_t, const void*, floa
 int linear_bf16_w8a8(const void*, int64_t, const int8_t*, const float*, const void*, void*, int64_t, int64_t,
                      int64_t, hipStream_t);
 int linear_bf16_supported(int64_t, int64_t, int64_t);
-int64_t calib_sink_len();
-int calib_mfma_i8(int, int, int32_t*, int64_t, hipStream_t);
-int calib_read(const void*, int64_t, int32_t*, int64_t, hipStream_t);
-int calib_stream_lds(const void*, int64_t, int, int, int32_t*, int64_t, hipStream_t);
 
 }  // namespace mw8
 
@@ -248,22 +244,6 @@ int mw8_rmsnorm_quant_bf16(const void* x, void* residual, const void* weight, fl
 int mw8_rmsnorm_strided_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, const void* weight, float eps,
                              int64_t G, int64_t inner, int64_t H, mw8_stream_t st) {
   MW8_ENTRY(mw8::rmsnorm_strided_bf16(x, ldx, y, ldy, weight, eps, G, inner, H, S(st)));
-}
-
-int64_t mw8_calib_sink_len(void) { return mw8::calib_sink_len(); }
-
-int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int64_t sink_len,
-                      mw8_stream_t st) {
-  MW8_ENTRY(mw8::calib_mfma_i8(random_operands, iters, sink, sink_len, S(st)));
-}
-
-int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, mw8_stream_t st) {
-  MW8_ENTRY(mw8::calib_read(buf, bytes, sink, sink_len, S(st)));
-}
-
-int mw8_calib_stream_lds(const void* buf, int64_t region_bytes, int32_t passes, int32_t shared, int32_t* sink,
-                         int64_t sink_len, mw8_stream_t st) {
-  MW8_ENTRY(mw8::calib_stream_lds(buf, region_bytes, passes, shared, sink, sink_len, S(st)));
 }
 
 }  // extern "C"

@@ -22,6 +22,14 @@
 //
 // All write one int per thread to `sink` so that nothing is optimised
 // away; the caller times the launches with events on the same stream.
+//
+// Built as its own library, libmw8_calib.so (C ABI in include/mw8_calib.h),
+// so that the product library carries no measurement surface; its error
+// state is its own (mw8_calib_last_error).
+#include <cstdarg>
+#include <cstdio>
+
+#include "mw8_calib.h"
 #include "mw8_common.h"
 
 namespace mw8 {
@@ -123,7 +131,26 @@ __global__ __launch_bounds__(256) void calib_stream_lds_kernel(const char* buf, 
   sink[blockIdx.x * 256 + threadIdx.x] = ring[threadIdx.x * 16];
 }
 
-}  // namespace
+thread_local char g_calib_error[512] = "";
+
+int calib_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_calib_error, sizeof(g_calib_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int calib_check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return calib_error(kErrLaunch, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return kOk;
+}
+
+#define CALIB_REQUIRE(cond, code, ...)                    \
+  do {                                                    \
+    if (!(cond)) return calib_error((code), __VA_ARGS__); \
+  } while (0)
 
 int64_t calib_sink_len() {
   return static_cast<int64_t>(kCalibBlocks) * kCalibThreads > static_cast<int64_t>(kReadBlocks) * kReadThreads
@@ -132,39 +159,62 @@ int64_t calib_sink_len() {
 }
 
 int calib_mfma_i8(int random_operands, int iters, int32_t* sink, int64_t sink_len, hipStream_t st) {
-  MW8_REQUIRE(sink != nullptr, kErrArg, "calib_mfma_i8: null sink");
-  MW8_REQUIRE(sink_len >= calib_sink_len(), kErrShape, "calib_mfma_i8: sink needs %lld int32",
+  CALIB_REQUIRE(sink != nullptr, kErrArg, "calib_mfma_i8: null sink");
+  CALIB_REQUIRE(sink_len >= calib_sink_len(), kErrShape, "calib_mfma_i8: sink needs %lld int32",
               (long long)calib_sink_len());
-  MW8_REQUIRE(iters > 0, kErrShape, "calib_mfma_i8: iters must be positive");
+  CALIB_REQUIRE(iters > 0, kErrShape, "calib_mfma_i8: iters must be positive");
   if (random_operands)
     hipLaunchKernelGGL(calib_mfma_kernel<1>, dim3(kCalibBlocks), dim3(kCalibThreads), 0, st, iters, sink);
   else
     hipLaunchKernelGGL(calib_mfma_kernel<0>, dim3(kCalibBlocks), dim3(kCalibThreads), 0, st, iters, sink);
-  return check_launch("calib_mfma_i8");
+  return calib_check_launch("calib_mfma_i8");
 }
 
 int calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, hipStream_t st) {
-  MW8_REQUIRE(buf != nullptr && sink != nullptr, kErrArg, "calib_read: null pointer");
-  MW8_REQUIRE(bytes > 0 && bytes % 16 == 0, kErrShape, "calib_read: bytes must be a positive multiple of 16");
-  MW8_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15u) == 0, kErrAlign, "calib_read: 16-byte alignment");
-  MW8_REQUIRE(sink_len >= calib_sink_len(), kErrShape, "calib_read: sink needs %lld int32",
+  CALIB_REQUIRE(buf != nullptr && sink != nullptr, kErrArg, "calib_read: null pointer");
+  CALIB_REQUIRE(bytes > 0 && bytes % 16 == 0, kErrShape, "calib_read: bytes must be a positive multiple of 16");
+  CALIB_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15u) == 0, kErrAlign, "calib_read: 16-byte alignment");
+  CALIB_REQUIRE(sink_len >= calib_sink_len(), kErrShape, "calib_read: sink needs %lld int32",
               (long long)calib_sink_len());
   hipLaunchKernelGGL(calib_read_kernel, dim3(kReadBlocks), dim3(kReadThreads), 0, st,
                      static_cast<const v4i*>(buf), bytes / 16, sink);
-  return check_launch("calib_read");
+  return calib_check_launch("calib_read");
 }
 
 int calib_stream_lds(const void* buf, int64_t region_bytes, int passes, int shared, int32_t* sink,
                      int64_t sink_len, hipStream_t st) {
-  MW8_REQUIRE(buf != nullptr && sink != nullptr, kErrArg, "calib_stream_lds: null pointer");
-  MW8_REQUIRE(region_bytes >= 32768 && region_bytes % 32768 == 0 && region_bytes <= (int64_t{1} << 30), kErrShape,
+  CALIB_REQUIRE(buf != nullptr && sink != nullptr, kErrArg, "calib_stream_lds: null pointer");
+  CALIB_REQUIRE(region_bytes >= 32768 && region_bytes % 32768 == 0 && region_bytes <= (int64_t{1} << 30), kErrShape,
               "calib_stream_lds: region_bytes must be a multiple of 32 KiB, at most 1 GiB");
-  MW8_REQUIRE(passes >= 1 && (shared == 0 || shared == 1), kErrArg, "calib_stream_lds: passes >= 1, shared 0 or 1");
-  MW8_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15u) == 0, kErrAlign, "calib_stream_lds: 16-byte alignment");
-  MW8_REQUIRE(sink_len >= static_cast<int64_t>(kStreamBlocks) * 256, kErrShape, "calib_stream_lds: sink too short");
+  CALIB_REQUIRE(passes >= 1 && (shared == 0 || shared == 1), kErrArg, "calib_stream_lds: passes >= 1, shared 0 or 1");
+  CALIB_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15u) == 0, kErrAlign, "calib_stream_lds: 16-byte alignment");
+  CALIB_REQUIRE(sink_len >= static_cast<int64_t>(kStreamBlocks) * 256, kErrShape, "calib_stream_lds: sink too short");
   hipLaunchKernelGGL(calib_stream_lds_kernel, dim3(kStreamBlocks), dim3(256), 0, st, static_cast<const char*>(buf),
                      region_bytes, passes, shared, sink);
-  return check_launch("calib_stream_lds");
+  return calib_check_launch("calib_stream_lds");
 }
 
+}  // namespace
 }  // namespace mw8
+
+extern "C" {
+
+const char* mw8_calib_last_error(void) { return mw8::g_calib_error; }
+
+int64_t mw8_calib_sink_len(void) { return mw8::calib_sink_len(); }
+
+int mw8_calib_mfma_i8(int32_t random_operands, int32_t iters, int32_t* sink, int64_t sink_len,
+                      mw8_stream_t st) {
+  return mw8::calib_mfma_i8(random_operands, iters, sink, sink_len, static_cast<hipStream_t>(st));
+}
+
+int mw8_calib_read(const void* buf, int64_t bytes, int32_t* sink, int64_t sink_len, mw8_stream_t st) {
+  return mw8::calib_read(buf, bytes, sink, sink_len, static_cast<hipStream_t>(st));
+}
+
+int mw8_calib_stream_lds(const void* buf, int64_t region_bytes, int32_t passes, int32_t shared, int32_t* sink,
+                         int64_t sink_len, mw8_stream_t st) {
+  return mw8::calib_stream_lds(buf, region_bytes, passes, shared, sink, sink_len, static_cast<hipStream_t>(st));
+}
+
+}  // extern "C"

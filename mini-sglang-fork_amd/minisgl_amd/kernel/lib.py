@@ -18,6 +18,8 @@ from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
 
 LIB_NAME = "libmw8.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# the benchmark's measurement kernels (include/mw8_calib.h), a library of their own
+CALIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmw8_calib.so")
 
 _P = c_void_p
 _I32 = c_int32
@@ -79,10 +81,6 @@ SIGNATURES = {
     ),
     "mw8_rmsnorm_quant_bf16": (ctypes.c_int, [_P, _P, _P, c_float, _I64, _I64, _P, _P, _P, _P]),
     "mw8_rmsnorm_strided_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _P, c_float, _I64, _I64, _I64, _P]),
-    "mw8_calib_sink_len": (_I64, []),
-    "mw8_calib_mfma_i8": (ctypes.c_int, [_I32, _I32, _P, _I64, _P]),
-    "mw8_calib_read": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
-    "mw8_calib_stream_lds": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _I64, _P]),
 }
 
 ERROR_NAMES = {
@@ -122,4 +120,33 @@ def check(rc: int) -> None:
         raise MW8Error(rc, msg)
 
 
-__all__ = ["load", "check", "MW8Error", "LIB_PATH", "SIGNATURES", "c_float"]
+# name -> (restype, argtypes); must match include/mw8_calib.h
+CALIB_SIGNATURES = {
+    "mw8_calib_last_error": (ctypes.c_char_p, []),
+    "mw8_calib_sink_len": (_I64, []),
+    "mw8_calib_mfma_i8": (ctypes.c_int, [_I32, _I32, _P, _I64, _P]),
+    "mw8_calib_read": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
+    "mw8_calib_stream_lds": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _I64, _P]),
+}
+
+
+@functools.lru_cache(maxsize=None)
+def load_calib(path: str = CALIB_PATH) -> ctypes.CDLL:
+    """Load libmw8_calib.so (benchmark measurement kernels only)."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} not found: build the HIP libraries first")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in CALIB_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def check_calib(rc: int) -> None:
+    if rc != 0:
+        raise MW8Error(rc, load_calib().mw8_calib_last_error().decode(errors="replace"))
+
+
+__all__ = ["load", "check", "load_calib", "check_calib", "MW8Error", "LIB_PATH", "CALIB_PATH", "SIGNATURES",
+           "CALIB_SIGNATURES", "c_float"]

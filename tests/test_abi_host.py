@@ -15,10 +15,11 @@ from minisgl_amd.kernel import lib as mw8lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mw8.h")
+CALIB_HEADER = os.path.join(ROOT, "include", "mw8_calib.h")
 
 
-def _declared():
-    text = open(HEADER).read()
+def _declared(path=HEADER):
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(mw8_[a-z0-9_]+)\s*\(", text)))
 
@@ -43,6 +44,22 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_binding_covers_header():
     assert set(_declared()) == set(mw8lib.SIGNATURES)
+
+
+def test_measurement_kernels_are_a_library_of_their_own():
+    """The benchmark's measurement kernels (include/mw8_calib.h) are exported
+    by libmw8_calib.so and bound by kernel/lib.py, and the product library
+    exports none of them."""
+    names = _declared(CALIB_HEADER)
+    assert set(names) == set(mw8lib.CALIB_SIGNATURES)
+    calib = ctypes.CDLL(mw8lib.CALIB_PATH)
+    assert [n for n in names if not hasattr(calib, n)] == []
+    product = ctypes.CDLL(mw8lib.LIB_PATH)
+    assert [n for n in names if hasattr(product, n)] == []
+    clib = mw8lib.load_calib()
+    assert clib.mw8_calib_sink_len() == 2048 * 256  # the read grid, the larger of the kernels
+    assert clib.mw8_calib_read(None, 1 << 20, None, 0, None) == 1  # MW8_ERR_ARG before any launch
+    assert b"null pointer" in clib.mw8_calib_last_error()
 
 
 def test_version_and_pure_host_helpers(lib):
