@@ -47,7 +47,9 @@ _WORKSPACE: Dict[torch.device, torch.Tensor] = {}
 
 
 def reserve_gemm_workspace(device: torch.device) -> torch.Tensor:
-    """The GEMM workspace of ``device``: one buffer of
+    """A caller-side GEMM workspace for ``device``, for the entry points
+    that take one (the int32 parity hook ``gemm_w8a8_i32``, and C callers
+    of ``mw8_gemm_w8a8_bf16``; ``gemm_w8a8`` needs none): one buffer of
     ``mw8_gemm_workspace_max_bytes()`` (the bound over every shape and
     tiling, 64 MiB on a 256-CU MI355X), allocated on first use and never
     grown, replaced or freed.  So a HIP graph that captured a GEMM keeps a
@@ -243,13 +245,18 @@ def gemm_w8a8(
     _need(y.dtype == torch.bfloat16 and y.shape == (M, N) and y.is_contiguous(), "bad out buffer")
     if M == 0:
         return y
-    ws = gemm_workspace(M, N, K, q.device)
-    check(
-        load().mw8_gemm_w8a8_bf16(
-            _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K,
-            _ptr(ws), 0 if ws is None else ws.numel(), _stream(q),
+    # The allocation-free entry: the K split's int32 partial tiles go to the
+    # library's static per-device scratch (the same 64 MiB bound as a
+    # reserved workspace, the same sharing rule: calls on one stream share
+    # it, concurrent streams must not), so no workspace tensor is held
+    # beside it.  It takes the current device's scratch: q's device is
+    # made current for the call.
+    with torch.cuda.device(q.device):
+        check(
+            load().mw8_gemm_w8a8_bf16_noalloc(
+                _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K, _stream(q),
+            )
         )
-    )
     return y
 
 

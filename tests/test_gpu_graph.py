@@ -5,8 +5,9 @@ into the static buffers (:152-158).  Every replay is checked against the
 oracle (dense: bit-exact on the replayed inputs; MoE: bit-identical to the
 eager layer on the same inputs, and the eager layer against the oracle's
 end-to-end chain), with eager work and synchronizations between replays.
-No kernel here records a memset, and the GEMM workspace is one reserved
-buffer that never moves, so captured pointers stay valid."""
+No kernel here records a memset, and the dense GEMM's K-split memory is the
+library's static per-device scratch, which never moves, so captured pointers
+stay valid."""
 
 import numpy as np
 import pytest
@@ -83,10 +84,11 @@ def test_linear_dropins_graph_replay(bs):
 
 def test_graphs_survive_later_shapes():
     """Two captures of the o_proj drop-in at M = 40 and M = 100 (tile core
-    with a K split through the workspace), then eager calls at larger and
-    other sizes (M = 4096, 300, 2080), then both graphs replayed on fresh
-    inputs: still bit-exact (the workspace is reserved once at its bound and
-    never replaced, so no captured pointer dangles)."""
+    with a K split through the library's static scratch), then eager calls
+    at larger and other sizes (M = 4096, 300, 2080), then both graphs
+    replayed on fresh inputs: still bit-exact (the scratch sits at one
+    address per device for the life of the process, so no captured pointer
+    dangles)."""
     announce("graphs survive later shapes")
     gen = torch.Generator().manual_seed(77)
     layer = _dense_layers(gen)["o_proj"]
