@@ -10,6 +10,12 @@ int8 MFMA GEMM with the scale/bias epilogue, both HIP kernels.
 This build runs on one GPU, so every layer is built at tensor-parallel
 size 1: local sizes equal full sizes and the row-parallel all-reduce
 (:104-105, :125-126) is absent.
+
+Any input size K works, as with ``F.linear``: the GEMM kernels take K in
+steps of 16 bytes, so for other K the layer runs the GEMM over the weight
+zero-padded to the next multiple of 16 (a copy cached per weight tensor)
+and the quantized rows with a zero tail.  Zero columns add nothing to an
+int32 dot product, so the output is the unpadded product bit for bit.
 """
 
 from __future__ import annotations
@@ -28,6 +34,10 @@ def quantize_weight(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     ``weight[n, k] = rint(w[n, k] / weight_scale[n])`` (the same per-row
     kernel as the activation quantizer)."""
     return quant_per_token(w.contiguous())
+
+
+def _k16(K: int) -> int:
+    return (K + 15) // 16 * 16
 
 
 class _LinearW8A8Impl(BaseOP):
@@ -51,7 +61,25 @@ class _LinearW8A8Impl(BaseOP):
 
     def forward_quantized(self, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
         """GEMM + epilogue on an already-quantized input (q int8 [M, K], s fp32 [M])."""
+        K = q.shape[1]
+        if K % 16 != 0:
+            qp = torch.empty((q.shape[0], _k16(K)), dtype=torch.int8, device=q.device)
+            qp[:, K:].zero_()
+            qp[:, :K].copy_(q)
+            return gemm_w8a8(qp, s, self._padded_weight(), self.weight_scale, self.bias)
         return gemm_w8a8(q, s, self.weight, self.weight_scale, self.bias)
+
+    def _padded_weight(self) -> torch.Tensor:
+        """``weight`` zero-padded to a multiple of 16 columns, cached per
+        weight tensor and version (a new or modified weight rebuilds it)."""
+        w = self.weight
+        key = (w.data_ptr(), w._version, w.shape)
+        if getattr(self, "_wpad_key", None) != key:
+            N, K = w.shape
+            wp = torch.zeros((N, _k16(K)), dtype=torch.int8, device=w.device)
+            wp[:, :K].copy_(w)
+            self._wpad, self._wpad_key = wp, key
+        return self._wpad
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
@@ -68,6 +96,11 @@ class _LinearW8A8Impl(BaseOP):
         ):
             # decode batch: quantization inside the GEMM launch (one kernel)
             y = linear_bf16_w8a8(x2, self.weight, self.weight_scale, self.bias)
+        elif K % 16 != 0:  # quantize into rows with a zero tail up to the GEMM's K step
+            qp = torch.empty((M, _k16(K)), dtype=torch.int8, device=x2.device)
+            qp[:, K:].zero_()
+            _, s = quant_per_token(x2, out=qp[:, :K])
+            y = gemm_w8a8(qp, s, self._padded_weight(), self.weight_scale, self.bias)
         else:
             q, s = quant_per_token(x2)
             y = self.forward_quantized(q, s)

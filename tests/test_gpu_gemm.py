@@ -206,6 +206,36 @@ def test_linear_layers_drop_in():
             assert bf16_bits_equal(y, y_ref).all()
 
 
+@pytest.mark.parametrize("K", [8, 100, 1000, 4100])
+def test_linear_layer_any_k(K):
+    """K off the GEMM's 16-byte step, as F.linear takes it: the drop-in
+    pads the weight (a cached copy) and the quantized rows with zeros, and
+    the output equals the oracle's unpadded product bit for bit at decode
+    and prefill batch sizes, with bias, after a weight reload (the cached
+    copy is rebuilt), and through forward_quantized."""
+    announce(f"linear any K={K}")
+    gen = torch.Generator().manual_seed(K)
+    N = 136
+    layer = LinearReplicated(K, N, has_bias=True)
+    for trial in range(2):  # the second load replaces the weight: the padded copy must follow
+        sd = {
+            "weight": torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8).to(DEV),
+            "weight_scale": (torch.rand(N, generator=gen) * 1e-2 + 1e-4).to(DEV),
+            "bias": torch.randn(N, generator=gen).to(torch.bfloat16).to(DEV),
+        }
+        layer.load_state_dict(dict(sd))
+        args = (sd["weight"].cpu().numpy(), sd["weight_scale"].cpu().numpy(), f32(sd["bias"]))
+        for M in (1, 3, 64, 300):
+            x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+            y = layer.forward(x.to(DEV))
+            y_ref, *_ = orc.linear_w8a8(f32(x), *args)
+            eq = bf16_bits_equal(y, y_ref)
+            assert eq.all(), f"trial {trial} M={M}: {(~eq).sum()} outputs differ"
+        q, s = quant_per_token(x.to(DEV))
+        y = layer.forward_quantized(q, s)
+        assert bf16_bits_equal(y, y_ref).all(), "forward_quantized"
+
+
 def _tuning_count(kind):
     from minisgl_amd.kernel.lib import load
 
