@@ -110,7 +110,8 @@ int mw8_rmsnorm_strided_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, c
                              float eps, int64_t G, int64_t inner, int64_t H, mw8_stream_t stream);
 
 /*
- * Tile-configuration override, process-wide: decode_cfg indexes the dense
+ * Tile-configuration override of the calling thread (other threads keep
+ * the automatic choice; a thread starts on it): decode_cfg indexes the dense
  * decode-core configurations (forcing one keeps M <= 64 on the decode
  * core), tile_cfg the dense tile-core ones (forcing one takes M > 32 to the
  * tile core), moe_cfg the grouped (fused-MoE) configurations (for block

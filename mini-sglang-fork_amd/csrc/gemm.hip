@@ -46,10 +46,12 @@ namespace {
 
 constexpr int64_t kDecodeMaxM = 64;
 
-// Tuning override (-1 = automatic); set through mw8_set_tuning.
-std::atomic<int> g_decode_cfg{-1};
-std::atomic<int> g_tile_cfg{-1};
-std::atomic<int> g_moe_cfg{-1};
+// Tuning override (-1 = automatic), per calling thread: set through
+// mw8_set_tuning, it changes the choice for the calls of the thread that set
+// it and leaves every other thread on the automatic choice.
+thread_local int g_decode_cfg = -1;
+thread_local int g_tile_cfg = -1;
+thread_local int g_moe_cfg = -1;
 
 // ------------------------------------------------------------------ decode
 // core 0: decode_gemm_kernel (RG 16-row groups per block, WAVES waves, D = U
@@ -149,7 +151,7 @@ int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
 template <int EPI>
 int dispatch_decode(const GemmArgs& g, hipStream_t st) {
   const int tg = static_cast<int>((g.M + 15) / 16);
-  int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+  int cfg = g_decode_cfg;
   if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(g.M, g.N, g.K);
   switch (tg) {
     case 1: return decode_by_cfg<1, EPI>(cfg, g, st);
@@ -404,7 +406,7 @@ bool tile_cfg_fits(int cfg, int64_t M, int64_t N, int64_t K) {
 }
 
 int select_tile_cfg(int64_t M, int64_t N, int64_t K) {
-  const int cfg = g_tile_cfg.load(std::memory_order_relaxed);
+  const int cfg = g_tile_cfg;
   if (!tile_cfg_fits(cfg, M, N, K)) return default_tile_cfg(M, N, K);
   return cfg;
 }
@@ -526,7 +528,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // kXQMaxStages K stages of 256 bytes.
 int xq_decode_cfg(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > kXQMaxTokens || N < 1 || K < 16 || K % 16 != 0) return -1;
-  int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+  int cfg = g_decode_cfg;
   if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
   const DecodeCfg& c = kDecodeCfgs[cfg];
   if (c.core != 1) return -1;
@@ -541,8 +543,8 @@ int xq_decode_cfg(int64_t M, int64_t N, int64_t K) {
 // configuration is forced; a forced tile configuration takes it for any K.
 bool use_tile_path(int64_t M, int64_t K) {
   if (M > kDecodeMaxM) return true;
-  if (M <= 32 || g_decode_cfg.load(std::memory_order_relaxed) >= 0) return false;
-  return K % 128 == 0 || g_tile_cfg.load(std::memory_order_relaxed) >= 0;
+  if (M <= 32 || g_decode_cfg >= 0) return false;
+  return K % 128 == 0 || g_tile_cfg >= 0;
 }
 
 int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
@@ -616,9 +618,9 @@ int linear_bf16_w8a8(const void* x, int64_t ldx, const int8_t* W, const float* s
 }
 
 void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
-  g_decode_cfg.store(decode_cfg, std::memory_order_relaxed);
-  g_tile_cfg.store(tile_cfg, std::memory_order_relaxed);
-  g_moe_cfg.store(moe_cfg, std::memory_order_relaxed);
+  g_decode_cfg = decode_cfg;
+  g_tile_cfg = tile_cfg;
+  g_moe_cfg = moe_cfg;
 }
 
 int tuning_count(int kind);
@@ -740,7 +742,7 @@ int launch_grouped_epi(const GemmArgs& g, unsigned blocks, int bm, hipStream_t s
     if (bm == 64) return launch_tile<64, 128, 128, 2, 2, EPI, SortedRows>(g, grid, st);
     return launch_tile<128, 128, 128, 2, 2, EPI, SortedRows>(g, grid, st);
   }
-  int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  int cfg = g_moe_cfg;
   if (cfg < 0 || cfg >= kNumMoeCfgs) cfg = default_moe_cfg(g);
   if (cfg == 1 && g.num_experts < kPersistMaxSlots)
     return launch_grouped_persist<128, 256, 64, 2, 2, 3, EPI, 2>(g, st);
@@ -774,7 +776,7 @@ constexpr int kNumSmallMoeCfgs = 3;
 template <int EPI>
 int launch_grouped_small_epi(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   if (g.align_bsz == 32) return launch_grouped_ring<1, 3, EPI, 2>(g, blocks, st);  // two token groups
-  const int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  const int cfg = g_moe_cfg;
   switch (cfg) {
     case 1: return launch_grouped_ring<2, 3, EPI>(g, blocks, st);
     case 2: return launch_grouped_ring<1, 4, EPI>(g, blocks, st);
@@ -789,7 +791,7 @@ int launch_grouped_small_epi(const GemmArgs& g, unsigned blocks, hipStream_t st)
 const char* gemm_kernel_name(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return "";
   if (!use_tile_path(M, K)) {
-    int cfg = g_decode_cfg.load(std::memory_order_relaxed);
+    int cfg = g_decode_cfg;
     if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
     return kDecodeCfgs[cfg].core == 0 ? "decode_gemm_kernel" : "decode3_gemm_kernel";
   }
@@ -876,7 +878,7 @@ int launch_moe_gemm_sum(const GemmArgs& g, int64_t max_sorted, hipStream_t st, b
 // Gate|up GEMM with the gated activation fused (persistent chunk walk, the
 // moe cfg 1 tiling): out [rows, N/2] = act(gate) * up, bf16.
 int launch_grouped_act(const GemmArgs& g, int act, hipStream_t st) {
-  const int cfg = g_moe_cfg.load(std::memory_order_relaxed);
+  const int cfg = g_moe_cfg;
   if (cfg == 2 && 256 % g.align_bsz == 0 && stream_fits(g, g.num_valid, g.N / 2)) {
     if (act == 0) return launch_stream<true, 0>(g, static_cast<unsigned>(device_cus()), st);
     return launch_stream<true, 1>(g, static_cast<unsigned>(device_cus()), st);

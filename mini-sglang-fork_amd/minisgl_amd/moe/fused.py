@@ -21,6 +21,16 @@ All counts stay on the device (no host sync), so the call can be captured
 in a HIP graph.  For the smallest decode batches (M * k <= 32) the backend
 runs steps 1-3 as one launch (``moe_prepare_small``), otherwise steps 1 and
 3 as one launch (``moe_route_quant``), with the same outputs bit for bit.
+
+Any hidden size H and intermediate size I: the int8 kernels contract over
+multiples of 16 bytes, so a layer whose H or I is not one runs on copies
+zero-padded to the next multiple of 16 (``padded_experts_w8a8``): hidden
+columns past H, gate and up rows past I and down columns past I are zero.
+Zero terms leave every int32 sum as it is, a zero gate and up row gives
+``act(0) * 0 = 0`` (silu and gelu), which leaves each row's amax, scale and
+quantized values as they are, and the result is the unpadded problem's bit
+for bit (the reference's Triton kernel masks its K tail instead,
+python/minisgl/kernel/triton/fused_moe.py:159-174).
 """
 
 from __future__ import annotations
@@ -109,6 +119,45 @@ def try_get_optimal_moe_config(w1_shape, w2_shape, top_k: int, M: int) -> Dict[s
     return get_default_config(M, E, N, w1_shape[2], top_k)
 
 
+def _up16(n: int) -> int:
+    return -(-n // 16) * 16
+
+
+def padded_experts_w8a8(w1, w1_scale, w2, w2_scale):
+    """(w1, w1_scale, w2, w2_scale) with H and I zero-padded to multiples of
+    16: w1 [E, 2 I16, H16] with gate rows at [0, I) and up rows at
+    [I16, I16 + I), w1_scale [E, 2 I16], w2 [E, H16, I16], w2_scale
+    [E, H16]; padded rows get a zero scale.  The copies are cached on ``w1``
+    and rebuilt when any of the four tensors is replaced or written in place
+    (data pointer and version counter), so a captured graph replays on the
+    copies its warm-up call made."""
+    E, N, H = w1.shape
+    I = N // 2
+    H16, I16 = _up16(H), _up16(I)
+    key = (H16, I16) + tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in (w1, w1_scale, w2, w2_scale))
+    hit = getattr(w1, "_mw8_padded", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    w1p = w1.new_zeros((E, 2, I16, H16))
+    w1p[:, :, :I, :H] = w1.view(E, 2, I, H)
+    s1p = w1_scale.new_zeros((E, 2, I16))
+    s1p[:, :, :I] = w1_scale.reshape(E, 2, I)
+    w2p = w2.new_zeros((E, H16, I16))
+    w2p[:, :H, :I] = w2
+    s2p = w2_scale.new_zeros((E, H16))
+    s2p[:, :H] = w2_scale.reshape(E, H)
+    out = (w1p.view(E, 2 * I16, H16), s1p.view(E, 2 * I16), w2p, s2p)
+    w1._mw8_padded = (key, out)
+    return out
+
+
+def _padded_hidden(hidden_states: torch.Tensor) -> torch.Tensor:
+    M, H = hidden_states.shape
+    hp = hidden_states.new_zeros((M, _up16(H)))
+    hp[:, :H] = hidden_states
+    return hp
+
+
 def fused_experts_impl_w8a8(
     hidden_states: torch.Tensor,
     w1: torch.Tensor,
@@ -130,6 +179,13 @@ def fused_experts_impl_w8a8(
     M, H = hidden_states.shape
     E, N, _ = w1.shape
     k = topk_ids.shape[1]
+    if H % 16 != 0 or (N // 2) % 16 != 0:
+        hp = _padded_hidden(hidden_states)
+        w1p, s1p, w2p, s2p = padded_experts_w8a8(w1, w1_scale, w2, w2_scale)
+        fused_experts_impl_w8a8(
+            hp, w1p, s1p, w2p, s2p, topk_weights, topk_ids, activation, apply_router_weight_on_input
+        )
+        return hidden_states.copy_(hp[:, :H])
     config = functools.partial(try_get_optimal_moe_config, w1.shape, w2.shape, k)(M)
     bsz = config["BLOCK_SIZE_M"]
 
@@ -230,18 +286,27 @@ class FusedMoeW8A8(BaseMoeBackend):
             raise ValueError("the W8A8 MoE backend needs w1_scale and w2_scale")
         M, H = hidden_states.shape
         E = w1.shape[0]
-        # int8 GEMM operand granularity: both contraction sizes (H for GEMM1,
-        # I for GEMM2) must be multiples of 16
-        if H % 16 != 0 or w2.shape[2] % 16 != 0 or w1.shape[1] != 2 * w2.shape[2]:
+        if w1.shape[1] != 2 * w2.shape[2] or w2.shape[1] != H:
             raise ValueError(
-                f"W8A8 MoE needs hidden and intermediate sizes that are multiples of 16 and "
-                f"w1 [E, 2I, H] / w2 [E, H, I] (got w1 {tuple(w1.shape)}, w2 {tuple(w2.shape)})"
+                f"W8A8 MoE takes w1 [E, 2I, H] and w2 [E, H, I] "
+                f"(got w1 {tuple(w1.shape)}, w2 {tuple(w2.shape)}, hidden size {H})"
             )
         # the contract fused_experts_impl_w8a8 asserts, for the fast paths too
         assert H == w1.shape[2], "Hidden size mismatch"
         assert hidden_states.dtype == torch.bfloat16, "W8A8 MoE takes bf16 activations"
         assert w1.dtype == torch.int8 and w2.dtype == torch.int8, "W8A8 MoE takes int8 weights"
         assert w1.is_contiguous() and w2.is_contiguous(), "Expert weights must be contiguous"
+        if H % 16 != 0 or w2.shape[2] % 16 != 0:
+            # the int8 kernels contract over multiples of 16: run on zero-padded
+            # copies (same bits), then write the H real columns back in place
+            assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+            hp = _padded_hidden(hidden_states)
+            w1p, s1p, w2p, s2p = padded_experts_w8a8(w1, w1_scale, w2, w2_scale)
+            self.forward(
+                hp, w1p, w2p, gating_output, topk, renormalize, activation, apply_router_weight_on_input,
+                w1_scale=s1p, w2_scale=s2p,
+            )
+            return hidden_states.copy_(hp[:, :H])
         bsz = try_get_optimal_moe_config(w1.shape, w2.shape, topk, M)["BLOCK_SIZE_M"]
         contiguous = hidden_states.is_contiguous() and gating_output.is_contiguous()
         if (
@@ -297,5 +362,6 @@ __all__ = [
     "get_default_config",
     "try_get_optimal_moe_config",
     "fused_experts_impl_w8a8",
+    "padded_experts_w8a8",
     "FusedMoeW8A8",
 ]

@@ -94,6 +94,25 @@ def test_version_and_pure_host_helpers(lib):
     assert lib.mw8_gemm_workspace_bytes(32, 34816, 5120) == 0  # decode core
 
 
+def test_tuning_override_is_per_thread(lib):
+    """A tuning override changes the choice of the thread that set it only:
+    another thread, before and while it holds, sees the automatic tiling."""
+    import threading
+
+    auto = b"tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"
+    seen = []
+    lib.mw8_set_tuning(-1, 5, -1)
+    try:
+        assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) != auto
+        t = threading.Thread(target=lambda: seen.append(lib.mw8_gemm_kernel_name(8192, 34816, 5120)))
+        t.start()
+        t.join()
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
+    assert seen == [auto]
+    assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) == auto
+
+
 def test_moe_gemm_sum_supported_sizes(lib):
     """The fused down-projection + slot sum keeps its routing tables in LDS:
     every decode batch of config 3 (up to E = 128 tokens x top-8, sorted

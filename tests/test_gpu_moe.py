@@ -822,11 +822,14 @@ def test_fused_topk_marks_padded_tokens():
     assert set(s[s < 40].tolist()) == set(range(28))  # only the 7 x 4 unpadded pairs are placed
 
 
-def test_backend_rejects_unsupported_sizes():
+def test_backend_rejects_mismatched_shapes():
     be = create_moe_backend("fused_w8a8")
     h = torch.zeros(2, 40, dtype=torch.bfloat16, device=DEV)
-    w1 = torch.zeros(4, 64, 40, dtype=torch.int8, device=DEV)
     w2 = torch.zeros(4, 40, 32, dtype=torch.int8, device=DEV)
-    with pytest.raises(ValueError, match="multiples of 16"):
-        be.forward(h, w1, w2, torch.zeros(2, 4, device=DEV), 2, True,
-                   w1_scale=torch.ones(4, 64, device=DEV), w2_scale=torch.ones(4, 40, device=DEV))
+    for w1 in (torch.zeros(4, 60, 40, dtype=torch.int8, device=DEV),   # 60 rows for I = 32
+               torch.zeros(4, 64, 40, dtype=torch.int8, device=DEV)):
+        w2x = w2 if w1.shape[1] == 60 else torch.zeros(4, 48, 32, dtype=torch.int8, device=DEV)  # H 48 vs 40
+        with pytest.raises(ValueError, match=r"w1 \[E, 2I, H\] and w2 \[E, H, I\]"):
+            be.forward(h, w1, w2x, torch.zeros(2, 4, device=DEV), 2, True,
+                       w1_scale=torch.ones(4, w1.shape[1], device=DEV),
+                       w2_scale=torch.ones(4, w2x.shape[1], device=DEV))
