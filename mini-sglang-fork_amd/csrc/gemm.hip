@@ -57,7 +57,9 @@ thread_local int g_moe_cfg = -1;
 // core 0: decode_gemm_kernel (RG 16-row groups per block, WAVES waves, D = U
 // K steps per load batch); core 1: decode3_gemm_kernel over a CU-balanced
 // grid (a multiple of the CU count, each block up to 16 RG rows, D = ring
-// depth).
+// depth); core 2: decode_sx_gemm_kernel (up to 16 tokens, K % 256 == 0:
+// one block per CU, a wave per 16 rows of its range, a shared token ring;
+// waves from N, D = ring depth; other sizes take the automatic choice).
 struct DecodeCfg {
   int core, rg, waves, d;
 };
@@ -70,6 +72,8 @@ constexpr DecodeCfg kDecodeCfgs[] = {
     {1, 2, 4, 2},  // 5
     {1, 2, 4, 3},  // 6
     {1, 2, 8, 2},  // 7
+    {2, 1, 0, 3},  // 8: shared token ring, 3 stages
+    {2, 1, 0, 4},  // 9: shared token ring, 4 stages (3 past 9 waves: LDS)
 };
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
@@ -106,6 +110,52 @@ int launch_decode3_xq(const GemmArgs& g, hipStream_t st) {
   return kOk;
 }
 
+// core 2: one block per CU (a multiple of the CU count: every block at most
+// 16 x kSxMaxWaves rows), a wave per 16 rows of the widest block's range.
+constexpr int kSxMaxWaves = 12;
+
+bool sx_fits(int64_t M, int64_t K) { return M >= 1 && M <= 16 && K % 256 == 0; }
+
+void sx_plan(int64_t N, int& waves, int64_t& blocks) {
+  const int64_t cus = device_cus();
+  const int64_t per = cus * 16 * kSxMaxWaves;
+  blocks = cus * ((N + per - 1) / per);
+  waves = static_cast<int>(((N + blocks - 1) / blocks + 15) / 16);
+}
+
+template <int WAVES, int D, int EPI>
+int launch_decode_sx_w(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  constexpr int kD = (WAVES + 1) * D * kRingStage <= 163840 ? D : 3;
+  constexpr int kLds = (WAVES + 1) * kD * kRingStage;
+  constexpr auto kern = decode_sx_gemm_kernel<WAVES, kD, EPI>;
+  if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WAVES), kLds, st, g);
+  return kOk;
+}
+
+template <int D, int EPI>
+int launch_decode_sx(const GemmArgs& g, hipStream_t st) {
+  int waves = 0;
+  int64_t blocks = 0;
+  sx_plan(g.N, waves, blocks);
+  MW8_REQUIRE(blocks < (int64_t{1} << 31), kErrShape, "gemm: N=%lld too large", (long long)g.N);
+  const unsigned b = static_cast<unsigned>(blocks);
+  switch (waves) {
+    case 1: return launch_decode_sx_w<1, D, EPI>(g, b, st);
+    case 2: return launch_decode_sx_w<2, D, EPI>(g, b, st);
+    case 3: return launch_decode_sx_w<3, D, EPI>(g, b, st);
+    case 4: return launch_decode_sx_w<4, D, EPI>(g, b, st);
+    case 5: return launch_decode_sx_w<5, D, EPI>(g, b, st);
+    case 6: return launch_decode_sx_w<6, D, EPI>(g, b, st);
+    case 7: return launch_decode_sx_w<7, D, EPI>(g, b, st);
+    case 8: return launch_decode_sx_w<8, D, EPI>(g, b, st);
+    case 9: return launch_decode_sx_w<9, D, EPI>(g, b, st);
+    case 10: return launch_decode_sx_w<10, D, EPI>(g, b, st);
+    case 11: return launch_decode_sx_w<11, D, EPI>(g, b, st);
+    default: return launch_decode_sx_w<12, D, EPI>(g, b, st);
+  }
+}
+
 template <int TG, int EPI>
 int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
   switch (cfg) {
@@ -134,6 +184,16 @@ int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
 // (gate_up, 2176 row groups): 16-row blocks, 2 waves x 2 slots at one
 // token (30.6 us, 5.8 TB/s), one wave x 4 slots up to 8, 32-row blocks of
 // one wave x 4 slots at 17-32 tokens.
+// Wide N at 4-16 tokens (K % 256 == 0): the shared token ring (cfg 8):
+// the one-wave blocks re-read the token panel per 16 rows (gate_up at 8
+// tokens: 94 MB of token reads beside 178 MB of weights).  Same box, us,
+// best decode3 configuration -> cfg 8: N 34816, K 5120 at 4 / 8 / 12 / 16
+// tokens 31.7 / 34.2 / 37.5 / 40.6 -> 31.4 / 31.4 / 31.7 / 31.7; N 16384
+// 17.5 -> 16.7; N 51200 at 8 / 16 tokens 47.9 / 56.0 -> 45.1 / 46.1; at 2-3
+// tokens decode3 (29.5 / 31.1 against 30.5 / 31.2).  With K = 8192 and
+// the walk staggered per block, level with the K-split decode3 (N 25600:
+// 36.0 / 36.2; N 34816: 45.8 / 44.1) and ahead of the one-wave blocks
+// (55.7).
 // From 33 tokens on the token operand, read per wave through the texture
 // path, costs more than the weight stream: the register-streaming core
 // with 32 rows over 8 waves (cfg 0) wins, or 64 rows per block for very
@@ -141,6 +201,7 @@ int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
 int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
   const bool wide = N >= 16384;
   if (M == 1) return wide ? 3 : 6;
+  if (wide && M >= 4 && sx_fits(M, K)) return 8;
   if (M <= 8) return wide ? 2 : (K > 8192 ? 6 : 7);
   if (M <= 16) return 5;
   if (M <= 32) return wide ? 4 : 7;
@@ -153,6 +214,11 @@ int dispatch_decode(const GemmArgs& g, hipStream_t st) {
   const int tg = static_cast<int>((g.M + 15) / 16);
   int cfg = g_decode_cfg;
   if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(g.M, g.N, g.K);
+  if (kDecodeCfgs[cfg].core == 2) {
+    if (sx_fits(g.M, g.K))
+      return kDecodeCfgs[cfg].d == 4 ? launch_decode_sx<4, EPI>(g, st) : launch_decode_sx<3, EPI>(g, st);
+    cfg = default_decode_cfg(g.M, g.N, g.K);
+  }
   switch (tg) {
     case 1: return decode_by_cfg<1, EPI>(cfg, g, st);
     case 2: return decode_by_cfg<2, EPI>(cfg, g, st);
@@ -793,6 +859,10 @@ const char* gemm_kernel_name(int64_t M, int64_t N, int64_t K) {
   if (!use_tile_path(M, K)) {
     int cfg = g_decode_cfg;
     if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
+    if (kDecodeCfgs[cfg].core == 2) {
+      if (sx_fits(M, K)) return "decode_sx_gemm_kernel";
+      cfg = default_decode_cfg(M, N, K);
+    }
     return kDecodeCfgs[cfg].core == 0 ? "decode_gemm_kernel" : "decode3_gemm_kernel";
   }
   const int cfg = select_tile_cfg(M, N, K);

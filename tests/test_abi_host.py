@@ -141,7 +141,7 @@ def test_workspace_bound_and_tuning_counts(lib):
     # the allocation-free entry's static scratch (64 MiB) holds every plan on 256 CUs
     assert mx <= 64 << 20
     counts = [lib.mw8_tuning_count(k) for k in range(4)]
-    assert counts == [8, 13, 3, 3] and lib.mw8_tuning_count(9) == 0
+    assert counts == [10, 13, 3, 3] and lib.mw8_tuning_count(9) == 0
     worst = 0
     try:
         for tile in range(-1, counts[1]):
@@ -369,8 +369,10 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
         (17408, 5120): [r64, sq, wide, wide],
     }
     for (K, N), names in expect.items():
-        for M in (1, 8):
-            assert lib.mw8_gemm_kernel_name(M, N, K) == b"decode3_gemm_kernel", (M, N, K)
+        assert lib.mw8_gemm_kernel_name(1, N, K) == b"decode3_gemm_kernel", (1, N, K)
+        # 8 tokens: the shared token ring for the wide gate_up, decode3 otherwise
+        want8 = b"decode_sx_gemm_kernel" if N >= 16384 else b"decode3_gemm_kernel"
+        assert lib.mw8_gemm_kernel_name(8, N, K) == want8, (8, N, K)
         for M, name in zip((64, 512, 4096, 8192), names):
             assert lib.mw8_gemm_kernel_name(M, N, K).decode() == name, (M, N, K)
 

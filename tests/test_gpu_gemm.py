@@ -285,7 +285,10 @@ def test_gemm_every_tile_config(M, K, N, bias):
      (1, 1328, 200), (8, 1328, 200), (40, 1328, 200),  # K % 64 == 48: partial last step
      (3, 4160, 72), (16, 4160, 72),  # 65 steps: several pipelined batches per wave
      # CU-balanced grids: uneven row ranges of 1-32 rows per block
-     (1, 1344, 5000), (16, 1344, 8200), (32, 2048, 4100), (7, 1024, 16400)],
+     (1, 1344, 5000), (16, 1344, 8200), (32, 2048, 4100), (7, 1024, 16400),
+     # shared-token core (K % 256 == 0, up to 16 tokens): 9 waves with a ragged
+     # last wave, one wave of 2-3 rows, 10 waves (3 stages), a grid of 512 blocks
+     (8, 2048, 34820), (16, 512, 600), (2, 256, 40000), (4, 768, 49200)],
 )
 def test_gemm_every_decode_config(M, K, N):
     from minisgl_amd.kernel.lib import load
