@@ -57,7 +57,7 @@ thread_local int g_moe_cfg = -1;
 // core 0: decode_gemm_kernel (RG 16-row groups per block, WAVES waves, D = U
 // K steps per load batch); core 1: decode3_gemm_kernel over a CU-balanced
 // grid (a multiple of the CU count, each block up to 16 RG rows, D = ring
-// depth); core 2: decode_sx_gemm_kernel (up to 16 tokens, K % 256 == 0:
+// depth); core 2: decode_sx_gemm_kernel (up to 64 tokens, K % 256 == 0:
 // one block per CU, a wave per 16 rows of its range, a shared token ring;
 // waves from N, D = ring depth; other sizes take the automatic choice).
 struct DecodeCfg {
@@ -73,7 +73,7 @@ constexpr DecodeCfg kDecodeCfgs[] = {
     {1, 2, 4, 3},  // 6
     {1, 2, 8, 2},  // 7
     {2, 1, 0, 3},  // 8: shared token ring, 3 stages
-    {2, 1, 0, 4},  // 9: shared token ring, 4 stages (3 past 9 waves: LDS)
+    {2, 1, 0, 4},  // 9: shared token ring, 4 stages for up to 16 tokens (else 3)
 };
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
@@ -110,49 +110,57 @@ int launch_decode3_xq(const GemmArgs& g, hipStream_t st) {
   return kOk;
 }
 
-// core 2: one block per CU (a multiple of the CU count: every block at most
-// 16 x kSxMaxWaves rows), a wave per 16 rows of the widest block's range.
-constexpr int kSxMaxWaves = 12;
+// core 2: one block per CU (a multiple of the CU count), a wave per 16 rows
+// of the widest block's range, TG = ceil(M / 16) token groups; the LDS of
+// (WAVES + TG) D stages of 4 KB bounds the waves: WAVES + TG <= 40 / D.
+bool sx_fits(int64_t M, int64_t K) { return M >= 1 && M <= 64 && K % 256 == 0; }
 
-bool sx_fits(int64_t M, int64_t K) { return M >= 1 && M <= 16 && K % 256 == 0; }
+constexpr int sx_max_waves(int tg, int d) { return 40 / d - tg; }
 
-void sx_plan(int64_t N, int& waves, int64_t& blocks) {
+void sx_plan(int64_t N, int tg, int d, int& waves, int64_t& blocks) {
   const int64_t cus = device_cus();
-  const int64_t per = cus * 16 * kSxMaxWaves;
+  const int64_t per = cus * 16 * sx_max_waves(tg, d);
   blocks = cus * ((N + per - 1) / per);
   waves = static_cast<int>(((N + blocks - 1) / blocks + 15) / 16);
+  if (waves < tg) waves = tg;  // wave t issues token group t
 }
 
-template <int WAVES, int D, int EPI>
+template <int TG, int WAVES, int D, int EPI>
 int launch_decode_sx_w(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  constexpr int kD = (WAVES + 1) * D * kRingStage <= 163840 ? D : 3;
-  constexpr int kLds = (WAVES + 1) * kD * kRingStage;
-  constexpr auto kern = decode_sx_gemm_kernel<WAVES, kD, EPI>;
+  constexpr int kLds = (WAVES + TG) * D * kRingStage;
+  static_assert(kLds <= 163840, "LDS");
+  constexpr auto kern = decode_sx_gemm_kernel<TG, WAVES, D, EPI>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WAVES), kLds, st, g);
   return kOk;
 }
 
-template <int D, int EPI>
-int launch_decode_sx(const GemmArgs& g, hipStream_t st) {
+// the instance with `waves` waves among WAVES .. sx_max_waves(TG, D)
+template <int TG, int D, int EPI, int WAVES = TG>
+int launch_decode_sx_n(const GemmArgs& g, int waves, unsigned blocks, hipStream_t st) {
+  if constexpr (WAVES < sx_max_waves(TG, D)) {
+    if (waves > WAVES) return launch_decode_sx_n<TG, D, EPI, WAVES + 1>(g, waves, blocks, st);
+  }
+  return launch_decode_sx_w<TG, WAVES, D, EPI>(g, blocks, st);
+}
+
+template <int TG, int D, int EPI>
+int launch_decode_sx_tg(const GemmArgs& g, hipStream_t st) {
   int waves = 0;
   int64_t blocks = 0;
-  sx_plan(g.N, waves, blocks);
+  sx_plan(g.N, TG, D, waves, blocks);
   MW8_REQUIRE(blocks < (int64_t{1} << 31), kErrShape, "gemm: N=%lld too large", (long long)g.N);
-  const unsigned b = static_cast<unsigned>(blocks);
-  switch (waves) {
-    case 1: return launch_decode_sx_w<1, D, EPI>(g, b, st);
-    case 2: return launch_decode_sx_w<2, D, EPI>(g, b, st);
-    case 3: return launch_decode_sx_w<3, D, EPI>(g, b, st);
-    case 4: return launch_decode_sx_w<4, D, EPI>(g, b, st);
-    case 5: return launch_decode_sx_w<5, D, EPI>(g, b, st);
-    case 6: return launch_decode_sx_w<6, D, EPI>(g, b, st);
-    case 7: return launch_decode_sx_w<7, D, EPI>(g, b, st);
-    case 8: return launch_decode_sx_w<8, D, EPI>(g, b, st);
-    case 9: return launch_decode_sx_w<9, D, EPI>(g, b, st);
-    case 10: return launch_decode_sx_w<10, D, EPI>(g, b, st);
-    case 11: return launch_decode_sx_w<11, D, EPI>(g, b, st);
-    default: return launch_decode_sx_w<12, D, EPI>(g, b, st);
+  return launch_decode_sx_n<TG, D, EPI>(g, waves, static_cast<unsigned>(blocks), st);
+}
+
+// D = 4 stages for one token group (D = 3 otherwise: LDS)
+template <int EPI>
+int launch_decode_sx(const GemmArgs& g, int d, hipStream_t st) {
+  switch ((g.M + 15) / 16) {
+    case 1: return d == 4 ? launch_decode_sx_tg<1, 4, EPI>(g, st) : launch_decode_sx_tg<1, 3, EPI>(g, st);
+    case 2: return launch_decode_sx_tg<2, 3, EPI>(g, st);
+    case 3: return launch_decode_sx_tg<3, 3, EPI>(g, st);
+    default: return launch_decode_sx_tg<4, 3, EPI>(g, st);
   }
 }
 
@@ -198,10 +206,18 @@ int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
 // path, costs more than the weight stream: the register-streaming core
 // with 32 rows over 8 waves (cfg 0) wins, or 64 rows per block for very
 // wide N (cfg 1), which keeps fewer blocks re-reading the token panel.
+// Whether the shared token ring is the automatic choice at (M, N, K): wide
+// N at 4-64 tokens, one block per CU holding the widest row range.
+bool sx_default(int64_t M, int64_t N, int64_t K) {
+  if (N < 16384 || M < 4 || !sx_fits(M, K)) return false;
+  const int tg = static_cast<int>((M + 15) / 16);
+  return (N + device_cus() - 1) / device_cus() <= 16 * sx_max_waves(tg, 3);
+}
+
 int default_decode_cfg(int64_t M, int64_t N, int64_t K) {
   const bool wide = N >= 16384;
   if (M == 1) return wide ? 3 : 6;
-  if (wide && M >= 4 && sx_fits(M, K)) return 8;
+  if (sx_default(M, N, K)) return 8;
   if (M <= 8) return wide ? 2 : (K > 8192 ? 6 : 7);
   if (M <= 16) return 5;
   if (M <= 32) return wide ? 4 : 7;
@@ -215,8 +231,7 @@ int dispatch_decode(const GemmArgs& g, hipStream_t st) {
   int cfg = g_decode_cfg;
   if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(g.M, g.N, g.K);
   if (kDecodeCfgs[cfg].core == 2) {
-    if (sx_fits(g.M, g.K))
-      return kDecodeCfgs[cfg].d == 4 ? launch_decode_sx<4, EPI>(g, st) : launch_decode_sx<3, EPI>(g, st);
+    if (sx_fits(g.M, g.K)) return launch_decode_sx<EPI>(g, kDecodeCfgs[cfg].d, st);
     cfg = default_decode_cfg(g.M, g.N, g.K);
   }
   switch (tg) {
@@ -607,9 +622,10 @@ int xq_decode_cfg(int64_t M, int64_t N, int64_t K) {
 // tile core when K % 128 == 0 (its 64-row rings stream 1.2-2x faster than
 // the decode core at 33-64 tokens on MI355X), unless a decode
 // configuration is forced; a forced tile configuration takes it for any K.
-bool use_tile_path(int64_t M, int64_t K) {
+bool use_tile_path(int64_t M, int64_t N, int64_t K) {
   if (M > kDecodeMaxM) return true;
   if (M <= 32 || g_decode_cfg >= 0) return false;
+  if (g_tile_cfg < 0 && sx_default(M, N, K)) return false;  // the shared token ring
   return K % 128 == 0 || g_tile_cfg >= 0;
 }
 
@@ -638,7 +654,7 @@ int gemm_common(const int8_t* A, const float* sa, const int8_t* W, const float* 
   g.top_k = 1;
   g.staged_out = epi == kEpiBf16 && N % 8 == 0 && aligned16(out);
   int rc;
-  if (!use_tile_path(M, K)) {
+  if (!use_tile_path(M, N, K)) {
     rc = epi == kEpiBf16 ? dispatch_decode<kEpiBf16>(g, st) : dispatch_decode<kEpiI32>(g, st);
   } else {
     MW8_REQUIRE(ws == nullptr || aligned16(ws), kErrAlign, "gemm: workspace needs 16-byte alignment");
@@ -692,7 +708,7 @@ void set_tuning(int decode_cfg, int tile_cfg, int moe_cfg) {
 int tuning_count(int kind);
 
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || !use_tile_path(M, K)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || !use_tile_path(M, N, K)) return 0;
   const int cfg = select_tile_cfg(M, N, K);
   return cfg < kNumRingCfgs ? plan_split(M, N, K, kTileCfgs[cfg]).ws : 0;
 }
@@ -856,7 +872,7 @@ int launch_grouped_small_epi(const GemmArgs& g, unsigned blocks, hipStream_t st)
 // profiling aid: matches the kernel names of a trace).
 const char* gemm_kernel_name(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return "";
-  if (!use_tile_path(M, K)) {
+  if (!use_tile_path(M, N, K)) {
     int cfg = g_decode_cfg;
     if (cfg < 0 || cfg >= kNumDecodeCfgs) cfg = default_decode_cfg(M, N, K);
     if (kDecodeCfgs[cfg].core == 2) {

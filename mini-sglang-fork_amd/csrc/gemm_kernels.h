@@ -1697,35 +1697,39 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------
-// Dense decode core with a shared token ring (up to 16 tokens, K % 256 == 0)
+// Dense decode core with a shared token ring (up to 16 TG tokens, K % 256 == 0)
 // ------------------------------------------------------------------------
-// Wide N at a few tokens: one-wave decode3 blocks (nine per CU at N = 34816)
-// each read the whole token panel through the texture path, about half as
-// many bytes again as their weight rows (gate_up at 8 tokens: 94 MB of
-// token reads beside 178 MB of weights).  Here one block per CU (a grid of
-// a multiple of the CU count) owns a range of at most 16 WAVES weight rows:
-// wave w streams rows [n0 + 16 w, n0 + 16 w + 16) of the range through its
-// own LDS ring of D stages of 256 K bytes (the decode3 DMA and swizzle), and
-// the block's token rows come once per block into a shared ring of D
-// stages.  Wave 0 issues the token stages, each one stage later than its
-// own weight stage of the same index and after the barrier that frees the
-// slot, so its issue order is W(0) X(0) W(1) X(1) ...: at stage s wave 0
-// waits with D-1 weight and D-2 token stages still in flight, the other
-// waves with D-1 weight stages.  One barrier per stage makes token stage s
-// visible to every wave and frees the slot of stage s-1.  Token rows past
-// M and weight rows past the range read zeros through the buffer range
-// check (no traffic); stages past K are issued past the range as well, so
-// every stage issues the same number of operations.  Block b walks the K
-// stages from stage b n_st / G on: with every block at the same K offset,
-// a row stride of 8192 bytes put all the concurrent requests on the same
-// low address bits (MI355X, gate_up-wide N = 34816 at K = 8192 and 8
-// tokens: 59.2 us in lockstep, 45.8 us staggered; K = 5120 unchanged).
-template <int WAVES, int D, int EPI>
+// Wide N at a few dozen tokens: one-wave decode3 blocks (nine per CU at
+// N = 34816) each read the whole token panel through the texture path,
+// about half as many bytes again as their weight rows (gate_up at 8
+// tokens: 94 MB of token reads beside 178 MB of weights), and from 33
+// tokens the tile rings take over at a fraction of the weight stream's
+// rate.  Here one block per CU (a grid of a multiple of the CU count) owns
+// a range of at most 16 WAVES weight rows: wave w streams rows
+// [n0 + 16 w, n0 + 16 w + 16) of the range through its own LDS ring of D
+// stages of 256 K bytes (the decode3 DMA and swizzle), and the block's TG
+// groups of 16 token rows come once per block into a shared ring of D
+// stages.  Wave t < TG issues token group t of each stage, one stage
+// later than its own weight stage of the same index and after the barrier
+// that frees the slot, so its issue order is W(0) X(0) W(1) X(1) ...: at
+// stage s it waits with D-1 weight and D-2 token stages still in flight,
+// the other waves with D-1 weight stages.  One barrier per stage makes
+// token stage s visible to every wave and frees the slot of stage s-1.
+// Token rows past M and weight rows past the range read zeros through the
+// buffer range check (no traffic); stages past K are issued past the range
+// as well, so every stage issues the same number of operations.  Block b
+// walks the K stages from stage b n_st / G on: with every block at the
+// same K offset, a row stride of 8192 bytes put all the concurrent
+// requests on the same low address bits (MI355X, N = 34816 at K = 8192
+// and 8 tokens: 59.2 us in lockstep, 45.8 us staggered; K = 5120
+// unchanged).
+template <int TG, int WAVES, int D, int EPI>
 __global__ __launch_bounds__(64 * WAVES) void decode_sx_gemm_kernel(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  static_assert(D >= 2 && D <= 4 && WAVES >= 1, "shape");
-  constexpr int kOps = 4;  // 1 KB DMA instructions per weight or token stage
+  static_assert(TG >= 1 && TG <= 4 && WAVES >= TG && D >= 2 && D <= 4, "shape");
+  constexpr int kOps = 4;  // 1 KB DMA instructions per weight stage and per token group stage
   static_assert((2 * D - 3) * kOps < 64, "vmcnt range");
+  constexpr int kXStage = TG * kRingStage;  // TG groups of 16 rows x 256 bytes
   extern __shared__ __align__(16) unsigned char ring[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1742,14 +1746,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode_sx_gemm_kernel(GemmArgs g) 
       kBufferFlags);
   const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A)), 0, static_cast<int>(g.M * g.lda), kBufferFlags);
-  // instruction j of a stage fills LDS rows 4j .. 4j+3: lane l fills row
-  // 4j + l/16, chunk l%16, from global chunk (l%16) ^ (row & 15)
+  const bool x_issuer = wave < TG;  // wave t issues token group t (wave-uniform)
+  // instruction j of a stage fills LDS rows 4j .. 4j+3 of its 16-row slot:
+  // lane l fills row 4j + l/16, chunk l%16, from global chunk (l%16) ^ (row & 15)
   uint32_t w_off[4], x_off[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = 4 * j + (lane >> 4), c = (lane & 15) ^ (row & 15);
+    const int m = 16 * wave + row;  // token row of this wave's group (issuers only)
     w_off[j] = static_cast<uint32_t>(row * g.K + 16 * c);
-    x_off[j] = row < g.M ? static_cast<uint32_t>(row * g.lda + 16 * c) : 0x80000000u;
+    x_off[j] = x_issuer && m < g.M ? static_cast<uint32_t>(m * g.lda + 16 * c) : 0x80000000u;
   }
   const int n_st = static_cast<int>(g.K / 256);
   // block b walks the stages from b n_st / G on (wrapping)
@@ -1765,54 +1771,61 @@ __global__ __launch_bounds__(64 * WAVES) void decode_sx_gemm_kernel(GemmArgs g) 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff(st), 0,
                                                kStreamAux);
   };
-  auto issue_x = [&](int st) {  // wave 0 only
-    unsigned char* slot = xring + (st % D) * kRingStage;
+  auto issue_x = [&](int st) {  // waves < TG: token group `wave`
+    unsigned char* slot = xring + (st % D) * kXStage + wave * kRingStage;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(slot + j * 1024), 16, x_off[j], soff(st), 0, 0);
   };
-  v4i acc = v4i{0};
+  v4i acc[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) acc[tg] = v4i{0};
   auto consume = [&](int st) {
     const unsigned char* ws = wring + (st % D) * kRingStage;
-    const unsigned char* xs = xring + (st % D) * kRingStage;
+    const unsigned char* xs = xring + (st % D) * kXStage;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int off = r16 * 256 + 16 * ((4 * kb + grp) ^ r16);
       const v4i w = *reinterpret_cast<const v4i*>(ws + off);
-      const v4i x = *reinterpret_cast<const v4i*>(xs + off);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, x, acc, 0, 0, 0);
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        const v4i x = *reinterpret_cast<const v4i*>(xs + tg * kRingStage + off);
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, x, acc[tg], 0, 0, 0);
+      }
     }
   };
   // prologue: W(0) X(0) ... W(D-2) X(D-2) W(D-1)
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     issue_w(d);
-    if (wave == 0 && d < D - 1) issue_x(d);
+    if (x_issuer && d < D - 1) issue_x(d);
   }
   for (int s = 0; s < n_st; ++s) {
-    if (wave == 0) wait_vmcnt<(2 * D - 3) * kOps>(); else wait_vmcnt<(D - 1) * kOps>();
+    if (x_issuer) wait_vmcnt<(2 * D - 3) * kOps>(); else wait_vmcnt<(D - 1) * kOps>();
     raw_barrier();  // token stage s visible to every wave; every wave past its reads of stage s-1
-    if (wave == 0) issue_x(s + D - 1);
+    if (x_issuer) issue_x(s + D - 1);
     consume(s);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slot done before its refill
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the slots done before their refill
     issue_w(s + D);
   }
   wait_vmcnt<0>();  // the padding stages' DMA has landed before the wave ends
 
-  // lane (r16, grp) holds weight rows wr0 + 4 grp + v, token r16
-  if (r16 < g.M) {
-    const int m = r16;
+  // lane (r16, grp) holds weight rows wr0 + 4 grp + v of token 16 tg + r16
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    const int m = 16 * tg + r16;
+    if (m >= g.M) continue;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int nl = 4 * grp + v;
       if (nl >= nrows) continue;
       const int64_t n = wr0 + nl;
       if constexpr (epi_bf16_out(EPI)) {
-        float t = epi_scale(acc[v], g.sa[m], g.sw[n]);
+        float t = epi_scale(acc[tg][v], g.sa[m], g.sw[n]);
         if (g.bias) t = t + bf16_to_f32(g.bias[n]);
         static_cast<uint16_t*>(g.out)[static_cast<int64_t>(m) * g.ldo + n] = f32_to_bf16(t);
       } else {
-        static_cast<int32_t*>(g.out)[static_cast<int64_t>(m) * g.ldo + n] = acc[v];
+        static_cast<int32_t*>(g.out)[static_cast<int64_t>(m) * g.ldo + n] = acc[tg][v];
       }
     }
   }

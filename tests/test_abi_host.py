@@ -355,9 +355,11 @@ def test_backend_requires_scales():
 def test_default_tiling_of_the_benchmark_shapes(lib):
     """The tiling the library picks for each Qwen3-14B benchmark shape (the
     time model plus the split-K rules, planned for 256 CUs without a GPU):
-    decode cores up to 8 rows, in-block split-K for qkv / o_proj at 64 and
-    512 rows, the 64x128 ring for the wide / deep shapes at 64 rows, and
-    the 256x256 or 256x320 rings (whichever fills whole waves) above."""
+    decode cores up to 8 rows (the shared token ring for the wide gate_up at
+    8 rows), in-block split-K for qkv / o_proj at 64 and 512 rows, the
+    shared token ring for gate_up and the 64x128 ring for the deep down at
+    64 rows, and the 256x256 or 256x320 rings (whichever fills whole waves)
+    above."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
     sq, wide = t3.format(256, 256, 4, 2, 2), t3.format(256, 320, 4, 2, 2)
     ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
@@ -365,7 +367,7 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     expect = {
         (5120, 7168): [ks64, ks512, sq, wide],
         (5120, 5120): [ks64, ks512, wide, wide],
-        (5120, 34816): [r64, wide, wide, sq],
+        (5120, 34816): ["decode_sx_gemm_kernel", wide, wide, sq],
         (17408, 5120): [r64, sq, wide, wide],
     }
     for (K, N), names in expect.items():

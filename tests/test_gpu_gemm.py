@@ -286,9 +286,11 @@ def test_gemm_every_tile_config(M, K, N, bias):
      (3, 4160, 72), (16, 4160, 72),  # 65 steps: several pipelined batches per wave
      # CU-balanced grids: uneven row ranges of 1-32 rows per block
      (1, 1344, 5000), (16, 1344, 8200), (32, 2048, 4100), (7, 1024, 16400),
-     # shared-token core (K % 256 == 0, up to 16 tokens): 9 waves with a ragged
+     # shared-token core (K % 256 == 0, up to 64 tokens): 9 waves with a ragged
      # last wave, one wave of 2-3 rows, 10 waves (3 stages), a grid of 512 blocks
-     (8, 2048, 34820), (16, 512, 600), (2, 256, 40000), (4, 768, 49200)],
+     (8, 2048, 34820), (16, 512, 600), (2, 256, 40000), (4, 768, 49200),
+     # and 2-4 token groups: 17-64 tokens, ragged M
+     (20, 1024, 20000), (48, 512, 36000), (64, 256, 9000)],
 )
 def test_gemm_every_decode_config(M, K, N):
     from minisgl_amd.kernel.lib import load

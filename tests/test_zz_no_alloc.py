@@ -38,9 +38,9 @@ def test_noalloc_gemm_equals_workspace_gemm():
     lib = load()
     # (M, N, K): down at M=512 (40 tiles of 256x256, each split into 6 K
     # ranges: 60 MiB of partial tiles, nearly the whole scratch), then a
-    # smaller input that splits (gate_up at 64 tokens: 272 tiles of 64x128,
-    # 16 of them split 16 ways), then a decode shape (no split)
-    for M, N, K, seed in ((512, 5120, 17408, 1), (64, 34816, 5120, 2), (8, 2048, 1024, 3)):
+    # smaller input that splits (down at 64 tokens: 40 tiles of 64x128, each
+    # split into 6 K ranges), then a decode shape (no split)
+    for M, N, K, seed in ((512, 5120, 17408, 1), (64, 5120, 17408, 2), (8, 2048, 1024, 3)):
         announce(f"noalloc gemm M={M} N={N} K={K}")
         c = linear_case(M, K, N, seed=seed)
         q, s = quant_per_token(c["x"].to(DEV))
