@@ -42,3 +42,28 @@ def _shapes(seed=20261202, count=40):
 def test_gemm_random_shape(M, N, K, bias):
     announce(f"gemm random M={M} N={N} K={K} bias={bias}")
     _run_case(M, K, N, seed=M * 7 + N * 3 + K, bias=bias)
+
+
+def _wide_shapes(seed=20261204, count=12):
+    """Wide N (16384-40000, ragged) at 4-64 tokens with K a multiple of 256:
+    the default dispatch's shared-token decode core, with 1-4 token groups
+    and 4-12 waves per block."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        M = int(rng.integers(4, 65))
+        N = int(rng.integers(16384, 40001))
+        K = 256 * int(rng.integers(1, 17))
+        if M * N * K > 6e10:
+            continue
+        out.append((M, N, K, bool(rng.random() < 0.3)))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,bias", _wide_shapes())
+def test_gemm_random_wide_decode(M, N, K, bias):
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm random wide M={M} N={N} K={K} bias={bias}")
+    assert load().mw8_gemm_kernel_name(M, N, K) == b"decode_sx_gemm_kernel"
+    _run_case(M, K, N, seed=M + N + K, bias=bias)
