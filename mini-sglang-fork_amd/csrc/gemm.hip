@@ -192,16 +192,20 @@ int decode_by_cfg(int cfg, const GemmArgs& g, hipStream_t st) {
 // (gate_up, 2176 row groups): 16-row blocks, 2 waves x 2 slots at one
 // token (30.6 us, 5.8 TB/s), one wave x 4 slots up to 8, 32-row blocks of
 // one wave x 4 slots at 17-32 tokens.
-// Wide N at 4-16 tokens (K % 256 == 0): the shared token ring (cfg 8):
-// the one-wave blocks re-read the token panel per 16 rows (gate_up at 8
-// tokens: 94 MB of token reads beside 178 MB of weights).  Same box, us,
-// best decode3 configuration -> cfg 8: N 34816, K 5120 at 4 / 8 / 12 / 16
-// tokens 31.7 / 34.2 / 37.5 / 40.6 -> 31.4 / 31.4 / 31.7 / 31.7; N 16384
-// 17.5 -> 16.7; N 51200 at 8 / 16 tokens 47.9 / 56.0 -> 45.1 / 46.1; at 2-3
-// tokens decode3 (29.5 / 31.1 against 30.5 / 31.2).  With K = 8192 and
-// the walk staggered per block, level with the K-split decode3 (N 25600:
-// 36.0 / 36.2; N 34816: 45.8 / 44.1) and ahead of the one-wave blocks
-// (55.7).
+// Wide N at 4-64 tokens (K % 256 == 0, one block per CU covering the
+// widest row range): the shared token ring (cfg 8).  The one-wave blocks
+// re-read the token panel per 16 rows (gate_up at 8 tokens: 13% more L2
+// read requests than the weights alone), and from 33 tokens the 64x128
+// ring runs a K-split tail.  Same box, us, previous automatic choice ->
+// cfg 8: N 34816, K 5120 at 4 / 8 / 12 / 16 / 24 / 32 / 48 / 64 tokens
+// 31.7 / 34.2 / 37.5 / 40.6 / 43.4 / 51.1 / 46.1 / 48.0 -> 31.4 / 31.4 /
+// 31.7 / 31.7 / 32.3 / 34.3 / 36.2 / 38.5; N 16384 at 8 tokens 17.5 ->
+// 16.7; N 51200 at 8 / 16 tokens 47.9 / 56.0 -> 45.1 / 46.1 (at 64 tokens
+// two blocks per CU: 63.0 against 61.9 for the tile ring, not taken); at
+// 2-3 tokens decode3 stays (29.5 / 31.1 against 30.5 / 31.2).  With
+// K = 8192 and the walk staggered per block, level with the K-split decode3
+// (N 25600: 36.0 / 36.2; N 34816: 45.8 / 44.1) and ahead of the one-wave
+// blocks (55.7).
 // From 33 tokens on the token operand, read per wave through the texture
 // path, costs more than the weight stream: the register-streaming core
 // with 32 rows over 8 waves (cfg 0) wins, or 64 rows per block for very
