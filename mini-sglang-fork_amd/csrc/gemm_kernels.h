@@ -1460,10 +1460,25 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   }
   v4i xr[D][4][TG];  // token chunks of the stages in flight, per ring slot
 
+  // Dense one-wave blocks walk their stages from stage s_begin + n b / G on
+  // (wrapping): blocks in lockstep at one K offset put a row stride of a
+  // power of two on the same low address bits (MI355X, N 34816, K 8192 at
+  // 2 / 3 tokens: 52.3 / 54.6 -> 44.4 / 47.4 us; K 5120 and the K-split
+  // configurations, which already walk several offsets per block,
+  // unchanged; the grouped walks measured level to 1% slower).
+  const int n_w = s_end - s_begin;
+  const int s_rot = kXQ || WAVES > 1 || Rows::kGrouped || n_w <= 0
+                        ? 0
+                        : static_cast<int>(static_cast<int64_t>(n_w) * blockIdx.x / gridDim.x);
   auto issue = [&](int d, int st) {
     unsigned char* slot = my_ring + d * kStage;
+    int se = st;  // the K stage that slot d takes (a wave's own stages only)
+    if (st < s_end) {
+      se = st + s_rot;
+      if (se >= s_end) se -= n_w;
+    }
     // a padding stage (st >= s_end) reads past the buffer range: zeros, no traffic
-    const int soff = st < s_end ? st * 256 : 0x7fff0000;
+    const int soff = st < s_end ? se * 256 : 0x7fff0000;
 #pragma unroll
     for (int j = 0; j < 4 * RG; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(slot + j * 1024), 16, w_off[j], soff, 0,
@@ -1471,7 +1486,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     if constexpr (!kXQ) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const int64_t k = static_cast<int64_t>(st) * 256 + 64 * kb + 16 * grp;
+        const int64_t k = static_cast<int64_t>(se) * 256 + 64 * kb + 16 * grp;
         const bool kin = k < g.K;
 #pragma unroll
         for (int tg = 0; tg < TG; ++tg) {
