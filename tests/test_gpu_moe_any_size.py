@@ -11,7 +11,7 @@ the layer equals that staged chain bit for bit.  The cases take every
 dispatch path: router-id rows (up to 16 tokens), the one-launch prepare
 (over 256 experts), 16-row alignment blocks with GEMM2 and the slot sum
 fused, and 64-row prefill blocks with the activation as a separate pass or
-in GEMM1's epilogue (K a multiple of 64 after padding)."""
+in GEMM1's epilogue (K a multiple of 64 after padding), with silu and gelu."""
 
 import numpy as np
 import pytest
@@ -55,19 +55,21 @@ def _pad_by_hand(c, H, I):
 
 
 @pytest.mark.parametrize(
-    "M,E,k,H,I,on_input",
-    [(1, 8, 2, 100, 40, False),      # router-id rows
-     (12, 16, 4, 72, 24, True),      # router-id rows, routed weight on GEMM1's input
-     (5, 300, 2, 40, 8, False),      # over 256 experts: router, alignment and quant in one launch
-     (40, 64, 2, 200, 56, False),    # 16-row blocks, GEMM2 and the slot sum fused
-     (300, 8, 2, 136, 40, False),    # 64-row blocks, separate activation (H16 = 144)
-     (520, 8, 2, 250, 40, True)],    # 64-row blocks, activation in GEMM1's epilogue (H16 = 256)
+    "M,E,k,H,I,on_input,act",
+    [(1, 8, 2, 100, 40, False, "silu"),      # router-id rows
+     (12, 16, 4, 72, 24, True, "silu"),      # router-id rows, routed weight on GEMM1's input
+     (5, 300, 2, 40, 8, False, "silu"),      # over 256 experts: router, alignment and quant in one launch
+     (40, 64, 2, 200, 56, False, "silu"),    # 16-row blocks, GEMM2 and the slot sum fused
+     (300, 8, 2, 136, 40, False, "silu"),    # 64-row blocks, separate activation (H16 = 144)
+     (520, 8, 2, 250, 40, True, "silu"),     # 64-row blocks, activation in GEMM1's epilogue (H16 = 256)
+     (24, 8, 2, 120, 20, False, "gelu"),     # gelu, 64-row blocks, separate activation
+     (600, 8, 2, 250, 24, False, "gelu")],   # gelu in GEMM1's epilogue
 )
-def test_moe_layer_any_size(M, E, k, H, I, on_input):
-    announce(f"moe any size M={M} E={E} k={k} H={H} I={I} on_input={on_input}")
+def test_moe_layer_any_size(M, E, k, H, I, on_input, act):
+    announce(f"moe any size M={M} E={E} k={k} H={H} I={I} on_input={on_input} act={act}")
     H16, I16 = _up16(H), _up16(I)
     c = moe_case(M, hidden=H, num_experts=E, inter=I, seed=M + E + H + I)
-    layer = MoELayer(E, k, H, I, renormalize=True, apply_router_weight_on_input=on_input)
+    layer = MoELayer(E, k, H, I, renormalize=True, activation=act, apply_router_weight_on_input=on_input)
     layer.load_state_dict({
         "gate_up_proj": c["w1"].to(DEV), "down_proj": c["w2"].to(DEV),
         "gate_up_scale": c["s_w1"].to(DEV), "down_scale": c["s_w2"].to(DEV),
@@ -80,7 +82,7 @@ def test_moe_layer_any_size(M, E, k, H, I, on_input):
         out = layer.forward(h, logits)
         out2 = layer.forward(c["hidden"].to(DEV), logits).clone()
         outp = create_moe_backend("fused_w8a8").forward(
-            hp.clone(), w1p, w2p, logits, k, True, apply_router_weight_on_input=on_input,
+            hp.clone(), w1p, w2p, logits, k, True, activation=act, apply_router_weight_on_input=on_input,
             w1_scale=s1p, w2_scale=s2p,
         )
         torch.cuda.synchronize()
@@ -110,9 +112,9 @@ def test_moe_layer_any_size(M, E, k, H, I, on_input):
     assert bf16_bits_equal(c1[:, :I], c1_ref[:, :I]).all()
     assert bf16_bits_equal(c1[:, I16:I16 + I], c1_ref[:, I:]).all()
     assert not c1[:, I:I16].any() and not c1[:, I16 + I:].any()
-    qa, sa, act = act_and_mul_quant(c1, "silu", return_act=True)
-    assert not act[:, I:].any()
-    qa_ref, sa_ref = orc.quant_per_token(f32(act[:, :I]))
+    qa, sa, a = act_and_mul_quant(c1, act, return_act=True)
+    assert not a[:, I:].any()
+    qa_ref, sa_ref = orc.quant_per_token(f32(a[:, :I]))
     np.testing.assert_array_equal(qa[:, :I].cpu().numpy(), qa_ref)
     np.testing.assert_array_equal(sa.cpu().numpy().view(np.uint32), sa_ref.view(np.uint32))
     assert not qa[:, I:].any()
