@@ -186,9 +186,9 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
  * The array of the current device is used (make the device of the
  * operands current).  Calls on one device share that array: calls that
  * overlap on one device (concurrent streams) race.  Allocates nothing;
- * results equal mw8_gemm_w8a8_bf16's bit for bit.  The Python wrapper
- * (gemm_w8a8) calls this entry, so that the array is the only K-split
- * memory a device holds.
+ * results equal mw8_gemm_w8a8_bf16's bit for bit.  (The Python wrappers
+ * use mw8_gemm_w8a8_bf16 with a per-call workspace, which concurrent
+ * streams do not share.)
  */
 int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W, const float* sw,
                                const void* bias, void* y, int64_t M, int64_t N, int64_t K,

@@ -47,9 +47,9 @@ _WORKSPACE: Dict[torch.device, torch.Tensor] = {}
 
 
 def reserve_gemm_workspace(device: torch.device) -> torch.Tensor:
-    """A caller-side GEMM workspace for ``device``, for the entry points
-    that take one (the int32 parity hook ``gemm_w8a8_i32``, and C callers
-    of ``mw8_gemm_w8a8_bf16``; ``gemm_w8a8`` needs none): one buffer of
+    """A reserved GEMM workspace for ``device``, for callers that drive the
+    C entry points themselves (``gemm_w8a8`` and ``gemm_w8a8_i32`` take a
+    per-call workspace from torch's caching allocator instead): one buffer of
     ``mw8_gemm_workspace_max_bytes()`` (the bound over every shape and
     tiling, 64 MiB on a 256-CU MI355X), allocated on first use and never
     grown, replaced or freed.  So a HIP graph that captured a GEMM keeps a
@@ -69,6 +69,18 @@ def reserve_gemm_workspace(device: torch.device) -> torch.Tensor:
         ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
         _WORKSPACE[dev] = ws
     return ws
+
+
+def _call_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
+    """The K split's int32 partial tiles for one call at (M, N, K), or None
+    when no split applies: a buffer from torch's caching allocator, which
+    hands a freed block back only to work ordered after its last use on the
+    same stream (and takes it from the graph's private pool under capture),
+    so calls on concurrent streams never share one.  The size is planned for
+    q's device and the calling thread's tuning override, as the call is."""
+    with torch.cuda.device(device):
+        need = int(load().mw8_gemm_workspace_bytes(M, N, K))
+    return torch.empty(need, dtype=torch.uint8, device=device) if need > 0 else None
 
 
 def gemm_workspace(M: int, N: int, K: int, device: torch.device) -> Optional[torch.Tensor]:
@@ -245,16 +257,12 @@ def gemm_w8a8(
     _need(y.dtype == torch.bfloat16 and y.shape == (M, N) and y.is_contiguous(), "bad out buffer")
     if M == 0:
         return y
-    # The allocation-free entry: the K split's int32 partial tiles go to the
-    # library's static per-device scratch (the same 64 MiB bound as a
-    # reserved workspace, the same sharing rule: calls on one stream share
-    # it, concurrent streams must not), so no workspace tensor is held
-    # beside it.  It takes the current device's scratch: q's device is
-    # made current for the call.
-    with torch.cuda.device(q.device):
+    ws = _call_workspace(M, N, K, q.device)
+    with torch.cuda.device(q.device):  # the library plans the tiling for the current device
         check(
-            load().mw8_gemm_w8a8_bf16_noalloc(
-                _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K, _stream(q),
+            load().mw8_gemm_w8a8_bf16(
+                _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ptr(bias), _ptr(y), M, N, K, _ptr(ws),
+                0 if ws is None else ws.numel(), _stream(q),
             )
         )
     return y
@@ -302,13 +310,14 @@ def gemm_w8a8_i32(q: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     acc = torch.empty((M, N), dtype=torch.int32, device=q.device)
     if M == 0:
         return acc
-    ws = gemm_workspace(M, N, K, q.device)
-    check(
-        load().mw8_gemm_w8a8_i32(
-            _ptr(q), _ptr(w), _ptr(acc), M, N, K, _ptr(ws), 0 if ws is None else ws.numel(),
-            _stream(q),
+    ws = _call_workspace(M, N, K, q.device)
+    with torch.cuda.device(q.device):
+        check(
+            load().mw8_gemm_w8a8_i32(
+                _ptr(q), _ptr(w), _ptr(acc), M, N, K, _ptr(ws), 0 if ws is None else ws.numel(),
+                _stream(q),
+            )
         )
-    )
     return acc
 
 

@@ -415,3 +415,35 @@ def test_linear_layer_decode_takes_the_fused_path():
         lin.quant_per_token = orig
     y_ref, *_ = orc.linear_w8a8(f32(x), sd["weight"].numpy(), sd["weight_scale"].numpy())
     assert bf16_bits_equal(y, y_ref).all()
+
+
+def test_gemm_concurrent_streams():
+    """Two K-split GEMMs (down at 512 rows: 40 tiles in 6 K ranges, 60 MiB of
+    int32 partial tiles each) in flight at once on two streams, then the same
+    pair on one stream: bit-identical.  Each call's partial tiles have a
+    buffer of their own (torch's caching allocator keys blocks by stream)."""
+    from minisgl_amd.kernel.lib import load
+
+    announce("gemm concurrent streams")
+    M, K, N = 512, 17408, 5120
+    assert load().mw8_gemm_workspace_bytes(M, N, K) > 0, "the case must take the K split"
+    cases = [linear_case(M, K, N, seed=s) for s in (21, 22)]
+    ins = []
+    for c in cases:
+        q, s = quant_per_token(c["x"].to(DEV))
+        ins.append((q, s, c["w"].to(DEV), c["s_w"].to(DEV)))
+    torch.cuda.synchronize()
+    want = [gemm_w8a8(*a) for a in ins]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got = [None, None]
+    for _ in range(3):
+        for i, st in enumerate(streams):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                got[i] = gemm_w8a8(*ins[i])
+        for st in streams:
+            torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(got[i].view(torch.int16), want[i].view(torch.int16)), f"stream {i}"
