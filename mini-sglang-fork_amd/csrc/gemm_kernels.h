@@ -1350,13 +1350,20 @@ struct RingDrain<D, OPS, D> {
 // read zeros), and the epilogue scatters to pair rows with the routed
 // weight.
 // kXQ (dense, one token group, bf16 output): g.A holds the bf16 activation
-// rows [M <= 16, lda elements], quantized inside the block -- the fused
-// F.linear of a decode batch.  Every block computes the rows' absmax; each
-// wave quantizes its K range of the rows into its (not yet used) ring slots
-// with the quantizer's arithmetic, loads its token fragments of every stage
-// into registers (at most kXQMaxStages stages per wave), and only then
-// starts the weight stream; the epilogue takes the row scales from LDS.
-constexpr int kXQMaxStages = 6, kXQMaxTokens = 4;
+// rows [M <= 4, lda elements], quantized inside the block -- the fused
+// F.linear of a decode batch.  Each wave loads its K range of the M rows
+// (16-element chunks spread over its lanes, all in flight at once) and
+// then issues its first D-1 weight stages; it adds its partial row maxima
+// into LDS and, after one barrier, quantizes its chunks with the
+// quantizer's arithmetic into its last ring slot (the rows int8, row-major;
+// M times the range fits one slot), loads its token fragments of every
+// stage into registers (at most kXQMaxStages stages per wave) and issues
+// the last weight stage into that slot.  Every block quantizes all M rows,
+// so the fused form pays off for a few rows only (MI355X, N = K = 5120, us,
+// fused vs quantizer launch + GEMM: 5 tokens 10.6 vs 11.5, 6 tokens 11.7
+// vs 11.5, 8 tokens 12.8 vs 11.9).  The epilogue takes the row scales from
+// LDS.
+constexpr int kXQMaxTokens = 4, kXQMaxStages = 6;
 
 template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1, bool kXQ = false>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
@@ -1538,69 +1545,112 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
     }
   }
 
-  // fused quantization (kXQ): row absmax over the block, the wave's K range
-  // quantized into its ring slots, its token fragments into registers
+  // fused quantization (kXQ): the wave's K range of the rows loaded at once,
+  // the rows' absmax over the block, the range quantized into the wave's
+  // ring slots, its token fragments into registers
   __shared__ uint32_t xq_max[kXQ ? 16 : 1];
-  __shared__ float xq_s[kXQ ? 16 : 1];
-  v4i xq[kXQ ? kXQMaxStages : 1][4];
+  __shared__ float xq_s[kXQ ? 16 : 1], xq_r[kXQ ? 16 : 1];
+  __shared__ int xq_fast[kXQ ? 16 : 1];
+  constexpr int kXS = kXQ ? kXQMaxStages : 1;
+  constexpr int kXQChunks = kXQMaxTokens * kXS * 16 / 64;  // 16-element chunks per lane, at most
+  v4i xq[kXS][4];
   if constexpr (kXQ) {
+    static_assert(D * kOps < 64, "token loads complete before the weight stages");
     const int M = static_cast<int>(g.M);
-    const uint16_t* X = reinterpret_cast<const uint16_t*>(g.A);
-    const int64_t ldx = g.lda;
     if (tid < 16) xq_max[tid] = 0;
-    __syncthreads();
-    for (int m = 0; m < M; ++m) {
+    __syncthreads();  // nothing in flight yet
+    // this wave's K range [256 s_begin, 256 s_end) of each row in 16-element
+    // chunks, chunk c = m * cpr + j (row m, elements 256 s_begin + 16 j ..),
+    // lane l holding chunks l, l + 64, ... through a buffer view of the M
+    // rows; chunks past the rows' chunks or past K (K % 16 == 0: a chunk is
+    // all in or all out) read zeros without traffic
+    const int kw = 256 * (s_end - s_begin), cpr = kw / 16, nch = M * cpr;
+    const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        scalar_ptr(const_cast<int8_t*>(g.A)), 0, static_cast<int>(g.M * g.lda * 2), kBufferFlags);
+    v4i xc[kXQChunks][2];
+#pragma unroll
+    for (int u = 0; u < kXQChunks; ++u) {
+      xc[u][0] = xc[u][1] = v4i{0};
+      if (64 * u < nch) {  // wave-uniform: the wave's chunks only
+        const int c = lane + 64 * u, m = c / cpr, j = c - m * cpr;
+        const int64_t k = 256 * static_cast<int64_t>(s_begin) + 16 * j;
+        const uint32_t off = c < nch && k < g.K ? static_cast<uint32_t>((m * g.lda + k) * 2) : 0x80000000u;
+        xc[u][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, off, 0, 0));
+        xc[u][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, off + 16, 0, 0));
+      }
+    }
+    // weight stages 0 .. D-2 behind the loads (stages past the wave's range
+    // read zeros without traffic, so exactly D-1 stages of operations follow
+    // the loads); the last slot stays free for the int8 rows
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d) issue(d, s_begin + d);
+    wait_vmcnt<(D - 1) * kOps>();  // the row loads are in
+#pragma unroll
+    for (int u = 0; u < kXQChunks; ++u) {
+      const int c = lane + 64 * u;
+      if (64 * u >= nch) break;  // wave-uniform
       uint32_t mx = 0;
-      for (int64_t c = tid; c < g.K / 8; c += 64 * WAVES) {
-        const v4i v = *reinterpret_cast<const v4i*>(X + m * ldx + 8 * c);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t w = static_cast<uint32_t>(v[j]), lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
+          const uint32_t w = static_cast<uint32_t>(xc[u][h][j]), lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
           mx = lo > mx ? lo : mx;
           mx = hi > mx ? hi : mx;
         }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t o = __shfl_xor(mx, off, 64);
-        mx = o > mx ? o : mx;
-      }
-      if (lane == 0) atomicMax(&xq_max[m], mx);
+      if (c < nch) atomicMax(&xq_max[c / cpr], mx);
     }
-    __syncthreads();
-    if (tid < 16) xq_s[tid] = tid < M ? row_scale(bf16_to_f32(static_cast<uint16_t>(xq_max[tid]))).s : 0.0f;
-    // this wave's K range [256 s_begin, 256 s_end) of each row, int8, row-major in its ring
-    const int kw = 256 * (s_end - s_begin);
-    for (int m = 0; m < M; ++m) {
-      const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(xq_max[m])));
-      for (int u = lane; u < kw / 16; u += 64) {
-        const int64_t k = 256 * static_cast<int64_t>(s_begin) + 16 * u;
-        v4i q = v4i{0};
-        if (k < g.K) {  // K % 16 == 0: a 16-element chunk is all in or all out
-          const v4i v0 = *reinterpret_cast<const v4i*>(X + m * ldx + k);
-          const v4i v1 = *reinterpret_cast<const v4i*>(X + m * ldx + k + 8);
-          U16x8 a, b;
+    // raw barriers (LDS waits only): the weight stages stay in flight
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    raw_barrier();
+    if (tid < 16) {
+      const RowScale rs = row_scale(bf16_to_f32(static_cast<uint16_t>(xq_max[tid])));
+      xq_s[tid] = tid < M ? rs.s : 0.0f;
+      xq_r[tid] = rs.r;
+      xq_fast[tid] = rs.fast ? 1 : 0;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    raw_barrier();
+    // this wave's range of each row, int8, row-major in its last ring slot
+    unsigned char* xslot = my_ring + (D - 1) * kStage;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            a.w[j] = static_cast<uint32_t>(v0[j]);
-            b.w[j] = static_cast<uint32_t>(v1[j]);
-          }
-          const uint2 qa = rs.fast ? quant8<true>(a, rs) : quant8<false>(a, rs);
-          const uint2 qb = rs.fast ? quant8<true>(b, rs) : quant8<false>(b, rs);
-          q = v4i{static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qb.x), static_cast<int>(qb.y)};
+    for (int u = 0; u < kXQChunks; ++u) {
+      const int c = lane + 64 * u;
+      if (64 * u >= nch) break;  // wave-uniform
+      if (c < nch) {
+        const int m = c / cpr, j = c - m * cpr;
+        RowScale rs;
+        rs.s = xq_s[m];
+        rs.r = xq_r[m];
+        rs.fast = xq_fast[m] != 0;
+        U16x8 a, b;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          a.w[t] = static_cast<uint32_t>(xc[u][0][t]);
+          b.w[t] = static_cast<uint32_t>(xc[u][1][t]);
         }
-        *reinterpret_cast<v4i*>(my_ring + m * kw + 16 * u) = q;
+        uint2 qa, qb;
+        if (rs.fast) {
+          qa = quant8<true>(a, rs);
+          qb = quant8<true>(b, rs);
+        } else {
+          qa = quant8<false>(a, rs);
+          qb = quant8<false>(b, rs);
+        }
+        *reinterpret_cast<v4i*>(xslot + m * kw + 16 * j) =
+            v4i{static_cast<int>(qa.x), static_cast<int>(qa.y), static_cast<int>(qb.x), static_cast<int>(qb.y)};
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's ring writes done (one wave reads them)
 #pragma unroll
-    for (int i = 0; i < kXQMaxStages; ++i)
+    for (int i = 0; i < kXS; ++i)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         xq[i][kb] = r16 < M && i < s_end - s_begin
-                        ? *reinterpret_cast<const v4i*>(my_ring + r16 * kw + 256 * i + 64 * kb + 16 * grp)
+                        ? *reinterpret_cast<const v4i*>(xslot + r16 * kw + 256 * i + 64 * kb + 16 * grp)
                         : v4i{0};
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // fragments read before the weight DMA reuses the ring
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // fragments read before the weight DMA reuses the slot
+    issue(D - 1, s_begin + D - 1);  // (past the wave's range: zeros, no traffic)
   }
 
   v4i acc[RG][TG];
@@ -1628,12 +1678,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   const int n_st = s_end - s_begin;
   if constexpr (kXQ) {
     // fused quantization: every stage's token fragments are in xq (compile-
-    // time indices), so the wave's stages run fully unrolled
+    // time indices), so the wave's stages run fully unrolled; the first D
+    // stages went out in the prologue
 #pragma unroll
-    for (int i = 0; i < D; ++i)
-      if (i < n_st) issue(i, s_begin + i);
-#pragma unroll
-    for (int i = 0; i < kXQMaxStages; ++i) {
+    for (int i = 0; i < kXS; ++i) {
       if (i < n_st) {
         const int later = n_st - 1 - i < D - 1 ? n_st - 1 - i : D - 1;  // stages issued after stage i
         wait_stages<kOps, (D - 1 < 3 ? D - 1 : 3)>(later);

@@ -352,8 +352,10 @@ def test_linear_bf16_fused_quant(K, N):
     """The one-launch decode linear (mw8_linear_bf16_w8a8: per-token
     quantization inside the decode GEMM) equals quant_per_token followed by
     gemm_w8a8 bit for bit, for 1-4 tokens, under every decode configuration
-    that takes the shape; rows with a stride past K, an all-zero row, x20
-    outliers and a bias; and the oracle on every row."""
+    that takes the shape; rows with a stride past K, an all-zero row, a row
+    of tiny values (absmax below 2^-60: the division path of the quantizer,
+    beside rows on the reciprocal path in the same wave), x20 outliers and a
+    bias; and the oracle on every row."""
     from minisgl_amd.kernel import linear_bf16_supported, linear_bf16_w8a8
     from minisgl_amd.kernel.lib import load
 
@@ -369,6 +371,8 @@ def test_linear_bf16_fused_quant(K, N):
         buf[:, :K][torch.rand(M, K, generator=gen) < 1e-3] *= 20
         if M >= 3:
             buf[1] = 0.0  # all-zero row: s = 0, q = 0
+        if M >= 4:
+            buf[2] *= 2.0**-70  # absmax below 2^-60: the division path
         xb = buf.to(torch.bfloat16)
         x = xb.to(DEV)[:, :K]  # row stride K + 64
         for b, bref in ((None, None), (bd, f32(bias))):
@@ -391,18 +395,19 @@ def test_linear_bf16_fused_quant(K, N):
             assert ran >= 2, f"M={M}: the default and at least one forced configuration take the shape"
 
 
-def test_linear_layer_decode_takes_the_fused_path():
-    """LinearOProj.forward on a one-token bf16 input runs the one-launch
+@pytest.mark.parametrize("M", [1, 4])
+def test_linear_layer_decode_takes_the_fused_path(M):
+    """LinearOProj.forward on a decode batch of bf16 rows runs the one-launch
     fused linear (no separate quantizer call) and matches the oracle."""
     import minisgl_amd.layers.linear as lin
 
-    announce("linear layer fused decode path")
+    announce(f"linear layer fused decode path M={M}")
     gen = torch.Generator().manual_seed(9)
     layer = LinearOProj(5120, 5120, has_bias=False)
     sd = {"weight": torch.randint(-127, 128, (5120, 5120), generator=gen, dtype=torch.int8),
           "weight_scale": torch.rand(5120, generator=gen) * 1e-2}
     layer.load_state_dict({k: v.to(DEV) for k, v in sd.items()})
-    x = torch.randn(1, 5120, generator=gen).to(torch.bfloat16)
+    x = torch.randn(M, 5120, generator=gen).to(torch.bfloat16)
 
     def _no_quant(*a, **kw):
         raise AssertionError("the decode forward called the separate quantizer")
