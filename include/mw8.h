@@ -201,10 +201,10 @@ int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W
  * mw8_quant_per_token_bf16 arithmetic), int8 GEMM and epilogue, bit for
  * bit what the two calls write.  Each block of the decode core quantizes
  * the few token rows itself, so there is no quantizer launch and no int8
- * copy of x.  Takes M <= 4 where the decode core streams at most 6 K
- * stages of 256 bytes per wave and one ring slot holds a wave's range of
- * the int8 rows (mw8_linear_bf16_supported); returns MW8_ERR_SHAPE
- * otherwise, also when x spans 2^31 bytes or more.  Replaces _LinearTPImpl.forward -> F.linear
+ * copy of x.  Takes M <= 16 and M K <= 20480 where the decode core
+ * streams at most 6 K stages of 256 bytes per wave and one ring slot holds
+ * a wave's range of the int8 rows (mw8_linear_bf16_supported); returns
+ * MW8_ERR_SHAPE otherwise, also when x spans 2^31 bytes or more.  Replaces _LinearTPImpl.forward -> F.linear
  * (python/minisgl/layers/linear.py:31-32) for an input with no quantizing
  * producer (the attention output into o_proj, python/minisgl/models/utils.py:123).
  */

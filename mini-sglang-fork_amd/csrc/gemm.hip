@@ -609,20 +609,22 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Whether decode configuration cfg takes a fused-quantization call: a
 // decode3 configuration whose waves each stream at most kXQMaxStages K
-// stages of 256 bytes and hold their range of the M int8 rows in one ring
+// stages of 256 bytes, load their range of the M rows in at most
+// kXQChunks 16-element chunks per lane and hold it as int8 in one ring
 // slot.
 bool xq_cfg_fits(int cfg, int64_t M, int64_t K) {
   const DecodeCfg& c = kDecodeCfgs[cfg];
   if (c.core != 1) return false;
   const int64_t per_wave = ((K + 255) / 256 + c.waves - 1) / c.waves;
-  return per_wave <= kXQMaxStages && M * 256 * per_wave <= int64_t{c.rg} * kRingStage;
+  return per_wave <= kXQMaxStages && (M * 16 * per_wave + 63) / 64 <= kXQChunks &&
+         M * 256 * per_wave <= int64_t{c.rg} * kRingStage;
 }
 
 // The decode configuration a fused-quantization call at (M, N, K) runs, or
-// -1 if it does not take it: at most kXQMaxTokens rows, the override or the
-// default decode configuration.
+// -1 if it does not take it: at most kXQMaxTokens rows and kXQMaxElems
+// elements, the override or the default decode configuration.
 int xq_decode_cfg(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || M > kXQMaxTokens || N < 1 || K < 16 || K % 16 != 0) return -1;
+  if (M < 1 || M > kXQMaxTokens || M * K > kXQMaxElems || N < 1 || K < 16 || K % 16 != 0) return -1;
   int cfg = g_decode_cfg;
   if (cfg < 0 || cfg >= kNumDecodeCfgs) {
     cfg = default_decode_cfg(M, N, K);
@@ -691,9 +693,9 @@ int linear_bf16_w8a8(const void* x, int64_t ldx, const int8_t* W, const float* s
   MW8_REQUIRE(x && W && sw && y, kErrArg, "linear_bf16: null x/W/scales/y");
   const int cfg = xq_decode_cfg(M, N, K);
   MW8_REQUIRE(cfg >= 0, kErrShape,
-              "linear_bf16: M=%lld N=%lld K=%lld is not a fused decode shape (M <= %d, at most %d K stages of "
-              "256 bytes per wave, the rows' range within one ring slot)",
-              (long long)M, (long long)N, (long long)K, kXQMaxTokens, kXQMaxStages);
+              "linear_bf16: M=%lld N=%lld K=%lld is not a fused decode shape (M <= %d, M K <= %lld, at most %d K "
+              "stages of 256 bytes per wave, the rows' range within one ring slot)",
+              (long long)M, (long long)N, (long long)K, kXQMaxTokens, (long long)kXQMaxElems, kXQMaxStages);
   MW8_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned16(x) && aligned16(W), kErrAlign,
               "linear_bf16: x rows and W need 16-byte alignment (ldx=%lld)", (long long)ldx);
   MW8_REQUIRE(N < (1ll << 31) && N * K < (1ll << 31), kErrShape, "linear_bf16: W exceeds 2^31 bytes");

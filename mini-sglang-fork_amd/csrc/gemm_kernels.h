@@ -1350,7 +1350,7 @@ struct RingDrain<D, OPS, D> {
 // read zeros), and the epilogue scatters to pair rows with the routed
 // weight.
 // kXQ (dense, one token group, bf16 output): g.A holds the bf16 activation
-// rows [M <= 4, lda elements], quantized inside the block -- the fused
+// rows [M <= 16, lda elements], quantized inside the block -- the fused
 // F.linear of a decode batch.  Each wave loads its K range of the M rows
 // (16-element chunks spread over its lanes, all in flight at once) and
 // then issues its first D-1 weight stages; it adds its partial row maxima
@@ -1359,11 +1359,13 @@ struct RingDrain<D, OPS, D> {
 // M times the range fits one slot), loads its token fragments of every
 // stage into registers (at most kXQMaxStages stages per wave) and issues
 // the last weight stage into that slot.  Every block quantizes all M rows,
-// so the fused form pays off for a few rows only (MI355X, N = K = 5120, us,
+// so the fused form pays off while M K is small (MI355X, N = K = 5120, us,
 // fused vs quantizer launch + GEMM: 5 tokens 10.6 vs 11.5, 6 tokens 11.7
-// vs 11.5, 8 tokens 12.8 vs 11.9).  The epilogue takes the row scales from
-// LDS.
-constexpr int kXQMaxTokens = 4, kXQMaxStages = 6;
+// vs 11.5, 8 tokens 12.8 vs 11.9): the host takes it up to kXQMaxElems
+// elements of x.  The epilogue takes the row scales from LDS.
+constexpr int kXQMaxTokens = 16, kXQMaxStages = 6;
+constexpr int64_t kXQMaxElems = 4 * 5120;  // M K
+constexpr int kXQChunks = 6;               // 16-element chunks of x per lane, at most
 
 template <int TG, int WAVES, int D, int EPI, class Rows = DenseRows, int RG = 1, bool kXQ = false>
 __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
@@ -1552,7 +1554,6 @@ __global__ __launch_bounds__(64 * WAVES) void decode3_gemm_kernel(GemmArgs g) {
   __shared__ float xq_s[kXQ ? 16 : 1], xq_r[kXQ ? 16 : 1];
   __shared__ int xq_fast[kXQ ? 16 : 1];
   constexpr int kXS = kXQ ? kXQMaxStages : 1;
-  constexpr int kXQChunks = kXQMaxTokens * kXS * 16 / 64;  // 16-element chunks per lane, at most
   v4i xq[kXS][4];
   if constexpr (kXQ) {
     static_assert(D * kOps < 64, "token loads complete before the weight stages");

@@ -87,7 +87,7 @@ class _LinearW8A8Impl(BaseOP):
         M, K = x2.shape
         N = self.weight.shape[0]
         if (
-            0 < M <= 4
+            0 < M <= 16
             and x2.dtype == torch.bfloat16
             and x2.stride(1) == 1
             and (M == 1 or x2.stride(0) % 8 == 0)

@@ -155,15 +155,17 @@ def test_workspace_bound_and_tuning_counts(lib):
 
 
 def test_linear_bf16_supported_shapes(lib):
-    """The one-launch decode linear takes 1-4 tokens where the decode core's
-    waves stream at most 6 K stages of 256 bytes and one ring slot holds a
-    wave's range of the int8 rows (planned for 256 CUs without a GPU):
-    o_proj / qkv of Qwen3-14B at 1-4 tokens, not at 5 tokens, not the
-    K = 17408 down projection, not K % 16 != 0."""
+    """The one-launch decode linear takes up to 16 tokens and 4 x 5120
+    elements of x, where the decode core's waves stream at most 6 K stages
+    of 256 bytes and one ring slot holds a wave's range of the int8 rows
+    (planned for 256 CUs without a GPU): o_proj / qkv of Qwen3-14B at 1-4
+    tokens, not at 5 tokens; config 0 (16 tokens, K = 1024), not 17 tokens;
+    not the K = 17408 down projection, not K % 16 != 0."""
     sup = lib.mw8_linear_bf16_supported
     for M in (1, 2, 3, 4):
         assert sup(M, 5120, 5120) == 1 and sup(M, 7168, 5120) == 1
     assert sup(5, 5120, 5120) == 0 and sup(0, 5120, 5120) == 0
+    assert sup(16, 6144, 1024) == 1 and sup(17, 6144, 1024) == 0
     assert sup(1, 5120, 17408) == 0
     assert sup(1, 5120, 5128) == 0
 

@@ -351,7 +351,7 @@ def test_gemm_stream_walk(M, K, N, bias):
 def test_linear_bf16_fused_quant(K, N):
     """The one-launch decode linear (mw8_linear_bf16_w8a8: per-token
     quantization inside the decode GEMM) equals quant_per_token followed by
-    gemm_w8a8 bit for bit, for 1-4 tokens, under every decode configuration
+    gemm_w8a8 bit for bit, for 1-16 tokens, under every decode configuration
     that takes the shape; rows with a stride past K, an all-zero row, a row
     of tiny values (absmax below 2^-60: the division path of the quantizer,
     beside rows on the reciprocal path in the same wave), x20 outliers and a
@@ -366,7 +366,7 @@ def test_linear_bf16_fused_quant(K, N):
     s_w = torch.rand(N, generator=gen) * 9e-3 + 1e-3
     bias = torch.randn(N, generator=gen).to(torch.bfloat16)
     wd, swd, bd = w.to(DEV), s_w.to(DEV), bias.to(DEV)
-    for M in (1, 2, 3, 4):
+    for M in (1, 2, 3, 4, 8, 16):
         buf = torch.randn(M, K + 64, generator=gen) * 2
         buf[:, :K][torch.rand(M, K, generator=gen) < 1e-3] *= 20
         if M >= 3:
@@ -392,7 +392,12 @@ def test_linear_bf16_fused_quant(K, N):
                     ran += 1
             finally:
                 lib.mw8_set_tuning(-1, -1, -1)
-            assert ran >= 2, f"M={M}: the default and at least one forced configuration take the shape"
+            if M <= 4 and M * K <= 4 * 5120:
+                assert ran >= 2, f"M={M}: the default and at least one forced configuration take the shape"
+            elif M * K <= 4 * 5120:
+                assert ran >= 1, f"M={M}: a configuration takes the shape"
+            else:
+                assert ran == 0, f"M={M}: past the fused form's element budget"
 
 
 @pytest.mark.parametrize("M", [1, 4])
