@@ -220,6 +220,26 @@ int mw8_gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M,
                       int64_t K, void* workspace, size_t workspace_bytes, mw8_stream_t stream);
 
 /*
+ * The gate_up GEMM with the gated activation in its epilogue: y bf16
+ * [M, I] = bf16(act(g) * u), g and u the bf16 W8A8 linear outputs of the
+ * gate rows W[0:I] and the up rows W[I:2I] of a gate|up weight W int8
+ * [2I, K] (scales sw fp32 [2I]), act 0 = silu, 1 = gelu (erf): bit for bit
+ * mw8_gemm_w8a8_bf16 into [M, 2I] followed by the activation of
+ * mw8_act_and_mul_quant_bf16 (its act_out), without the [M, 2I]
+ * intermediate.  Replaces gate_up_proj -> act_fn of GatedMLP.forward
+ * (python/minisgl/models/utils.py:44-50; silu_and_mul,
+ * python/minisgl/layers/activation.py:9-12).  Takes I % 8 == 0,
+ * K % 128 == 0 and shapes the plain GEMM runs on its ring cores (large
+ * enough M; mw8_gemm_act_supported), else MW8_ERR_SHAPE.  Workspace as
+ * mw8_gemm_w8a8_bf16, sized by mw8_gemm_act_workspace_bytes.
+ */
+int mw8_gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw, int32_t act, void* y,
+                           int64_t M, int64_t I, int64_t K, void* workspace, size_t workspace_bytes,
+                           mw8_stream_t stream);
+int32_t mw8_gemm_act_supported(int64_t M, int64_t I, int64_t K);
+size_t mw8_gemm_act_workspace_bytes(int64_t M, int64_t I, int64_t K);
+
+/*
  * Router: logits [M, E] (bf16 if logits_is_bf16 else fp32) -> fp32 softmax,
  * top-k, optional renormalisation (w / sum w, then w / (sum w + 1e-8)).
  * topk_w fp32 [M, topk], topk_ids int32 [M, topk].  E <= 1024, topk <= 64.

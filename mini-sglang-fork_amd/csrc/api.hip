@@ -29,6 +29,10 @@ int check_launch(const char* what) {
 int quant_per_token_bf16(const void*, int64_t, int64_t, int64_t, int8_t*, int64_t, float*, hipStream_t);
 int act_and_mul_quant_bf16(const void*, int64_t, int64_t, int, int8_t*, float*, void*, hipStream_t);
 size_t gemm_workspace_bytes(int64_t, int64_t, int64_t);
+int gemm_act_cfg(int64_t, int64_t, int64_t);
+size_t gemm_act_workspace_bytes(int64_t, int64_t, int64_t);
+int gemm_act_w8a8_bf16(const int8_t*, const float*, const int8_t*, const float*, int, void*, int64_t, int64_t,
+                       int64_t, void*, size_t, hipStream_t);
 size_t gemm_workspace_max_bytes();
 void set_tuning(int, int, int);
 int tuning_count(int);
@@ -134,6 +138,17 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* ws,
                        size_t ws_bytes, mw8_stream_t st) {
   MW8_ENTRY(mw8::gemm_w8a8_bf16(A, sa, W, sw, bias, y, M, N, K, ws, ws_bytes, S(st)));
+}
+
+int mw8_gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw, int32_t act, void* y,
+                           int64_t M, int64_t I, int64_t K, void* ws, size_t ws_bytes, mw8_stream_t st) {
+  MW8_ENTRY(mw8::gemm_act_w8a8_bf16(A, sa, W, sw, act, y, M, I, K, ws, ws_bytes, S(st)));
+}
+
+int32_t mw8_gemm_act_supported(int64_t M, int64_t I, int64_t K) { return mw8::gemm_act_cfg(M, I, K) >= 0 ? 1 : 0; }
+
+size_t mw8_gemm_act_workspace_bytes(int64_t M, int64_t I, int64_t K) {
+  return mw8::gemm_act_workspace_bytes(M, I, K);
 }
 
 int mw8_gemm_w8a8_bf16_noalloc(const int8_t* A, const float* sa, const int8_t* W, const float* sw,

@@ -755,6 +755,109 @@ int gemm_w8a8_i32(const int8_t* A, const int8_t* W, int32_t* acc, int64_t M, int
   return gemm_common(A, nullptr, W, nullptr, nullptr, acc, M, N, K, ws, ws_bytes, st, kEpiI32);
 }
 
+// ----------------------------------------- GEMM with the gated activation
+// y [M, I] = act_fn(gate) * up of the W8A8 GEMM against a gate|up weight
+// [2I, K] (gate rows first), each tile's B rows the gate rows and the
+// matching up rows of BN/2 activation columns (tile3_run kAct): the
+// [M, 2I] gate|up output never reaches memory.  The ring configurations
+// with a one-pass staged epilogue take it; the plain GEMM's pick at
+// (M, 2I, K) decides which, with the same K split of a short last wave
+// (split_reduce_act_kernel applies the activation).
+namespace {
+int act_tile_cfg(int64_t M, int64_t N2, int64_t K) {
+  const int cfg = select_tile_cfg(M, N2, K);
+  if (cfg == 2 || cfg == 3 || cfg == 4 || cfg == 5) return cfg;
+  if (cfg == 6 || cfg == 7) return 2;  // the 256x320 ring and the stream walk: 256x256
+  return M > 128 ? 2 : 4;
+}
+
+template <int BM, int BN, int WM, int WN, int NSTAGE, int kAct>
+int launch_tile3_act(const GemmArgs& g, unsigned tiles, hipStream_t st) {
+  constexpr int kLds = NSTAGE * (BM + BN) * 128;
+  constexpr auto kern = tile3_gemm_kernel<BM, BN, 128, WM, WN, NSTAGE, kEpiBf16, DenseRows, 0, 16, kAct>;
+  if (const int rc = set_lds_limit<kern>(kLds)) return rc;
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, st, g);
+  return kOk;
+}
+
+template <int BM, int BN, int kAct>
+int launch_split_reduce_act(const GemmArgs& g, const SplitPlan& sp, hipStream_t st) {
+  const int64_t threads = sp.tail * BM * (BN / 16);
+  hipLaunchKernelGGL((split_reduce_act_kernel<BM, BN, kAct>), dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, st, g);
+  return kOk;
+}
+
+template <int kAct>
+int dispatch_act(const GemmArgs& g, int cfg, unsigned tiles, bool split, const SplitPlan& sp, hipStream_t st) {
+  int rc;
+  switch (cfg) {
+    case 3: rc = launch_tile3_act<256, 128, 4, 2, 3, kAct>(g, tiles, st); break;
+    case 4: rc = launch_tile3_act<128, 128, 2, 2, 2, kAct>(g, tiles, st); break;
+    case 5: rc = launch_tile3_act<64, 128, 1, 4, 4, kAct>(g, tiles, st); break;
+    default: rc = launch_tile3_act<256, 256, 4, 2, 2, kAct>(g, tiles, st); break;
+  }
+  if (rc != kOk || !split) return rc;
+  switch (cfg) {
+    case 4: return launch_split_reduce_act<128, 128, kAct>(g, sp, st);
+    case 5: return launch_split_reduce_act<64, 128, kAct>(g, sp, st);
+    default: return launch_split_reduce_act<256, 256, kAct>(g, sp, st);
+  }
+}
+}  // namespace
+
+// The ring configuration a fused-activation GEMM at (M, I, K) runs, or -1:
+// I % 8 == 0 (16-byte output rows), K % 128 == 0, and a shape the plain
+// GEMM at (M, 2I, K) runs on the ring cores (not the decode cores).
+int gemm_act_cfg(int64_t M, int64_t I, int64_t K) {
+  if (M < 1 || I < 8 || I % 8 != 0 || K < 128 || K % 128 != 0 || K > (1ll << 17)) return -1;
+  if (!use_tile_path(M, 2 * I, K)) return -1;
+  return act_tile_cfg(M, 2 * I, K);
+}
+
+size_t gemm_act_workspace_bytes(int64_t M, int64_t I, int64_t K) {
+  const int cfg = gemm_act_cfg(M, I, K);
+  return cfg < 0 ? 0 : plan_split(M, 2 * I, K, kTileCfgs[cfg]).ws;
+}
+
+int gemm_act_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const float* sw, int act, void* y,
+                       int64_t M, int64_t I, int64_t K, void* ws, size_t ws_bytes, hipStream_t st) {
+  MW8_REQUIRE(A && sa && W && sw && y, kErrArg, "gemm_act: null pointer");
+  MW8_REQUIRE(act == 0 || act == 1, kErrArg, "gemm_act: act must be 0 (silu) or 1 (gelu)");
+  if (M == 0) return kOk;
+  const int cfg = gemm_act_cfg(M, I, K);
+  MW8_REQUIRE(cfg >= 0, kErrShape,
+              "gemm_act: M=%lld I=%lld K=%lld not taken (I %% 8 == 0, K %% 128 == 0, a ring-core shape)",
+              (long long)M, (long long)I, (long long)K);
+  MW8_REQUIRE(aligned16(A) && aligned16(W) && aligned16(y) && (ws == nullptr || aligned16(ws)), kErrAlign,
+              "gemm_act: A, W, y and the workspace need 16-byte alignment");
+  MW8_REQUIRE(M < (1ll << 31) && M * K < (1ll << 31) && 2 * I * K < (1ll << 31), kErrShape,
+              "gemm_act: A (%lld x %lld) or W (%lld x %lld) exceeds 2^31 bytes", (long long)M, (long long)K,
+              (long long)(2 * I), (long long)K);
+  GemmArgs g{};
+  g.A = A; g.sa = sa; g.W = W; g.sw = sw;
+  g.out = y; g.M = M; g.N = 2 * I; g.K = K; g.lda = K; g.ldo = I;
+  g.top_k = 1;
+  g.staged_out = 1;
+  const TileCfg c = kTileCfgs[cfg];
+  const int64_t tiles64 = ((M + c.bm - 1) / c.bm) * ((2 * I + c.bn - 1) / c.bn);
+  MW8_REQUIRE(tiles64 <= (int64_t{1} << 26), kErrShape, "gemm_act: %lld output tiles exceed the tile walk's range",
+              (long long)tiles64);
+  unsigned tiles = static_cast<unsigned>(tiles64);
+  const SplitPlan sp = plan_split(M, 2 * I, K, c);
+  const bool split = sp.sp > 1 && ws != nullptr && ws_bytes >= sp.ws;
+  g.tail_split = 1;
+  if (split) {
+    g.part = static_cast<int32_t*>(ws);
+    g.full_tiles = sp.full;
+    g.tail_split = sp.sp;
+    tiles = static_cast<unsigned>(sp.full + sp.tail * sp.sp);
+  }
+  const int rc = act == 0 ? dispatch_act<0>(g, cfg, tiles, split, sp, st) : dispatch_act<1>(g, cfg, tiles, split, sp, st);
+  if (rc != kOk) return rc;
+  return check_launch("gemm_act");
+}
+
 // ------------------------------------------------- allocation-free variant
 // The K split's int32 partial tiles live in a file-scope device array of
 // kScratchBytes (64 MiB: the workspace bound of a 256-CU MI355X, 256 slots

@@ -491,11 +491,13 @@ struct TileJob {
   int64_t split_unit; // >= 0: write the int32 partial tile part[split_unit]
 };
 
-// kAct >= 0 (grouped bf16, staged epilogue): the tile's B rows are the gate
-// rows [n0, n0 + BN/2) and the up rows N/2 + [n0, n0 + BN/2) of a gate|up
-// weight [N = 2I, K]; the epilogue writes act = bf16(act_fn(g) * u) for act
-// columns [n0, n0 + BN/2) of an [rows, I] output (g.ldo = I), g and u the
-// bf16-rounded GEMM outputs, as the separate activation kernel computes it.
+// kAct >= 0 (bf16, staged epilogue; grouped or dense rows): the tile's B
+// rows are the gate rows [n0, n0 + BN/2) and the up rows N/2 + [n0, n0 +
+// BN/2) of a gate|up weight [N = 2I, K]; the epilogue writes act =
+// bf16(act_fn(g) * u) for act columns [n0, n0 + BN/2) of an [rows, I]
+// output (g.ldo = I), g and u the bf16-rounded GEMM outputs, as the separate
+// activation kernel computes it.  A dense K-split unit writes its int32
+// partial tile in the same column order (gate half, then up half).
 // kWAux: cache policy of the weight DMA (0, or kStreamAux for weights that
 // only one block reads: a dense grid with a single row tile).
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1, int kWAux = 0,
@@ -558,8 +560,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   const int64_t a_base_row = Rows::kGrouped ? 0 : m0;
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       scalar_ptr(const_cast<int8_t*>(g.A + a_base_row * g.lda)), 0, 0x7fffffff, kBufferFlags);
-  static_assert(kAct < 0 || (Rows::kGrouped && epi_bf16_out(EPI)),
-                "fused activation: grouped bf16 with the staged epilogue (the host sets staged_out)");
+  static_assert(kAct < 0 || epi_bf16_out(EPI),
+                "fused activation: bf16 with the staged epilogue (the host sets staged_out)");
   constexpr int kHalfN = BN / 2;
   const int64_t half = g.N / 2;  // kAct: rows of each of the gate and up halves
   // weight row of tile row r (kAct: gate rows then the matching up rows)
@@ -922,7 +924,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 #pragma unroll
           for (int q0 = 0; q0 < BM * kActChunks; q0 += kThreads) {
             const int q = q0 + tid, r = q / kActChunks, ch = q % kActChunks;
-            const int64_t orow = meta_p[r];
+            int64_t orow;
+            if constexpr (Rows::kGrouped) {
+              orow = meta_p[r];
+            } else {
+              orow = m0 + r < g.M ? m0 + r : -1;
+            }
             const int64_t n = n0 + ch * 8;
             if (orow >= 0 && n < half) {
               const v4i gv = *reinterpret_cast<const v4i*>(lds + r * kRowBytes + (spos(r, ch) << 4));
@@ -1009,7 +1016,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
 // (XCD-contiguous), block full_tiles + u the K range u % tail_split of
 // tail tile u / tail_split (an int32 partial tile); without a split, block
 // b owns tile tile_of_block(b).
-template <int BM, int BN, int BK>
+// kAct: a tile of BN weight rows covers BN / 2 output (activation) columns.
+template <int BM, int BN, int BK, bool kAct = false>
 __device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, uint32_t b) {
   const uint32_t tm = static_cast<uint32_t>((g.M + BM - 1) / BM), tn = static_cast<uint32_t>((g.N + BN - 1) / BN);
   int64_t pm, pn, split_unit = -1;
@@ -1028,16 +1036,18 @@ __device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, uint32_t b)
   } else {
     tile_of_block(b, tm, tn, pm, pn);
   }
-  return TileJob{pm * BM, pn * BN, g.W, g.sw, kt_begin, kt_end, BM, split_unit};
+  return TileJob{pm * BM, pn * (kAct ? BN / 2 : BN), g.W, g.sw, kt_begin, kt_end, BM, split_unit};
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0, int MF = 32>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0, int MF = 32,
+          int kAct = -1>
 __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
   // pass only needs the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
   extern __shared__ __align__(16) unsigned char lds[];
   static_assert(!Rows::kRuns, "run tiles are walked by grouped_persist_kernel");
+  static_assert(kAct < 0 || !Rows::kGrouped, "grouped fused activation: grouped_persist_kernel");
   if constexpr (Rows::kGrouped) {
     // grouped grid: x = N tile, y = alignment block of BM sorted rows (an
     // XCD-contiguous walk of the (block, N tile) pairs measured slower at
@@ -1050,8 +1060,8 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
                       0, static_cast<int>(g.K / BK), BM, -1};
     tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, 0, MF>(g, lds, job);
   } else {
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, kWAux, MF>(g, lds,
-                                                                 dense_tile_job<BM, BN, BK>(g, blockIdx.x));
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kAct, kWAux, MF>(
+        g, lds, dense_tile_job<BM, BN, BK, (kAct >= 0)>(g, blockIdx.x));
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -2250,6 +2260,57 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
       if (n < g.N) static_cast<int32_t*>(g.out)[m * g.ldo + n] = a[j];
     }
   }
+}
+
+// K-split reduction of fused-activation tiles (kAct): a partial tile holds
+// the gate half of its columns, then the up half.  One thread per 8
+// activation columns of one tile row sums both halves in split order,
+// rounds g and u to bf16 as the tile epilogue does, and writes act =
+// bf16(act_fn(g) * u) to out[rows, N / 2] (N / 2 % 8 == 0, 16-byte rows).
+template <int BM, int BN, int kAct>
+__global__ __launch_bounds__(256) void split_reduce_act_kernel(GemmArgs g) {
+  constexpr int kH = BN / 2, kC8 = kH / 8;
+  const int64_t half = g.N / 2;
+  const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  const int64_t tail = tm * tn - g.full_tiles;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (tile, row, act col8)
+  if (idx >= tail * BM * kC8) return;
+  const int64_t tt = idx / (BM * kC8);
+  const int r = static_cast<int>((idx / kC8) % BM), c8 = static_cast<int>(idx % kC8) * 8;
+  int64_t pm, pn;
+  tile_of_index(g.full_tiles + tt, tm, tn, pm, pn);
+  const int64_t m = pm * BM + r, n0 = pn * kH + c8;
+  if (m >= g.M || n0 >= half) return;
+  const int32_t* p = g.part + (tt * g.tail_split) * (BM * BN) + r * BN + c8;
+  int32_t ga[8], ua[8];
+  for (int s = 0; s < g.tail_split; ++s) {
+    const int32_t* q = p + static_cast<int64_t>(s) * (BM * BN);
+    const v4i g0 = *reinterpret_cast<const v4i*>(q), g1 = *reinterpret_cast<const v4i*>(q + 4);
+    const v4i u0 = *reinterpret_cast<const v4i*>(q + kH), u1 = *reinterpret_cast<const v4i*>(q + kH + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ga[j] = s == 0 ? g0[j] : ga[j] + g0[j];
+      ga[4 + j] = s == 0 ? g1[j] : ga[4 + j] + g1[j];
+      ua[j] = s == 0 ? u0[j] : ua[j] + u0[j];
+      ua[4 + j] = s == 0 ? u1[j] : ua[4 + j] + u1[j];
+    }
+  }
+  const float sa = g.sa[m];
+  v4i o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t pk = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * w + h;
+      const int64_t n = n0 + j;
+      const float gv = bf16_to_f32(epi_bf16(ga[j], sa, g.sw[n], nullptr, n, 1.0f, false));
+      const float uv = bf16_to_f32(epi_bf16(ua[j], sa, g.sw[half + n], nullptr, half + n, 1.0f, false));
+      pk |= static_cast<uint32_t>(f32_to_bf16(act_fn<kAct>(gv) * uv)) << (16 * h);
+    }
+    o[w] = static_cast<int>(pk);
+  }
+  *reinterpret_cast<v4i*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n0) = o;
 }
 
 }  // namespace mw8

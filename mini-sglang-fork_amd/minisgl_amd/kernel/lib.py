@@ -43,6 +43,9 @@ SIGNATURES = {
     ),
     "mw8_gemm_w8a8_bf16_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "mw8_gemm_w8a8_i32": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _P, c_size_t, _P]),
+    "mw8_gemm_act_w8a8_bf16": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I64, _I64, _I64, _P, c_size_t, _P]),
+    "mw8_gemm_act_supported": (_I32, [_I64, _I64, _I64]),
+    "mw8_gemm_act_workspace_bytes": (c_size_t, [_I64, _I64, _I64]),
     "mw8_linear_bf16_w8a8": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "mw8_linear_bf16_supported": (_I32, [_I64, _I64, _I64]),
     "mw8_topk_softmax": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _P, _P]),

@@ -268,6 +268,58 @@ def gemm_w8a8(
     return y
 
 
+# Rows from which the gated MLP runs gate_up with the activation in its
+# epilogue.  MI355X, us, two-step (GEMM into [M, 2I], activation + requant)
+# -> fused (gemm_act_w8a8, then the requant of [M, I]): M 2080, I 25600
+# 625-641 -> 587-597; M 2080, I 6400 157-161 -> 154; M 4096 / 8192, I 17408
+# 693-703 -> 672, 1307-1311 -> 1262-1264; below it the two-step path is as
+# fast or faster (M 512, I 17408 124 -> 127; M 256, I 768 13.4 -> 28).
+GEMM_ACT_MIN_ROWS = 1024
+
+
+def gemm_act_supported(M: int, I: int, K: int) -> bool:
+    """Whether gemm_act_w8a8 takes (M, I, K) (host only; follows the tile
+    override): I % 8 == 0, K % 128 == 0 and a shape the plain GEMM at
+    (M, 2I, K) runs on its ring cores."""
+    return bool(load().mw8_gemm_act_supported(M, I, K))
+
+
+def gemm_act_w8a8(
+    q: torch.Tensor,
+    s_a: torch.Tensor,
+    w: torch.Tensor,
+    s_w: torch.Tensor,
+    activation: str = "silu",
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """y bf16 [M, I] = bf16(act(g) * u) of the W8A8 GEMM against a gate|up
+    weight w int8 [2I, K] (gate rows first; s_w fp32 [2I]): bit for bit
+    act_and_mul_quant(gemm_w8a8(q, s_a, w, s_w), activation,
+    return_act=True)[2], without the [M, 2I] gate|up output
+    (gemm_act_supported shapes)."""
+    M, N2, K = _check_gemm(q, w)
+    _need(N2 % 2 == 0, "W: [2I, K] gate|up rows")
+    I = N2 // 2
+    _need(activation in _ACT, f"unsupported activation {activation}")
+    _need(s_a.dtype == torch.float32 and s_a.shape == (M,) and s_a.is_contiguous(), "s_a: fp32 [M]")
+    _need(s_w.dtype == torch.float32 and s_w.shape == (N2,) and s_w.is_contiguous(), "s_w: fp32 [2I]")
+    y = out if out is not None else torch.empty((M, I), dtype=torch.bfloat16, device=q.device)
+    _need(y.dtype == torch.bfloat16 and y.shape == (M, I) and y.is_contiguous(), "bad out buffer")
+    if M == 0:
+        return y
+    with torch.cuda.device(q.device):
+        need = int(load().mw8_gemm_act_workspace_bytes(M, I, K))
+    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
+    with torch.cuda.device(q.device):
+        check(
+            load().mw8_gemm_act_w8a8_bf16(
+                _ptr(q), _ptr(s_a), _ptr(w), _ptr(s_w), _ACT[activation], _ptr(y), M, I, K, _ptr(ws),
+                0 if ws is None else ws.numel(), _stream(q),
+            )
+        )
+    return y
+
+
 def linear_bf16_supported(M: int, N: int, K: int) -> bool:
     """Whether linear_bf16_w8a8 takes a decode batch of this shape (host
     only; the answer follows the decode-configuration override)."""
@@ -695,6 +747,9 @@ __all__ = [
     "gemm_w8a8",
     "gemm_w8a8_i32",
     "linear_bf16_supported",
+    "GEMM_ACT_MIN_ROWS",
+    "gemm_act_supported",
+    "gemm_act_w8a8",
     "linear_bf16_w8a8",
     "topk_softmax",
     "moe_align_block_size",

@@ -183,6 +183,14 @@ def test_argument_errors_return_codes(lib):
     assert lin(None, 5120, FAKE_B, FAKE_C, None, FAKE_A, 1, 5120, 5120, None) == E["MW8_ERR_ARG"]
     assert lin(FAKE_A, 5120, FAKE_B, FAKE_C, None, FAKE_A, 5, 5120, 5120, None) == E["MW8_ERR_SHAPE"]
     assert lin(FAKE_A, 5124, FAKE_B, FAKE_C, None, FAKE_A, 2, 5120, 5120, None) == E["MW8_ERR_ALIGN"]
+    # the gate_up GEMM with the activation: null operand, bad activation, a decode shape, I % 8 != 0
+    act = lib.mw8_gemm_act_w8a8_bf16
+    assert act(None, FAKE_B, FAKE_C, FAKE_B, 0, FAKE_A, 2080, 25600, 5120, None, 0, None) == E["MW8_ERR_ARG"]
+    assert act(FAKE_A, FAKE_B, FAKE_C, FAKE_B, 2, FAKE_A, 2080, 25600, 5120, None, 0, None) == E["MW8_ERR_ARG"]
+    assert act(FAKE_A, FAKE_B, FAKE_C, FAKE_B, 0, FAKE_A, 1, 25600, 5120, None, 0, None) == E["MW8_ERR_SHAPE"]
+    assert act(FAKE_A, FAKE_B, FAKE_C, FAKE_B, 0, FAKE_A, 2080, 25604, 5120, None, 0, None) == E["MW8_ERR_SHAPE"]
+    assert lib.mw8_gemm_act_supported(2080, 25600, 5120) == 1 and lib.mw8_gemm_act_supported(8, 25600, 5120) == 0
+    assert lib.mw8_gemm_act_workspace_bytes(2080, 25600, 5120) > 0  # the short last wave splits along K
     # K % 16 != 0
     rc = lib.mw8_gemm_w8a8_i32(FAKE_A, FAKE_B, FAKE_C, 4, 8, 40, None, 0, None)
     assert rc == E["MW8_ERR_SHAPE"] and b"multiple of 16" in lib.mw8_last_error()
