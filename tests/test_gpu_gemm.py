@@ -347,7 +347,7 @@ def test_gemm_stream_walk(M, K, N, bias):
     assert bf16_bits_equal(y_stream[torch.as_tensor(rows, device=DEV)], y_ref).all()
 
 
-@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 7168), (1024, 6144), (1040, 520), (2048, 2056)])
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 7168), (1024, 6144), (1040, 520), (2048, 2056), (8192, 1024), (12288, 520)])
 def test_linear_bf16_fused_quant(K, N):
     """The one-launch decode linear (mw8_linear_bf16_w8a8: per-token
     quantization inside the decode GEMM) equals quant_per_token followed by
