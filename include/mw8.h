@@ -178,8 +178,9 @@ int mw8_gemm_w8a8_bf16(const int8_t* A, const float* sa, const int8_t* W, const 
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference.  The K split's partial tiles go to a static 64 MiB device
- * array of the library (held on every device it runs on until the process
- * ends, whether or not this entry is called); a split that would need more
+ * array of the library, in a code object of its own: a device holds it from
+ * the first call of this entry there until the process ends (the other
+ * entries never load it); a split that would need more
  * is not taken and those tiles run whole, as mw8_gemm_w8a8_bf16 does with a
  * short workspace (none needs more on a 256-CU MI355X: the bound is
  * mw8_gemm_workspace_max_bytes).
