@@ -15,9 +15,11 @@ copies, so no launch finds its weights in the 256 MB MALL.
 
 Printed (one JSON line): whole-step throughput in TOPS (value, wall clock
 over the K steps), per-shape time / TOPS / GB/s / roofline fraction from
-HIP events (the median of three passes enqueued back to back after the
-timed pass, so no graph waits for its host submission), the dominant
-kernel's roofline, the
+HIP events as the reference's perf_cuda takes them (each shape's graph
+replayed 10 times back to back between two events, per launch = elapsed /
+(10 K); the median of three such passes, after the timed region), the
+time of one replay between two events beside it, the dominant kernel's
+roofline, the
 CPU baseline (the CPU oracle, timed on the host on a bounded sample, plus
 the reference's bf16 ``F.linear`` CPU op on the same sample), and secondary
 measurements (quantizer at config 2, MoE layer tokens/s at config 3, the
@@ -47,6 +49,9 @@ for _p in (ROOT, os.path.join(ROOT, "mini-sglang-fork_amd")):
 
 METRIC = "W8A8 GEMM TOPS + HBM GB/s (roofline %) at M=1..8192; MoE layer tokens/s"
 HBM_PEAK_GBPS = 8000.0
+# back-to-back replays of a shape's graph per timed pass of its per-shape figure
+# (cuda_graph_repetitions x repetitions of python/minisgl/benchmark/perf.py:10-16)
+PERF_REPLAYS = 10
 INT8_OPS_PER_CLK_CU = 8192  # dense int8 MFMA ops per clock per CU (CDNA4)
 
 
@@ -471,7 +476,12 @@ def main() -> int:
         # Per-shape times: the first graphs after the synchronize wait for
         # the host to submit them, which the events count.  Three more
         # passes, enqueued back to back outside the timed region, run with
-        # the host ahead of the GPU; each shape reports their median.
+        # the host ahead of the GPU; each shape reports their median of one
+        # replay between two events (us_one_replay), and the median of three
+        # passes of 10 replays between two events (us), the reference's
+        # perf_cuda scheme (python/minisgl/benchmark/perf.py:10-51): the
+        # fixed start of a replay is then spread over 10 K launches, as the
+        # hundreds of nodes of a serving graph spread it.
         extra = []
         for _ in range(3):
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -481,19 +491,30 @@ def main() -> int:
                 g.replay()
                 e1.record(stream)
             extra.append(ev)
+        rep = []
+        for _ in range(3):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in plan]
+            for g, (e0, e1) in zip(graphs, ev):
+                e0.record(stream)
+                for _ in range(PERF_REPLAYS):
+                    g.replay()
+                e1.record(stream)
+            rep.append(ev)
         torch.cuda.synchronize()
     ops_step = sum(2.0 * M * N * K for M, _, K, N in plan)
     value = ops_step * args.steps / wall / 1e12
 
     shapes = []
     for i, (M, name, K, N) in enumerate(plan):
-        t = sorted(ev[i][0].elapsed_time(ev[i][1]) for ev in extra)[1] * 1e-3 / args.steps
+        t1 = sorted(ev[i][0].elapsed_time(ev[i][1]) for ev in extra)[1] * 1e-3 / args.steps
+        t = sorted(ev[i][0].elapsed_time(ev[i][1]) for ev in rep)[1] * 1e-3 / (PERF_REPLAYS * args.steps)
         ops = 2.0 * M * N * K
         nb = gemm_bytes(M, N, K)
         ai = ops / nb
         bound = "mfma" if ai >= peak_tops * 1e12 / (HBM_PEAK_GBPS * 1e9) else "hbm"
         shapes.append({
-            "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2),
+            "shape": name, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2), "us_one_replay": round(t1 * 1e6, 2),
             "tops": round(ops / t / 1e12, 2), "gbps": round(nb / t / 1e9, 1),
             "bound": bound, "roofline_frac": round(roofline_frac(ops, nb, t, peak_tops), 4),
             "kernel": lib.mw8_gemm_kernel_name(M, N, K).decode(),
@@ -516,8 +537,8 @@ def main() -> int:
         "kernel": f"{dom['kernel']} ({dom['shape']} M={dom['M']} K={dom['K']} N={dom['N']})",
         "per_launch": (f"{dom_ops / 1e9:.1f} GOP = 2*M*N*K and "
                        f"{gemm_bytes(dom['M'], dom['N'], dom['K']) / 1e6:.1f} MB algorithmic "
-                       f"per launch; time = HIP events around a graph of {args.steps} "
-                       f"launches on the launch stream / {args.steps}"),
+                       f"per launch; time = HIP events around {PERF_REPLAYS} back-to-back replays of "
+                       f"a graph of {args.steps} launches on the launch stream / {PERF_REPLAYS * args.steps}"),
     }
     log(f"step: {wall / args.steps * 1e3:.3f} ms, {value:.1f} TOPS; dominant {roofline['kernel']} "
         f"{dom['us']} us frac {dom['roofline_frac']}")
@@ -566,9 +587,10 @@ def main() -> int:
                          "o_proj(5120->5120) gate_up(5120->34816) down(17408->5120) x "
                          "M in {1,8,64,512,4096,8192}; one step = 24 GEMM launches"),
             "weight_copy_mb_per_shape": args.copy_mb,
-            "timing": ("value: wall clock over the K steps; per shape: HIP graph of `steps` "
-                       "launches replayed between HIP events, median of three back-to-back "
-                       "passes after the timed pass"),
+            "timing": ("value: wall clock over the K steps; per shape (us): HIP graph of `steps` "
+                       "launches replayed 10 times back to back between HIP events (the reference's "
+                       "perf_cuda), median of three passes after the timed pass; us_one_replay: one "
+                       "replay between HIP events, median of three back-to-back passes"),
             "ops_per_step": ops_step,
         },
         "device": peaks,
