@@ -256,13 +256,29 @@ int launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
   return kOk;
 }
 
+// The dense 256 x 256 ring streams its weight stages one stage ahead of its
+// A stages (2 A slots + 3 W slots of 32 KB, the whole LDS; the scale tables
+// move into the ring after the main loop).  Measured on MI355X (graph-timed,
+// rotating weights, us, lead 0 -> 1, bit-identical): gate_up M=8192
+// 1182.1 -> 1153.8, M=4096 620.3 -> 607.8; 8192 x 5120 x 17408 600.1 ->
+// 575.8; qkv M=8192 261.9 -> 259.3, M=4096 137.0 -> 132.5; 2080 x 10240 x
+// 5120 130.2 -> 122.8.  The weights' first touch comes from HBM, and one
+// stage of MFMA time does not cover it; the A panels mostly hit in L2.
+// The 128 x 128 (two per CU) and 64 x 128 rings gain 1-3% from the same
+// lead (256 x 5120 x 17408 49.6 -> 48.5, 256 x 7168 x 5120 33.4 -> 32.5;
+// 64 x 5120 x 17408 26.3 -> 25.8, 64 x 34816 x 5120 47.5 -> 46.7); the
+// 3-stage 256 x 128 ring, whose weights are already two stages ahead,
+// loses 1-4% with it (2080 x 10240 x 5120 120.3 -> 123.3) and keeps none.
+constexpr int kLead256 = 1, kLeadSmall = 1;
+
 // 128-byte K stages hold two 64-byte substeps of v_mfma_i32_16x16x64_i8
 // (the int8 MFMA with the higher power-limited rate on MI355X); 64-byte
 // stages run v_mfma_i32_32x32x32_i8 (two 32-byte substeps).
-template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0>
+template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0, int kBLead = 0>
 int launch_tile3(const GemmArgs& g, dim3 grid, hipStream_t st) {
-  constexpr int kLds = NSTAGE * (BM + BN) * BK;
-  constexpr auto kern = tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kWAux, BK == 128 ? 16 : 32>;
+  constexpr int kLds = NSTAGE * BM * BK + (NSTAGE + kBLead) * BN * BK;
+  constexpr auto kern =
+      tile3_gemm_kernel<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kWAux, BK == 128 ? 16 : 32, -1, kBLead>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   hipLaunchKernelGGL(kern, grid, dim3(64 * WM * WN), kLds, st, g);
   return kOk;
@@ -283,7 +299,8 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 128, false, 128, 2, false, "tile_gemm_kernel<128, 128, 128, 2, 2>"},
     // 1: ring, 4 waves (2x2), 4 stages, two per CU
     {128, 128, true, 64, 2, false, "tile3_gemm_kernel<128, 128, 64, 2, 2, 4>"},
-    // 2: ring, 8 waves (4x2), 2 stages
+    // 2: ring, 8 waves (4x2), 2 stages (the weight stages a stage further
+    // ahead, in a ring of 3: kLead256)
     {256, 256, true, 128, 1, true, "tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"},
     // 3: ring, 8 waves (4x2), 3 stages: grids of 129-256 tiles
     {256, 128, true, 128, 1, false, "tile3_gemm_kernel<256, 128, 128, 4, 2, 3>"},
@@ -577,15 +594,15 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   switch (cfg) {
     case 0: rc = launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 1: rc = launch_tile3<128, 128, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 2: rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 2: rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st); break;
     case 3: rc = launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 4:
-      rc = one_row ? launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows, kStreamAux>(g, dim3(tiles), st)
-                   : launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows>(g, dim3(tiles), st);
+      rc = one_row ? launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows, kStreamAux, kLeadSmall>(g, dim3(tiles), st)
+                   : launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows, 0, kLeadSmall>(g, dim3(tiles), st);
       break;
     case 5:
-      rc = one_row ? launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, kStreamAux>(g, dim3(tiles), st)
-                   : launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows>(g, dim3(tiles), st);
+      rc = one_row ? launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, kStreamAux, kLeadSmall>(g, dim3(tiles), st)
+                   : launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, 0, kLeadSmall>(g, dim3(tiles), st);
       break;
     case 6: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: {
@@ -593,7 +610,7 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
       if (EPI == kEpiBf16 && tiles >= cus && stream_fits(g, g.M, g.N))
         rc = launch_stream<false>(g, static_cast<unsigned>(cus), st);
       else
-        rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st);
+        rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st);
       break;
     }
   }
@@ -771,10 +788,10 @@ int act_tile_cfg(int64_t M, int64_t N2, int64_t K) {
   return M > 128 ? 2 : 4;
 }
 
-template <int BM, int BN, int WM, int WN, int NSTAGE, int kAct>
+template <int BM, int BN, int WM, int WN, int NSTAGE, int kAct, int kBLead = 0>
 int launch_tile3_act(const GemmArgs& g, unsigned tiles, hipStream_t st) {
-  constexpr int kLds = NSTAGE * (BM + BN) * 128;
-  constexpr auto kern = tile3_gemm_kernel<BM, BN, 128, WM, WN, NSTAGE, kEpiBf16, DenseRows, 0, 16, kAct>;
+  constexpr int kLds = NSTAGE * BM * 128 + (NSTAGE + kBLead) * BN * 128;
+  constexpr auto kern = tile3_gemm_kernel<BM, BN, 128, WM, WN, NSTAGE, kEpiBf16, DenseRows, 0, 16, kAct, kBLead>;
   if (const int rc = set_lds_limit<kern>(kLds)) return rc;
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, st, g);
   return kOk;
@@ -793,9 +810,9 @@ int dispatch_act(const GemmArgs& g, int cfg, unsigned tiles, bool split, const S
   int rc;
   switch (cfg) {
     case 3: rc = launch_tile3_act<256, 128, 4, 2, 3, kAct>(g, tiles, st); break;
-    case 4: rc = launch_tile3_act<128, 128, 2, 2, 2, kAct>(g, tiles, st); break;
-    case 5: rc = launch_tile3_act<64, 128, 1, 4, 4, kAct>(g, tiles, st); break;
-    default: rc = launch_tile3_act<256, 256, 4, 2, 2, kAct>(g, tiles, st); break;
+    case 4: rc = launch_tile3_act<128, 128, 2, 2, 2, kAct, kLeadSmall>(g, tiles, st); break;
+    case 5: rc = launch_tile3_act<64, 128, 1, 4, 4, kAct, kLeadSmall>(g, tiles, st); break;
+    default: rc = launch_tile3_act<256, 256, 4, 2, 2, kAct, kLead256>(g, tiles, st); break;
   }
   if (rc != kOk || !split) return rc;
   switch (cfg) {

@@ -416,6 +416,20 @@ __device__ __forceinline__ void wait_stages(int n) {
   wait_vmcnt_lgkm0<0>();
 }
 
+// Weight-lead rings: wait until a stage has landed while the loads issued
+// after its A stage stay in flight: W stages for the next r stages and A
+// stages for the next min(r, AMAX), L_A / L_B loads each (r <= MAXR <= 4).
+template <int LA, int LB, int MAXR, int AMAX>
+__device__ __forceinline__ void wait_lead(int r) {
+  static_assert(MAXR <= 4 && (4 * LB + 4 * LA) < 64, "vmcnt range");
+  constexpr auto cnt = [](int n) { return n * LB + (n < AMAX ? n : AMAX) * LA; };
+  if constexpr (MAXR >= 4) { if (r >= 4) { wait_vmcnt_lgkm0<cnt(4)>(); return; } }
+  if constexpr (MAXR >= 3) { if (r == 3) { wait_vmcnt_lgkm0<cnt(3)>(); return; } }
+  if constexpr (MAXR >= 2) { if (r == 2) { wait_vmcnt_lgkm0<cnt(2)>(); return; } }
+  if constexpr (MAXR >= 1) { if (r == 1) { wait_vmcnt_lgkm0<cnt(1)>(); return; } }
+  wait_vmcnt_lgkm0<0>();
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // A pointer the compiler can prove wave-uniform (it lives in SGPRs).  A
@@ -501,7 +515,7 @@ struct TileJob {
 // kWAux: cache policy of the weight DMA (0, or kStreamAux for weights that
 // only one block reads: a dense grid with a single row tile).
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kAct = -1, int kWAux = 0,
-          int MF = 32>
+          int MF = 32, int kBLead = 0>
 __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds, const TileJob& job) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using Mf = MfmaI8<MF>;
@@ -521,6 +535,18 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   static_assert(kLA >= 1 && kLB >= 1 && kLA * kRowsPerInst * kWaves == BM &&
                 kLB * kRowsPerInst * kWaves == BN, "DMA split");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5 && (NSTAGE - 2) * kL < 64, "stages");
+  // kBLead = 1: the weight stages run one stage ahead of the A stages, in a
+  // ring of NSTAGE + 1 slots beside the A ring of NSTAGE (on a 256 x 256
+  // tile the 2 + 3 slots of 32 KB fill the CU's 160 KB), so each weight
+  // stage has one stage more of MFMA time to arrive from HBM.  The scale
+  // tables then live in the ring, written after the main loop.  Issue
+  // order: A0 W0, then W s A s for s < NSTAGE, then W NSTAGE; stage kt of
+  // the main loop issues A kt+NSTAGE and W kt+NSTAGE+1.  Every W stage is
+  // thus issued before its A stage, and the loads issued after A j are W
+  // j+1, A j+1, W j+2, ... (wait_lead counts them).
+  static_assert(kBLead == 0 || (kBLead == 1 && MF == 16 && NSTAGE <= 4 && !Rows::kGrouped), "weight lead");
+  constexpr int kBSlots = NSTAGE + kBLead;
+  constexpr int kRingBytes = NSTAGE * kStageA + kBSlots * kStageB;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave / WN, wn = wave % WN;
@@ -545,11 +571,23 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   constexpr bool kMetaSa = epi_bf16_out(EPI);
   static_assert(!kMetaSa || (BM <= 64 * kWaves && BN <= 64 * kWaves), "one metadata row per thread");
   __shared__ int32_t meta_p[kMeta ? BM : 1];
-  __shared__ float meta_sa[kMetaSa ? BM : 1], meta_rt[kMeta ? BM : 1];
-  __shared__ float meta_sw[kMetaSa ? BN : 1], meta_bias[kMetaSa && !Rows::kGrouped ? BN : 1];
-  // ring + these tables + the persistent walk's run tables fit in the CU's 160 KB
-  static_assert(NSTAGE * kStage + 4 * (3 * BM + 2 * BN) + 4 * (2 * kPersistMaxSlots + 2 + 16) <= 163840,
-                "LDS budget");
+  __shared__ float meta_rt[kMeta ? BM : 1];
+  constexpr bool kTabInRing = kBLead > 0;  // the dense tables past the staged bf16 tile
+  float *meta_sa, *meta_sw, *meta_bias;
+  if constexpr (kTabInRing) {
+    meta_sa = reinterpret_cast<float*>(lds + BM * BN * 2);
+    meta_sw = meta_sa + BM;
+    meta_bias = meta_sw + BN;
+    static_assert(kRingBytes <= 163840 && BM * BN * 2 + 4 * (BM + 2 * BN) <= kRingBytes, "LDS budget");
+  } else {
+    __shared__ float t_sa[kMetaSa ? BM : 1], t_sw[kMetaSa ? BN : 1], t_bias[kMetaSa && !Rows::kGrouped ? BN : 1];
+    meta_sa = t_sa;
+    meta_sw = t_sw;
+    meta_bias = t_bias;
+    // ring + these tables + the persistent walk's run tables fit in the CU's 160 KB
+    static_assert(kRingBytes + 4 * (3 * BM + 2 * BN) + 4 * (2 * kPersistMaxSlots + 2 + 16) <= 163840,
+                  "LDS budget");
+  }
   int32_t meta_pv = 0;
   float meta_sav = 0.0f, meta_rtv = 1.0f, meta_swv = 0.0f, meta_bv = 0.0f;
   if constexpr (kMeta) {
@@ -614,17 +652,34 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
     w_doff[j] = static_cast<uint32_t>((wrow - w_base_row) * g.K + 16 * c);
   }
   const int nk = kt_end - kt_begin;
-  auto issue = [&](int kt) {
-    unsigned char* base = lds + (kt % NSTAGE) * kStage;
+  // LDS slots of stage kt: A and W side by side in one ring, or (kBLead)
+  // the A ring followed by the W ring
+  auto a_slot = [&](int kt) -> unsigned char* {
+    return lds + (kBLead ? (kt % NSTAGE) * kStageA : (kt % NSTAGE) * kStage);
+  };
+  auto b_slot = [&](int kt) -> unsigned char* {
+    if constexpr (kBLead > 0) return lds + NSTAGE * kStageA + (kt % kBSlots) * kStageB;
+    else return lds + (kt % NSTAGE) * kStage + kStageA;
+  };
+  auto issue_a = [&](int kt) {
+    unsigned char* base = a_slot(kt);
     const int k0 = (kt_begin + kt) * BK;
 #pragma unroll
     for (int j = 0; j < kLA; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + (j * kWaves + wave) * 1024), 16,
                                                a_doff[j], k0, 0, 0);
+  };
+  auto issue_b = [&](int kt) {
+    unsigned char* base = b_slot(kt);
+    const int k0 = (kt_begin + kt) * BK;
 #pragma unroll
     for (int j = 0; j < kLB; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(base + kStageA + (j * kWaves + wave) * 1024), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(base + (j * kWaves + wave) * 1024), 16,
                                                w_doff[j], k0, 0, kWAux);
+  };
+  auto issue = [&](int kt) {
+    issue_a(kt);
+    issue_b(kt);
   };
 
   const int frow = lane & (MF - 1), fgrp = lane / MF;
@@ -675,10 +730,22 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   };
   constexpr int kSub = BK / Mf::kK;  // k-substeps per stage (2 or 4)
 
-  // prologue: stages 0 .. NSTAGE-1 in flight, stage 0 landed, its fragments read
+  // prologue: stages 0 .. NSTAGE-1 in flight (kBLead: A0 W0 W1 A1 W2), stage
+  // 0 landed, its fragments read
+  if constexpr (kBLead > 0) {
+    issue(0);
 #pragma unroll
-  for (int s = 0; s < NSTAGE; ++s)
-    if (s < nk) issue(s);
+    for (int s = 1; s < NSTAGE; ++s)
+      if (s < nk) {
+        issue_b(s);
+        issue_a(s);
+      }
+    if (NSTAGE < nk) issue_b(NSTAGE);
+  } else {
+#pragma unroll
+    for (int s = 0; s < NSTAGE; ++s)
+      if (s < nk) issue(s);
+  }
   if constexpr (kMeta) {
     if (tid < BM) {  // visible to every wave after the barriers of the main loop
       const bool ok = meta_pv < g.num_valid;
@@ -686,16 +753,21 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       meta_sa[tid] = ok ? meta_sav : 0.0f;
       meta_rt[tid] = ok ? meta_rtv : 0.0f;
     }
-  } else if constexpr (kMetaSa) {
+  } else if constexpr (kMetaSa && !kTabInRing) {
     if (tid < BM) meta_sa[tid] = meta_sav;
   }
-  if constexpr (kMetaSa) {
+  if constexpr (kMetaSa && !kTabInRing) {
     if (tid < BN) {
       meta_sw[tid] = meta_swv;
       if constexpr (!Rows::kGrouped) meta_bias[tid] = meta_bv;
     }
   }
-  wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
+  if constexpr (kBLead > 0) {
+    // stage 0 (A0 W0) landed; W 1..NSTAGE and A 1..NSTAGE-1 may be in flight
+    wait_lead<kLA, kLB, NSTAGE, NSTAGE - 1>(nk - 1 < NSTAGE ? nk - 1 : NSTAGE);
+  } else {
+    wait_stages<kL, NSTAGE - 1>(nk - 1 < NSTAGE - 1 ? nk - 1 : NSTAGE - 1);
+  }
   raw_barrier();
   if constexpr (MF == 16) {
     // Two 64-byte substeps per stage.  The B fragments roll: fragment j of
@@ -710,7 +782,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
     static_assert(kSub == 2, "16x16x64 ring: 128-byte stages");
     constexpr int kASets = 4 * (2 * kFM + kFN) + 4 * kFM * kFN > 200 ? 1 : 2;
     auto read_a1 = [&](int kt, int ks, int set, int i) {
-      const unsigned char* la = lds + (kt % NSTAGE) * kStage;
+      const unsigned char* la = a_slot(kt);
       fa[set][i] = *reinterpret_cast<const v4i*>(la + swz_lds<BK>(a_off[i], 2 * fgrp + ks));
     };
     auto read_a = [&](int kt, int ks, int set) {
@@ -718,7 +790,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
       for (int i = 0; i < kFM; ++i) read_a1(kt, ks, set, i);
     };
     auto read_b = [&](int kt, int ks, int j) {
-      const unsigned char* lb = lds + (kt % NSTAGE) * kStage + kStageA;
+      const unsigned char* lb = b_slot(kt);
       fb[0][j] = *reinterpret_cast<const v4i*>(lb + swz_lds<BK>(b_off[j], 2 * fgrp + ks));
     };
     // MFMAs of column block j on A set `set`; with one A set, the last
@@ -742,8 +814,14 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         col(0, j, kt, 1);
         read_b(kt, 1, j);
       }
-      const int later = nk - 2 - kt;  // stages after kt+1 already issued
-      wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
+      if constexpr (kBLead > 0) {
+        // issued after stage kt+1's A: W kt+2 .. kt+NSTAGE, A kt+2 .. kt+NSTAGE-1
+        const int r = nk - 2 - kt;
+        wait_lead<kLA, kLB, NSTAGE - 1, NSTAGE - 2>(r < NSTAGE - 1 ? r : NSTAGE - 1);
+      } else {
+        const int later = nk - 2 - kt;  // stages after kt+1 already issued
+        wait_stages<kL, NSTAGE - 2>(later < NSTAGE - 2 ? later : NSTAGE - 2);
+      }
       raw_barrier();
       if constexpr (kASets == 2) read_a(kt + 1, 0, 0);
 #pragma unroll
@@ -751,7 +829,12 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
         col(1, j, kt + 1, 0);
         read_b(kt + 1, 0, j);
       }
-      if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+      if constexpr (kBLead > 0) {
+        if (kt + NSTAGE < nk) issue_a(kt + NSTAGE);
+        if (kt + NSTAGE + 1 < nk) issue_b(kt + NSTAGE + 1);
+      } else {
+        if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+      }
     }
     if constexpr (kASets == 2) read_a(nk - 1, 1, 1);
 #pragma unroll
@@ -820,7 +903,7 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   // R+4, R+5 per instruction) and the 16-byte row reads on distinct LDS
   // banks.  A tile whose bf16 image exceeds the ring is staged in row
   // passes of whole wave rows (kStagePasses).
-  constexpr int kRing = NSTAGE * kStage;
+  constexpr int kRing = kRingBytes;
   constexpr int kStagePasses = (BM * BN * 2 + kRing - 1) / kRing;
   constexpr int kPassRows = BM / kStagePasses;
   constexpr bool kStaged = epi_bf16_out(EPI) && BN >= 128 && kStagePasses <= 2 &&
@@ -828,6 +911,15 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
   static_assert(kAct < 0 || (kStaged && kStagePasses == 1), "fused activation: one staging pass");
   if constexpr (kStaged) {
     if (g.staged_out) {
+      if constexpr (kTabInRing) {  // every wave past its last fragment read; then the tables
+        __syncthreads();
+        if (tid < BM) meta_sa[tid] = meta_sav;
+        if (tid < BN) {
+          meta_sw[tid] = meta_swv;
+          meta_bias[tid] = meta_bv;
+        }
+        __syncthreads();
+      }
       constexpr int kRowBytes = BN * 2;
       constexpr int kChunksRow = BN / 8;
       // MF = 32: one word-store instruction covers rows R, R+1, R+4, R+5 (64
@@ -870,7 +962,8 @@ __device__ __forceinline__ void tile3_run(const GemmArgs& g, unsigned char* lds,
           for (int v = 0; v < kV; ++v) {
             const int r = wm * kWaveM + MF * i + Mf::row(lane, v);
             r_sa[v] = meta_sa[r];
-            r_rt[v] = kRouted ? meta_rt[r] : 1.0f;
+            if constexpr (kRouted) r_rt[v] = meta_rt[r];
+            else r_rt[v] = 1.0f;
           }
 #pragma unroll
           for (int vp = 0; vp < kV / 2; ++vp) {
@@ -1040,7 +1133,7 @@ __device__ __forceinline__ TileJob dense_tile_job(const GemmArgs& g, uint32_t b)
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int NSTAGE, int EPI, class Rows, int kWAux = 0, int MF = 32,
-          int kAct = -1>
+          int kAct = -1, int kBLead = 0>
 __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
   // The body uses device-only builtins (LDS DMA, raw waitcnt); the host
   // pass only needs the launch stub.
@@ -1060,7 +1153,7 @@ __global__ __launch_bounds__(64 * WM * WN) void tile3_gemm_kernel(GemmArgs g) {
                       0, static_cast<int>(g.K / BK), BM, -1};
     tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, -1, 0, MF>(g, lds, job);
   } else {
-    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kAct, kWAux, MF>(
+    tile3_run<BM, BN, BK, WM, WN, NSTAGE, EPI, Rows, kAct, kWAux, MF, kBLead>(
         g, lds, dense_tile_job<BM, BN, BK, (kAct >= 0)>(g, blockIdx.x));
   }
 #endif  // __HIP_DEVICE_COMPILE__
