@@ -394,13 +394,17 @@ SplitPlan plan_split(int64_t M, int64_t N, int64_t K, const TileCfg& c) {
 // resident on the busiest CU), plus the K split's partial tiles (written
 // and read back at ~4 TB/s) and its reduction launch, floored by the
 // weight stream (~3.6 TB/s for these tilings).  Rates (TOPS per CU) fitted
-// to MI355X sweeps of the Qwen3-14B shapes at M = 40 - 8192.
+// to MI355X sweeps of the Qwen3-14B shapes at M = 40 - 8192.  The 256x256
+// rate was raised with the weight lead (us, 256x256 vs 256x320, same box):
+// 4096 x 34816 x 5120 632.1 vs 659.3, 8192 x 7168 x 5120 263.3 vs 276.1;
+// the N = 5120 shapes keep 256x320's whole waves (8192 x 5120 x 17408 597.7
+// vs 572.9, 4096 x 5120 x 5120 117.9 vs 101.7).
 struct ModelCfg {
   int cfg;
   double c0, r1, r2;  // us per wave; rate with one / two blocks per CU
 };
 constexpr ModelCfg kModelCfgs[] = {
-    {2, 5.0, 9.2, 9.2},     // 256x256, 8 waves
+    {2, 5.0, 9.8, 9.8},     // 256x256, 8 waves, weight lead (gate_up M=4096 and qkv M=8192 over 256x320)
     {4, 3.0, 3.7, 6.1},     // 128x128 BK 128, 2 stages, two per CU
     {1, 3.0, 4.6, 5.9},     // 128x128 BK 64, 4 stages, two per CU
     {5, 3.0, 3.36, 3.36},   // 64x128, 4 stages

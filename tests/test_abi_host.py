@@ -369,16 +369,17 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     decode cores up to 8 rows (the shared token ring for the wide gate_up at
     8 rows), in-block split-K for qkv / o_proj at 64 and 512 rows, the
     shared token ring for gate_up and the 64x128 ring for the deep down at
-    64 rows, and the 256x256 or 256x320 rings (whichever fills whole waves)
-    above."""
+    64 rows, and above the 256x256 ring (its weight stages a stage ahead)
+    or, where it fills whole waves and 256x256 does not (N = 5120), the
+    256x320 ring."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
     sq, wide = t3.format(256, 256, 4, 2, 2), t3.format(256, 320, 4, 2, 2)
     ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
     r64 = t3.format(64, 128, 1, 4, 4)
     expect = {
-        (5120, 7168): [ks64, ks512, sq, wide],
+        (5120, 7168): [ks64, ks512, sq, sq],
         (5120, 5120): [ks64, ks512, wide, wide],
-        (5120, 34816): ["decode_sx_gemm_kernel", wide, wide, sq],
+        (5120, 34816): ["decode_sx_gemm_kernel", wide, sq, sq],
         (17408, 5120): [r64, sq, wide, wide],
     }
     for (K, N), names in expect.items():
