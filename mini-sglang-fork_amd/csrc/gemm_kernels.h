@@ -10,10 +10,11 @@
 // Cores:
 //   tile_gemm_kernel  -- register-staged MFMA tile (any K % 16 == 0).
 //   tile3_gemm_kernel -- the large-M ring: direct-to-LDS DMA of A and W
-//                  tiles, NSTAGE-deep ring, v_mfma_i32_16x16x64_i8 on
-//                  128-byte stages (v_mfma_i32_32x32x32_i8 on 64-byte
-//                  ones), K split of the last partial wave of tiles
-//                  (split_reduce_kernel).
+//                  tiles, NSTAGE-deep ring (optionally the W stages one
+//                  stage further ahead in a ring of their own: kBLead),
+//                  v_mfma_i32_16x16x64_i8 on 128-byte stages
+//                  (v_mfma_i32_32x32x32_i8 on 64-byte ones), K split of
+//                  the last partial wave of tiles (split_reduce_kernel).
 //   grouped_persist_kernel -- the same ring walking (expert chunk, column
 //                  tile) items of the fused-MoE GEMM.
 //   (gemm_ksplit.h: in-block split-K tiles for 33-768 rows; gemm_stream.h:
