@@ -277,6 +277,30 @@ def test_gemm_every_tile_config(M, K, N, bias):
         lib.mw8_set_tuning(-1, -1, -1)
 
 
+@pytest.mark.parametrize("K", [128, 256, 384, 640])
+@pytest.mark.parametrize("M,N", [(1040, 1040), (4096, 2048)])
+def test_gemm_rings_short_k(M, K, N):
+    """Every tile configuration at 1-5 K stages of 128 bytes: the prologue
+    and tail of the rings whose weight stages run ahead of their A stages
+    (fewer stages than ring slots, whole tiles at 4096 x 2048 and K-split
+    tiles at 1040 x 1040), against the oracle."""
+    from minisgl_amd.kernel.lib import load
+
+    announce(f"gemm rings short K M={M} K={K} N={N}")
+    c = linear_case(M, K, N, seed=K + N, bias=True)
+    q, s = quant_per_token(c["x"].to(DEV))
+    w, s_w, b = c["w"].to(DEV), c["s_w"].to(DEV), c["bias"].to(DEV)
+    q_ref, s_ref = orc.quant_per_token(f32(c["x"]))
+    acc_ref = orc.gemm_i32(q_ref, c["w"].numpy())
+    y_ref = orc.epilogue(acc_ref, s_ref, c["s_w"].numpy(), f32(c["bias"]))
+    lib = load()
+    try:
+        for cfg in range(_tuning_count(1)):
+            lib.mw8_set_tuning(-1, cfg, -1)
+            np.testing.assert_array_equal(gemm_w8a8_i32(q, w).cpu().numpy(), acc_ref, err_msg=f"cfg {cfg}")
+            assert bf16_bits_equal(gemm_w8a8(q, s, w, s_w, b), y_ref).all(), f"cfg {cfg}"
+    finally:
+        lib.mw8_set_tuning(-1, -1, -1)
 
 
 @pytest.mark.parametrize(
