@@ -304,12 +304,13 @@ constexpr TileCfg kTileCfgs[] = {
     {256, 256, true, 128, 1, true, "tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"},
     // 3: ring, 8 waves (4x2), 3 stages: grids of 129-256 tiles
     {256, 128, true, 128, 1, false, "tile3_gemm_kernel<256, 128, 128, 4, 2, 3>"},
-    // 4: ring, 4 waves (2x2), 2 stages, two per CU
+    // 4: ring, 4 waves (2x2), 2 stages (weight lead: kLeadSmall), two per CU
     {128, 128, true, 128, 2, true, "tile3_gemm_kernel<128, 128, 128, 2, 2, 2>"},
-    // 5: ring, 4 waves (1x4), 4 stages
+    // 5: ring, 4 waves (1x4), 4 stages (weight lead: kLeadSmall)
     {64, 128, true, 128, 1, true, "tile3_gemm_kernel<64, 128, 128, 1, 4, 4>"},
     // 6: ring, 8 waves (4x2), 2 stages, the bf16 tile staged in two row
-    // passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs
+    // passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs (no
+    // LDS for a weight lead: 2 x 32 KB A + 3 x 40 KB W would be 184 KB)
     {256, 320, true, 128, 1, false, "tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"},
     // 7: the pipelined persistent walk over 256x256 tiles (bf16 output, at
     // least 6 K stages and one tile per CU; else as cfg 2)
