@@ -269,6 +269,11 @@ int launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
 // 64 x 5120 x 17408 26.3 -> 25.8, 64 x 34816 x 5120 47.5 -> 46.7); the
 // 3-stage 256 x 128 ring, whose weights are already two stages ahead,
 // loses 1-4% with it (2080 x 10240 x 5120 120.3 -> 123.3) and keeps none.
+// With the lead the 256 x 256 tile runs its 8 waves as 2 x 4 of 128 x 64
+// (one A fragment set, re-read during the last column block) rather than
+// 4 x 2 of 64 x 128: 8 alternating rounds, us, 4x2 -> 2x4, bit-identical:
+// gate_up M=8192 1153.7 -> 1142.4, M=4096 608.7 -> 604.2; 2080 x 10240 x
+// 5120 125.9 -> 125.0; qkv M=8192 256.4 -> 256.2.
 constexpr int kLead256 = 1, kLeadSmall = 1;
 
 // 128-byte K stages hold two 64-byte substeps of v_mfma_i32_16x16x64_i8
@@ -299,9 +304,9 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 128, false, 128, 2, false, "tile_gemm_kernel<128, 128, 128, 2, 2>"},
     // 1: ring, 4 waves (2x2), 4 stages, two per CU
     {128, 128, true, 64, 2, false, "tile3_gemm_kernel<128, 128, 64, 2, 2, 4>"},
-    // 2: ring, 8 waves (4x2), 2 stages (the weight stages a stage further
-    // ahead, in a ring of 3: kLead256)
-    {256, 256, true, 128, 1, true, "tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"},
+    // 2: ring, 8 waves (2x4 of 128 x 64), 2 stages (the weight stages a
+    // stage further ahead, in a ring of 3: kLead256)
+    {256, 256, true, 128, 1, true, "tile3_gemm_kernel<256, 256, 128, 2, 4, 2>"},
     // 3: ring, 8 waves (4x2), 3 stages: grids of 129-256 tiles
     {256, 128, true, 128, 1, false, "tile3_gemm_kernel<256, 128, 128, 4, 2, 3>"},
     // 4: ring, 4 waves (2x2), 2 stages (weight lead: kLeadSmall), two per CU
@@ -599,7 +604,7 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
   switch (cfg) {
     case 0: rc = launch_tile<128, 128, 128, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 1: rc = launch_tile3<128, 128, 64, 2, 2, 4, EPI, DenseRows>(g, dim3(tiles), st); break;
-    case 2: rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st); break;
+    case 2: rc = launch_tile3<256, 256, 128, 2, 4, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st); break;
     case 3: rc = launch_tile3<256, 128, 128, 4, 2, 3, EPI, DenseRows>(g, dim3(tiles), st); break;
     case 4:
       rc = one_row ? launch_tile3<128, 128, 128, 2, 2, 2, EPI, DenseRows, kStreamAux, kLeadSmall>(g, dim3(tiles), st)
@@ -615,7 +620,7 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
       if (EPI == kEpiBf16 && tiles >= cus && stream_fits(g, g.M, g.N))
         rc = launch_stream<false>(g, static_cast<unsigned>(cus), st);
       else
-        rc = launch_tile3<256, 256, 128, 4, 2, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st);
+        rc = launch_tile3<256, 256, 128, 2, 4, 2, EPI, DenseRows, 0, kLead256>(g, dim3(tiles), st);
       break;
     }
   }
@@ -817,7 +822,7 @@ int dispatch_act(const GemmArgs& g, int cfg, unsigned tiles, bool split, const S
     case 3: rc = launch_tile3_act<256, 128, 4, 2, 3, kAct>(g, tiles, st); break;
     case 4: rc = launch_tile3_act<128, 128, 2, 2, 2, kAct, kLeadSmall>(g, tiles, st); break;
     case 5: rc = launch_tile3_act<64, 128, 1, 4, 4, kAct, kLeadSmall>(g, tiles, st); break;
-    default: rc = launch_tile3_act<256, 256, 4, 2, 2, kAct, kLead256>(g, tiles, st); break;
+    default: rc = launch_tile3_act<256, 256, 2, 4, 2, kAct, kLead256>(g, tiles, st); break;
   }
   if (rc != kOk || !split) return rc;
   switch (cfg) {

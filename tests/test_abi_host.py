@@ -79,7 +79,7 @@ def test_version_and_pure_host_helpers(lib):
     # automatic: N = 5120 at 4096 rows runs 256x320 tiles, 256 of them (no split)
     assert lib.mw8_gemm_kernel_name(4096, 5120, 5120) == b"tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"
     assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 0
-    assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) == b"tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"
+    assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) == b"tile3_gemm_kernel<256, 256, 128, 2, 4, 2>"
     assert lib.mw8_gemm_workspace_bytes(8192, 34816, 5120) == 0  # 4352 tiles: whole waves
     assert lib.mw8_gemm_workspace_bytes(4096, 7168, 5120) == 0   # 192 tail tiles: no split
     assert lib.mw8_gemm_workspace_bytes(512, 5120, 5120 + 64) == 0  # K % 128 != 0
@@ -99,7 +99,7 @@ def test_tuning_override_is_per_thread(lib):
     another thread, before and while it holds, sees the automatic tiling."""
     import threading
 
-    auto = b"tile3_gemm_kernel<256, 256, 128, 4, 2, 2>"
+    auto = b"tile3_gemm_kernel<256, 256, 128, 2, 4, 2>"
     seen = []
     lib.mw8_set_tuning(-1, 5, -1)
     try:
@@ -373,7 +373,7 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     or, where it fills whole waves and 256x256 does not (N = 5120), the
     256x320 ring."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
-    sq, wide = t3.format(256, 256, 4, 2, 2), t3.format(256, 320, 4, 2, 2)
+    sq, wide = t3.format(256, 256, 2, 4, 2), t3.format(256, 320, 4, 2, 2)
     ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
     r64 = t3.format(64, 128, 1, 4, 4)
     expect = {
