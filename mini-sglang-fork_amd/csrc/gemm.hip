@@ -273,7 +273,12 @@ int launch_tile(const GemmArgs& g, dim3 grid, hipStream_t st) {
 // (one A fragment set, re-read during the last column block) rather than
 // 4 x 2 of 64 x 128: 8 alternating rounds, us, 4x2 -> 2x4, bit-identical:
 // gate_up M=8192 1153.7 -> 1142.4, M=4096 608.7 -> 604.2; 2080 x 10240 x
-// 5120 125.9 -> 125.0; qkv M=8192 256.4 -> 256.2.
+// 5120 125.9 -> 125.0; qkv M=8192 256.4 -> 256.2.  The 256 x 320 ring
+// (no lead) gains more from 2 x 4 waves of 128 x 80, which spill 60 bytes
+// per lane against 144 for 4 x 2 of 64 x 160 (6 alternating rounds, us):
+// 8192 x 5120 x 17408 575.3 -> 534.3, 8192 x 5120 x 5120 193.8 -> 175.4,
+// 4096 x 5120 x 17408 298.9 -> 276.8, 4096 x 5120 x 5120 103.5 -> 91.9,
+// 512 x 34816 x 5120 104.7 -> 99.1.
 constexpr int kLead256 = 1, kLeadSmall = 1;
 
 // 128-byte K stages hold two 64-byte substeps of v_mfma_i32_16x16x64_i8
@@ -313,10 +318,10 @@ constexpr TileCfg kTileCfgs[] = {
     {128, 128, true, 128, 2, true, "tile3_gemm_kernel<128, 128, 128, 2, 2, 2>"},
     // 5: ring, 4 waves (1x4), 4 stages (weight lead: kLeadSmall)
     {64, 128, true, 128, 1, true, "tile3_gemm_kernel<64, 128, 128, 1, 4, 4>"},
-    // 6: ring, 8 waves (4x2), 2 stages, the bf16 tile staged in two row
-    // passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs (no
-    // LDS for a weight lead: 2 x 32 KB A + 3 x 40 KB W would be 184 KB)
-    {256, 320, true, 128, 1, false, "tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"},
+    // 6: ring, 8 waves (2x4 of 128 x 80), 2 stages, the bf16 tile staged in
+    // two row passes: N = 5120 at 4096 / 8192 rows in whole waves of the CUs
+    // (no LDS for a weight lead: 2 x 32 KB A + 3 x 40 KB W would be 184 KB)
+    {256, 320, true, 128, 1, false, "tile3_gemm_kernel<256, 320, 128, 2, 4, 2>"},
     // 7: the pipelined persistent walk over 256x256 tiles (bf16 output, at
     // least 6 K stages and one tile per CU; else as cfg 2)
     {256, 256, true, 128, 1, false, "stream_gemm_kernel<256, 0, false, -1>"},
@@ -404,7 +409,9 @@ SplitPlan plan_split(int64_t M, int64_t N, int64_t K, const TileCfg& c) {
 // rate was raised with the weight lead (us, 256x256 vs 256x320, same box):
 // 4096 x 34816 x 5120 632.1 vs 659.3, 8192 x 7168 x 5120 263.3 vs 276.1;
 // the N = 5120 shapes keep 256x320's whole waves (8192 x 5120 x 17408 597.7
-// vs 572.9, 4096 x 5120 x 5120 117.9 vs 101.7).
+// vs 572.9, 4096 x 5120 x 5120 117.9 vs 101.7).  With 2 x 4 waves the
+// 256x320 rate rose in turn and takes those two back (600.4 vs 605.8,
+// 250.2 vs 255.8); 4096 x 7168 x 5120 stays on 256x256 (133.0 vs 158.9).
 struct ModelCfg {
   int cfg;
   double c0, r1, r2;  // us per wave; rate with one / two blocks per CU
@@ -415,7 +422,7 @@ constexpr ModelCfg kModelCfgs[] = {
     {1, 3.0, 4.6, 5.9},     // 128x128 BK 64, 4 stages, two per CU
     {5, 3.0, 3.36, 3.36},   // 64x128, 4 stages
     {3, 6.0, 8.0, 8.0},     // 256x128, 8 waves, 3 stages (no K split): grids of 129-256 tiles
-    {6, 5.0, 9.0, 9.0},     // 256x320, 8 waves (near-ties go to 256x256)
+    {6, 5.0, 9.4, 9.4},     // 256x320, 8 waves 2x4 (near-ties go to 256x256)
 };
 
 double model_us(int64_t M, int64_t N, int64_t K, const ModelCfg& mc) {
@@ -614,7 +621,7 @@ int dispatch_tile(GemmArgs g, void* ws, size_t ws_bytes, hipStream_t st) {
       rc = one_row ? launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, kStreamAux, kLeadSmall>(g, dim3(tiles), st)
                    : launch_tile3<64, 128, 128, 1, 4, 4, EPI, DenseRows, 0, kLeadSmall>(g, dim3(tiles), st);
       break;
-    case 6: rc = launch_tile3<256, 320, 128, 4, 2, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
+    case 6: rc = launch_tile3<256, 320, 128, 2, 4, 2, EPI, DenseRows>(g, dim3(tiles), st); break;
     default: {
       const int64_t cus = device_cus();
       if (EPI == kEpiBf16 && tiles >= cus && stream_fits(g, g.M, g.N))

@@ -77,7 +77,7 @@ def test_version_and_pure_host_helpers(lib):
     finally:
         lib.mw8_set_tuning(-1, -1, -1)
     # automatic: N = 5120 at 4096 rows runs 256x320 tiles, 256 of them (no split)
-    assert lib.mw8_gemm_kernel_name(4096, 5120, 5120) == b"tile3_gemm_kernel<256, 320, 128, 4, 2, 2>"
+    assert lib.mw8_gemm_kernel_name(4096, 5120, 5120) == b"tile3_gemm_kernel<256, 320, 128, 2, 4, 2>"
     assert lib.mw8_gemm_workspace_bytes(4096, 5120, 5120) == 0
     assert lib.mw8_gemm_kernel_name(8192, 34816, 5120) == b"tile3_gemm_kernel<256, 256, 128, 2, 4, 2>"
     assert lib.mw8_gemm_workspace_bytes(8192, 34816, 5120) == 0  # 4352 tiles: whole waves
@@ -370,16 +370,16 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     8 rows), in-block split-K for qkv / o_proj at 64 and 512 rows, the
     shared token ring for gate_up and the 64x128 ring for the deep down at
     64 rows, and above the 256x256 ring (its weight stages a stage ahead)
-    or, where it fills whole waves and 256x256 does not (N = 5120), the
-    256x320 ring."""
+    or, where it fills the last wave of the CUs better (N = 5120, qkv at
+    8192 rows, gate_up at 4096), the 256x320 ring."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
-    sq, wide = t3.format(256, 256, 2, 4, 2), t3.format(256, 320, 4, 2, 2)
+    sq, wide = t3.format(256, 256, 2, 4, 2), t3.format(256, 320, 2, 4, 2)
     ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
     r64 = t3.format(64, 128, 1, 4, 4)
     expect = {
-        (5120, 7168): [ks64, ks512, sq, sq],
+        (5120, 7168): [ks64, ks512, sq, wide],
         (5120, 5120): [ks64, ks512, wide, wide],
-        (5120, 34816): ["decode_sx_gemm_kernel", wide, sq, sq],
+        (5120, 34816): ["decode_sx_gemm_kernel", wide, wide, sq],
         (17408, 5120): [r64, sq, wide, wide],
     }
     for (K, N), names in expect.items():
