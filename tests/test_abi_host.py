@@ -371,7 +371,7 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     shared token ring for gate_up and the 64x128 ring for the deep down at
     64 rows, and above the 256x256 ring (its weight stages a stage ahead)
     or, where it fills the last wave of the CUs better (N = 5120, qkv at
-    8192 rows, gate_up at 4096), the 256x320 ring."""
+    8192 rows), the 256x320 ring."""
     t3 = "tile3_gemm_kernel<{}, {}, 128, {}, {}, {}>"
     sq, wide = t3.format(256, 256, 2, 4, 2), t3.format(256, 320, 2, 4, 2)
     ks64, ks512 = "ksplit_gemm_kernel<64, 32, 8, 1, 1, 2, 3>", "ksplit_gemm_kernel<128, 128, 2, 2, 2, 2, 3>"
@@ -379,7 +379,7 @@ def test_default_tiling_of_the_benchmark_shapes(lib):
     expect = {
         (5120, 7168): [ks64, ks512, sq, wide],
         (5120, 5120): [ks64, ks512, wide, wide],
-        (5120, 34816): ["decode_sx_gemm_kernel", wide, wide, sq],
+        (5120, 34816): ["decode_sx_gemm_kernel", wide, sq, sq],
         (17408, 5120): [r64, sq, wide, wide],
     }
     for (K, N), names in expect.items():
